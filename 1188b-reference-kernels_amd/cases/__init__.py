@@ -1,0 +1,22 @@
+"""Drop-in counterparts of the reference's kernel cases on the MoE dispatch path.
+
+Each module keeps the reference case's entry point -- the bundle's
+`kernel_function(*inputs)` (kernel_results/<case>/kernel.py) or the
+`reference_*` function of a Contract-B case -- with the same arguments, output
+tuple and error behaviour, plus the case's seeded input generator
+(`get_inputs` / `make_inputs` / `make_row_id_map`), and runs the HIP kernels of
+this package.  Generated inputs are returned on `device` (default "cuda").
+"""
+from . import (case03_moe_grouped_gemm_fc1_fwd, case04_moe_grouped_gemm_fc2_fwd,  # noqa: F401
+               case06_cp_seq_chunk_index_select, case12_moe_row_id_map_pass2,
+               case15_moe_unpermute_mask_fwd, case17_moe_permute_with_mask_map,
+               case18_moe_permute_bwd_unpermute_mask, case21_permute_with_mask_map_trans,
+               case22_moe_permute_mask_kernel_true, case23_aten_topk,
+               case24_moe_unpermute_mask_kernel_false, case30_moe_permute_mask_kernel,
+               case32_moe_unpermute_mask_kernel)
+
+ALL = [case03_moe_grouped_gemm_fc1_fwd, case04_moe_grouped_gemm_fc2_fwd, case06_cp_seq_chunk_index_select,
+       case12_moe_row_id_map_pass2, case15_moe_unpermute_mask_fwd, case17_moe_permute_with_mask_map,
+       case18_moe_permute_bwd_unpermute_mask, case21_permute_with_mask_map_trans,
+       case22_moe_permute_mask_kernel_true, case23_aten_topk, case24_moe_unpermute_mask_kernel_false,
+       case30_moe_permute_mask_kernel, case32_moe_unpermute_mask_kernel]

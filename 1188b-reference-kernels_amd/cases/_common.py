@@ -1,0 +1,31 @@
+"""Helpers shared by the case modules."""
+from __future__ import annotations
+
+import torch
+
+from .. import ops
+
+
+def num_out_from_map(row_id_map: torch.Tensor) -> int:
+    """max(row_id_map) + 1 (0 if no entry is >= 0): the reference functions' output row count.
+
+    Reads one scalar back to the host, exactly where the reference does
+    (kernel_cases/case21_ref_permute_with_mask_map_trans.py:64,
+    kernel_results/case17_moe_permute_with_mask_map/binding.cpp:24).
+    """
+    if row_id_map.numel() == 0:
+        return 0
+    return max(int(row_id_map.max().item()) + 1, 0)
+
+
+def expert_major_map(selected_em: torch.Tensor, dtype=torch.int64, device="cuda") -> torch.Tensor:
+    """Expert-major row-id map [E, T] of an expert-major selection, built by the GPU kernel."""
+    mask_tm = selected_em.t().contiguous().to(device)
+    maps = ops.row_id_map(mask_tm, expert_major=dtype == torch.int64, token_major=False,
+                          expert_major_i32=dtype == torch.int32)
+    return maps["expert_major"] if dtype == torch.int64 else maps["expert_major_i32"]
+
+
+def check_scatter_shapes(inp: torch.Tensor, row_id_map: torch.Tensor) -> None:
+    if row_id_map.ndim != 2 or inp.ndim != 2 or row_id_map.shape[1] != inp.shape[0]:
+        raise ValueError(f"shapes inp {tuple(inp.shape)} row_id_map {tuple(row_id_map.shape)}")

@@ -1,0 +1,42 @@
+"""case22 deep_ep moe_permute_mask_kernel<bf16, true> on gfx950 (dispatch with probs).
+
+Drop-in for reference_permute_mask_with_probs
+(kernel_cases/case22_ref_moe_permute_mask_kernel_true.py:47-69):
+(out [num_out,H], permuted_probs [num_out]) with num_out = max(row_id_map)+1;
+the hidden row is copied, not scaled.  make_probs follows :88-103.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import inputs, ops
+from ._common import check_scatter_shapes, expert_major_map, num_out_from_map
+
+M = 16384
+HIDDEN = 8192
+NUM_EXPERTS = 320
+TOPK = 8
+
+
+def permute_mask_with_probs(inp: torch.Tensor, row_id_map: torch.Tensor, probs: torch.Tensor):
+    """Scatter inp[token] and probs[token, expert] to the destination rows."""
+    check_scatter_shapes(inp, row_id_map)
+    experts, tokens = row_id_map.shape
+    if probs.shape != (tokens, experts):
+        raise ValueError(f"probs {tuple(probs.shape)} expected {(tokens, experts)}")
+    num_out = num_out_from_map(row_id_map)
+    if num_out == 0:
+        return inp.new_empty((0, inp.shape[1])), probs.new_empty((0,))
+    return ops.permute(inp, row_id_map, probs, num_out=num_out, layout=ops.EXPERT_MAJOR, zero_tail=True)
+
+
+def make_row_id_map(num_tokens: int = M, num_experts: int = NUM_EXPERTS, topk: int = TOPK, device="cuda"):
+    return expert_major_map(inputs.modular_routing_mask(num_tokens, num_experts, topk), torch.int64, device)
+
+
+def make_probs(row_id_map: torch.Tensor, seed: int = 0, device="cuda") -> torch.Tensor:
+    """fp32 probs on the routed (token, expert) pairs; zeros elsewhere."""
+    return inputs.case22_probs((row_id_map >= 0).cpu(), seed).to(device)
+
+
+kernel_function = permute_mask_with_probs

@@ -1,0 +1,245 @@
+// Permute (token rows -> expert-major rows) with optional permuted probs.
+//
+// Math: kernel_cases/case17_moe_permute_with_mask_map.py:58-71 (token-major
+// int64 map) and the expert-major variants kernel_cases/case21...:52-68,
+// case22...:47-69, case30...:44-58:
+//   out[map(t, e)] = x[t];  permuted_probs[map(t, e)] = probs[t, e]   (map >= 0)
+//
+// Layout of the work: one wavefront per token.  The wave reads the token's
+// map entries 64 experts at a time, turns "entry >= 0" into a 64-bit ballot,
+// loads the x row once into VGPRs as 16-byte vectors (non-temporal), then
+// walks the ballot's set bits in ascending expert order and stores the row to
+// each destination.  The row is read from HBM once and written k times, which
+// is the algorithmic minimum (2TH + 2RH bytes plus the map and probs).
+#include <algorithm>
+
+#include "moe_common.h"
+
+namespace moe {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWavesPerBlock = kThreads / kWave;
+constexpr int kMaxVecPerLane = 16;  // 16 x 16 B per lane -> rows up to 8192 bf16 per pass
+
+struct PermuteArgs {
+  const uint16_t *x;
+  int64_t T, H, E;
+  const void *map;
+  const float *probs;
+  uint16_t *out;
+  float *pp;
+  int64_t num_out;
+  int32_t *block_counts;  // per-block number of map entries >= 0 (zero-tail pass), or null
+};
+
+template <bool kI64, bool kExpertMajor>
+__device__ __forceinline__ int64_t map_at(const PermuteArgs &a, int64_t t, int64_t e) {
+  return load_idx<kI64>(a.map, kExpertMajor ? e * a.T + t : t * a.E + e);
+}
+
+template <bool kI64, bool kExpertMajor, bool kProbs, bool kVec>
+__global__ __launch_bounds__(kThreads) void permute_kernel(PermuteArgs a) {
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave;
+  int routed = 0;
+
+  if (t < a.T) {
+    if constexpr (kVec) {
+      const int64_t nvec = a.H / 8;  // 16-byte vectors per row
+      const u32x4 *src = reinterpret_cast<const u32x4 *>(a.x + t * a.H);
+      for (int64_t seg = 0; seg < nvec || seg == 0; seg += kMaxVecPerLane * kWave) {
+        u32x4 buf[kMaxVecPerLane];
+#pragma unroll
+        for (int j = 0; j < kMaxVecPerLane; ++j) {
+          const int64_t v = seg + j * kWave + lane;
+          if (v < nvec) buf[j] = __builtin_nontemporal_load(src + v);
+        }
+        for (int64_t e0 = 0; e0 < a.E; e0 += kWave) {
+          const int64_t e = e0 + lane;
+          const int64_t dst = e < a.E ? map_at<kI64, kExpertMajor>(a, t, e) : -1;
+          uint64_t mask = __ballot(dst >= 0 && dst < a.num_out);
+          if (seg == 0) {
+            routed += __popcll(__ballot(dst >= 0));
+            if constexpr (kProbs) {
+              if (dst >= 0 && dst < a.num_out && a.pp != nullptr) a.pp[dst] = a.probs[t * a.E + e];
+            }
+          }
+          while (mask) {
+            const int b = __builtin_ctzll(mask);
+            mask &= mask - 1;
+            const int64_t d = readlane64(dst, b);
+            u32x4 *o = reinterpret_cast<u32x4 *>(a.out + d * a.H);
+#pragma unroll
+            for (int j = 0; j < kMaxVecPerLane; ++j) {
+              const int64_t v = seg + j * kWave + lane;
+              if (v < nvec) __builtin_nontemporal_store(buf[j], o + v);
+            }
+          }
+        }
+        if (nvec == 0) break;
+      }
+    } else {
+      // Scalar path for rows that are not a multiple of 16 bytes or misaligned.
+      const uint16_t *src = a.x + t * a.H;
+      for (int64_t e0 = 0; e0 < a.E; e0 += kWave) {
+        const int64_t e = e0 + lane;
+        const int64_t dst = e < a.E ? map_at<kI64, kExpertMajor>(a, t, e) : -1;
+        uint64_t mask = __ballot(dst >= 0 && dst < a.num_out);
+        routed += __popcll(__ballot(dst >= 0));
+        if constexpr (kProbs) {
+          if (dst >= 0 && dst < a.num_out && a.pp != nullptr) a.pp[dst] = a.probs[t * a.E + e];
+        }
+        while (mask) {
+          const int b = __builtin_ctzll(mask);
+          mask &= mask - 1;
+          const int64_t d = readlane64(dst, b);
+          uint16_t *o = a.out + d * a.H;
+          for (int64_t i = lane; i < a.H; i += kWave) o[i] = src[i];
+        }
+      }
+    }
+  }
+
+  if (a.block_counts != nullptr) {
+    __shared__ int wave_routed[kWavesPerBlock];
+    if (lane == 0) wave_routed[wave] = routed;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int s = 0;
+      for (int w = 0; w < kWavesPerBlock; ++w) s += wave_routed[w];
+      a.block_counts[blockIdx.x] = s;
+    }
+  }
+}
+
+// Zero-fills out rows [R, num_out) and pp[R, num_out), R = sum(block_counts).
+template <bool kVec>
+__global__ __launch_bounds__(kThreads) void permute_zero_tail_kernel(const int32_t *block_counts,
+                                                                     int64_t nblocks, uint16_t *out,
+                                                                     float *pp, int64_t H,
+                                                                     int64_t num_out) {
+  __shared__ int64_t partial[kThreads];
+  int64_t s = 0;
+  for (int64_t i = threadIdx.x; i < nblocks; i += kThreads) s += block_counts[i];
+  partial[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = kThreads / 2; w > 0; w >>= 1) {
+    if (threadIdx.x < w) partial[threadIdx.x] += partial[threadIdx.x + w];
+    __syncthreads();
+  }
+  const int64_t R = partial[0];
+  if (R >= num_out) return;
+  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t gstride = static_cast<int64_t>(gridDim.x) * kThreads;
+  if (pp != nullptr) {
+    for (int64_t i = R + gtid; i < num_out; i += gstride) pp[i] = 0.0f;
+  }
+  if constexpr (kVec) {
+    u32x4 *o = reinterpret_cast<u32x4 *>(out + R * H);
+    const int64_t n = (num_out - R) * H / 8;
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    for (int64_t i = gtid; i < n; i += gstride) __builtin_nontemporal_store(z, o + i);
+  } else {
+    uint16_t *o = out + R * H;
+    const int64_t n = (num_out - R) * H;
+    for (int64_t i = gtid; i < n; i += gstride) o[i] = 0;
+  }
+}
+
+template <bool kI64, bool kExpertMajor, bool kProbs>
+void launch_permute_3(const PermuteArgs &a, bool vec, int64_t grid, hipStream_t s) {
+  if (vec) {
+    permute_kernel<kI64, kExpertMajor, kProbs, true><<<dim3(grid), dim3(kThreads), 0, s>>>(a);
+  } else {
+    permute_kernel<kI64, kExpertMajor, kProbs, false><<<dim3(grid), dim3(kThreads), 0, s>>>(a);
+  }
+}
+
+template <bool kI64, bool kExpertMajor>
+void launch_permute_2(const PermuteArgs &a, bool vec, int64_t grid, hipStream_t s) {
+  if (a.probs != nullptr) {
+    launch_permute_3<kI64, kExpertMajor, true>(a, vec, grid, s);
+  } else {
+    launch_permute_3<kI64, kExpertMajor, false>(a, vec, grid, s);
+  }
+}
+
+}  // namespace
+}  // namespace moe
+
+extern "C" {
+
+size_t moe_permute_workspace_size(int64_t T) {
+  if (T < 0) return 0;
+  return static_cast<size_t>(moe::ceil_div(T, moe::kWavesPerBlock)) * sizeof(int32_t) + 256;
+}
+
+int moe_permute(const moe_bf16_t *x, int64_t T, int64_t H, const void *row_id_map, int idx_dtype,
+                int map_layout, int64_t E, const float *probs, moe_bf16_t *out,
+                float *permuted_probs, int64_t num_out, int zero_tail, void *workspace,
+                size_t workspace_bytes, void *stream) {
+  using namespace moe;
+  if (T < 0 || H < 0 || E < 0 || num_out < 0) {
+    return fail(MOE_ERR_SHAPE, "moe_permute: negative size (T=%lld H=%lld E=%lld num_out=%lld)",
+                (long long)T, (long long)H, (long long)E, (long long)num_out);
+  }
+  if (idx_dtype != MOE_IDX_I32 && idx_dtype != MOE_IDX_I64) {
+    return fail(MOE_ERR_INVALID_ARG, "moe_permute: idx_dtype %d is not MOE_IDX_I32/I64", idx_dtype);
+  }
+  if (map_layout != MOE_MAP_TOKEN_MAJOR && map_layout != MOE_MAP_EXPERT_MAJOR) {
+    return fail(MOE_ERR_INVALID_ARG, "moe_permute: map_layout %d is not a moe_map_layout_t", map_layout);
+  }
+  if ((T * H > 0 && x == nullptr) || (T * E > 0 && row_id_map == nullptr) ||
+      (num_out * H > 0 && out == nullptr)) {
+    return fail(MOE_ERR_INVALID_ARG, "moe_permute: null x, row_id_map or out");
+  }
+  if (permuted_probs != nullptr && probs == nullptr && T * E > 0) {
+    return fail(MOE_ERR_INVALID_ARG, "moe_permute: permuted_probs given without probs");
+  }
+  const int64_t nblocks = ceil_div(T, kWavesPerBlock);
+  if (nblocks > 0x7fffffff) return fail(MOE_ERR_CAPACITY, "moe_permute: T=%lld too large", (long long)T);
+  if (zero_tail && (workspace == nullptr || workspace_bytes < moe_permute_workspace_size(T))) {
+    return fail(MOE_ERR_WORKSPACE, "moe_permute: zero_tail needs %zu bytes of workspace, got %zu",
+                moe_permute_workspace_size(T), workspace_bytes);
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  PermuteArgs a;
+  a.x = x;
+  a.T = T;
+  a.H = H;
+  a.E = E;
+  a.map = row_id_map;
+  a.probs = probs;
+  a.out = out;
+  a.pp = probs != nullptr ? permuted_probs : nullptr;
+  a.num_out = num_out;
+  a.block_counts = zero_tail ? static_cast<int32_t *>(workspace) : nullptr;
+  const bool vec = (H % 8 == 0) && is_aligned(x, 16) && is_aligned(out, 16);
+  if (nblocks > 0) {
+    const bool i64 = idx_dtype == MOE_IDX_I64;
+    const bool em = map_layout == MOE_MAP_EXPERT_MAJOR;
+    if (i64 && em) launch_permute_2<true, true>(a, vec, nblocks, s);
+    else if (i64) launch_permute_2<true, false>(a, vec, nblocks, s);
+    else if (em) launch_permute_2<false, true>(a, vec, nblocks, s);
+    else launch_permute_2<false, false>(a, vec, nblocks, s);
+    int st = check_launch("moe_permute");
+    if (st != MOE_OK) return st;
+  }
+  if (zero_tail && num_out > 0) {
+    const int64_t tail_elems = num_out * (H > 0 ? H : 1);
+    const int64_t grid = std::min<int64_t>(1024, std::max<int64_t>(1, ceil_div(tail_elems, kThreads * 8)));
+    if (vec) {
+      permute_zero_tail_kernel<true><<<dim3(grid), dim3(kThreads), 0, s>>>(
+          a.block_counts, nblocks, out, a.pp, H, num_out);
+    } else {
+      permute_zero_tail_kernel<false><<<dim3(grid), dim3(kThreads), 0, s>>>(
+          a.block_counts, nblocks, out, a.pp, H, num_out);
+    }
+    return check_launch("moe_permute(zero tail)");
+  }
+  return MOE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,80 @@
+"""MoE FFN forward layer on one GPU, composed from this package's kernels.
+
+The reference has no entry point for the composed layer; it is the chain of
+its cases: router top-k (case23) -> mask map -> row-id map (case12) ->
+permute (case17) -> grouped GEMM fc1 (case03) + SwiGLU -> grouped GEMM fc2
+(case04) -> unpermute with probability-weighted merge (case15 + merge probs).
+
+Data layout in HBM (T tokens, H hidden, F ffn, E experts, k top-k, R = T*k):
+  x        bf16 [T, H]        token-major activations (input)
+  logits   fp32 [T, E]        router logits (input; the router GEMM is not part of this path)
+  mask     bool [T, E]        1 at the k selected experts
+  probs    fp32 [T, E]        softmax over the k selected logits, 0 elsewhere
+  row_map  int64 [T, E]       token-major destination row, -1 if unselected
+  offsets  int32 [E + 1]      first permuted row of each expert; offsets[E] = R
+  xp       bf16 [R, H]        permuted rows, expert-major (expert e = rows offsets[e]..)
+  h        bf16 [R, F]        silu(xp @ W1_gate^T) * (xp @ W1_up^T)
+  z        bf16 [R, H]        h @ W2^T
+  out      bf16 [T, H]        sum_e probs[t, e] * z[row_map[t, e]]  (fp32, ascending e)
+  W1       bf16 [E, 2F, H]    gate rows [0, F), up rows [F, 2F)  (out x in)
+  W2       bf16 [E, H, F]
+Every buffer is allocated once per shape and reused; no host synchronisation
+happens inside forward() (R = T * k is known on the host).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+
+
+class MoEFFN:
+    """forward(x, logits) -> out for fixed weights W1 [E, 2F, H], W2 [E, H, F]."""
+
+    def __init__(self, w1: torch.Tensor, w2: torch.Tensor, topk: int):
+        if w1.ndim != 3 or w2.ndim != 3:
+            raise ValueError("w1 must be [E, 2F, H] and w2 [E, H, F]")
+        E, F2, H = w1.shape
+        if w2.shape != (E, H, F2 // 2) or F2 % 2:
+            raise ValueError(f"w2 {tuple(w2.shape)} does not match w1 {tuple(w1.shape)}")
+        self.w1, self.w2 = w1, w2
+        self.E, self.H, self.F, self.k = E, H, F2 // 2, topk
+        self._bufs = None
+        self.last = {}
+
+    def _buffers(self, T: int, device) -> dict:
+        if self._bufs is None or self._bufs["T"] != T:
+            R = T * self.k
+            bf = dict(dtype=torch.bfloat16, device=device)
+            self._bufs = {
+                "T": T,
+                "xp": torch.empty(R, self.H, **bf),
+                "h": torch.empty(R, self.F, **bf),
+                "z": torch.empty(R, self.H, **bf),
+                "out": torch.empty(T, self.H, **bf),
+                "ws": torch.empty(ops._lib.lib().moe_row_id_map_workspace_size(T, self.E), dtype=torch.uint8,
+                                  device=device),
+            }
+        return self._bufs
+
+    def route(self, logits: torch.Tensor):
+        """(mask, probs, token-major row map, expert offsets) for router logits [T, E]."""
+        _, _, mask, probs = ops.topk(logits, self.k, with_mask=True, with_probs=True)
+        maps = ops.row_id_map(mask, expert_major=False, token_major=True, expert_offsets=True,
+                              workspace=self._buffers(logits.shape[0], logits.device)["ws"])
+        return mask, probs, maps["token_major"], maps["expert_offsets"]
+
+    def forward(self, x: torch.Tensor, logits: torch.Tensor) -> torch.Tensor:
+        T = x.shape[0]
+        if logits.shape != (T, self.E):
+            raise ValueError(f"logits {tuple(logits.shape)} expected {(T, self.E)}")
+        b = self._buffers(T, x.device)
+        mask, probs, row_map, offsets = self.route(logits)
+        ops.permute(x, row_map, num_out=T * self.k, layout=ops.TOKEN_MAJOR, zero_tail=False, out=b["xp"])
+        ops.grouped_gemm(b["xp"], self.w1, offsets, swiglu=True, out=b["h"])
+        ops.grouped_gemm(b["h"], self.w2, offsets, out=b["z"])
+        ops.unpermute(b["z"], row_map, probs, layout=ops.TOKEN_MAJOR, out=b["out"])
+        self.last = {"mask": mask, "probs": probs, "row_map": row_map, "offsets": offsets}
+        return b["out"]
+
+    __call__ = forward

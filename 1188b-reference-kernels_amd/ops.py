@@ -1,0 +1,269 @@
+"""Tensor-level API over the C ABI: validates, allocates outputs, launches.
+
+Every function runs its HIP kernels on torch's current stream of the input's
+device; torch tensors are only containers (allocation and streams).  There is
+no CPU or eager-torch fallback: inputs must live on the GPU and the native
+library must be built.
+"""
+from __future__ import annotations
+
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib
+from ._lib import (MOE_EPILOGUE_NONE, MOE_EPILOGUE_SWIGLU, MOE_IDX_I32, MOE_IDX_I64,
+                   MOE_MAP_EXPERT_MAJOR, MOE_MAP_TOKEN_MAJOR, call, ptr, stream_handle)
+
+TOKEN_MAJOR = "token_major"    # map [T, E]  (case12 non-trans, case17)
+EXPERT_MAJOR = "expert_major"  # map [E, T]  (case12 trans, case15/18/21/22/24/30/32)
+
+_LAYOUTS = {TOKEN_MAJOR: MOE_MAP_TOKEN_MAJOR, EXPERT_MAJOR: MOE_MAP_EXPERT_MAJOR}
+_IDX = {torch.int32: MOE_IDX_I32, torch.int64: MOE_IDX_I64}
+
+
+def _on_gpu(name: str, t: torch.Tensor) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a GPU tensor (got device {t.device}); there is no CPU path")
+
+
+def _dtype(name: str, t: torch.Tensor, *dtypes: torch.dtype) -> None:
+    if t.dtype not in dtypes:
+        raise TypeError(f"{name} must have dtype {' or '.join(map(str, dtypes))}, got {t.dtype}")
+
+
+def _map_dims(row_id_map: torch.Tensor, layout: str) -> tuple[int, int]:
+    """(tokens, experts) of a 2-D map in the given layout."""
+    if row_id_map.ndim != 2:
+        raise ValueError(f"row_id_map must be 2-D, got shape {tuple(row_id_map.shape)}")
+    if layout not in _LAYOUTS:
+        raise ValueError(f"map layout must be {TOKEN_MAJOR!r} or {EXPERT_MAJOR!r}, got {layout!r}")
+    a, b = row_id_map.shape
+    return (a, b) if layout == TOKEN_MAJOR else (b, a)
+
+
+# --------------------------------------------------------------------- top-k
+def topk(logits: torch.Tensor, k: int, *, with_mask: bool = False, with_probs: bool = False):
+    """Row-wise top-k of fp32 router logits (torch.topk(dim=1, largest, sorted)).
+
+    Returns (values fp32 [T,k], indices int64 [T,k]) and, on request, the
+    routing mask bool [T,E] and the merge probs fp32 [T,E] (softmax over the k
+    selected values, scattered; 0 elsewhere).
+    """
+    _on_gpu("logits", logits)
+    _dtype("logits", logits, torch.float32)
+    if logits.ndim != 2:
+        raise ValueError(f"expected 2D input, got {tuple(logits.shape)}")
+    T, E = logits.shape
+    if not (1 <= k <= E):
+        raise ValueError(f"k={k} out of range for N={E}")
+    x = logits.contiguous()
+    values = torch.empty(T, k, dtype=torch.float32, device=x.device)
+    indices = torch.empty(T, k, dtype=torch.int64, device=x.device)
+    mask = torch.empty(T, E, dtype=torch.bool, device=x.device) if with_mask else None
+    probs = torch.empty(T, E, dtype=torch.float32, device=x.device) if with_probs else None
+    call("moe_topk", ptr(x), T, E, k, ptr(values), ptr(indices),
+         ptr(mask.view(torch.uint8)) if mask is not None else None, ptr(probs), stream_handle())
+    out = [values, indices]
+    if with_mask:
+        out.append(mask)
+    if with_probs:
+        out.append(probs)
+    return tuple(out)
+
+
+# ---------------------------------------------------------------- row-id map
+def row_id_map(routing_map: torch.Tensor, *, expert_major: bool = True, token_major: bool = True,
+               expert_major_i32: bool = False, expert_offsets: bool = False,
+               workspace: Optional[torch.Tensor] = None) -> dict:
+    """Row-id map of a bool/uint8 routing mask [T, E].
+
+    Returns a dict with the requested outputs: "expert_major" int64 [E,T],
+    "token_major" int64 [T,E], "expert_major_i32" int32 [E,T] and
+    "expert_offsets" int32 [E+1] (offsets[e] = first row of expert e,
+    offsets[E] = number of routed rows).
+    """
+    _on_gpu("routing_map", routing_map)
+    _dtype("routing_map", routing_map, torch.bool, torch.uint8)
+    if routing_map.ndim != 2:
+        raise ValueError("routing_map must be [T,E]")
+    T, E = routing_map.shape
+    m = routing_map.contiguous().view(torch.uint8)
+    dev = m.device
+    res = {}
+    if expert_major:
+        res["expert_major"] = torch.empty(E, T, dtype=torch.int64, device=dev)
+    if token_major:
+        res["token_major"] = torch.empty(T, E, dtype=torch.int64, device=dev)
+    if expert_major_i32:
+        res["expert_major_i32"] = torch.empty(E, T, dtype=torch.int32, device=dev)
+    if expert_offsets:
+        res["expert_offsets"] = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    ws_bytes = _lib.lib().moe_row_id_map_workspace_size(T, E)
+    if workspace is None or workspace.numel() * workspace.element_size() < ws_bytes:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    call("moe_row_id_map", ptr(m), T, E, ptr(res.get("expert_major")), ptr(res.get("token_major")),
+         ptr(res.get("expert_major_i32")), ptr(res.get("expert_offsets")), ptr(workspace),
+         workspace.numel() * workspace.element_size(), stream_handle())
+    return res
+
+
+# ------------------------------------------------------------------- permute
+def permute(x: torch.Tensor, row_id_map: torch.Tensor, probs: Optional[torch.Tensor] = None, *,
+            num_out: int, layout: str = TOKEN_MAJOR, zero_tail: bool = True,
+            out: Optional[torch.Tensor] = None, permuted_probs: Optional[torch.Tensor] = None):
+    """out[map(t,e)] = x[t]; permuted_probs[map(t,e)] = probs[t,e] for map >= 0.
+
+    Rows of `out` at index >= R (R = number of entries >= 0) are zero when
+    `zero_tail` (the reference's new_zeros); pass zero_tail=False when num_out
+    is known to equal R.  Returns (out, permuted_probs or None).
+    """
+    _on_gpu("x", x)
+    _on_gpu("row_id_map", row_id_map)
+    _dtype("x", x, torch.bfloat16)
+    _dtype("row_id_map", row_id_map, torch.int32, torch.int64)
+    if x.ndim != 2:
+        raise ValueError(f"x must be [T,H], got {tuple(x.shape)}")
+    T, E = _map_dims(row_id_map, layout)
+    if T != x.shape[0]:
+        raise ValueError(f"shapes inp {tuple(x.shape)} row_id_map {tuple(row_id_map.shape)}")
+    H = x.shape[1]
+    xc, mc = x.contiguous(), row_id_map.contiguous()
+    pc = None
+    if probs is not None:
+        _on_gpu("probs", probs)
+        if tuple(probs.shape) != (T, E):
+            raise ValueError(f"probs {tuple(probs.shape)} expected {(T, E)}")
+        pc = probs.contiguous().to(torch.float32)
+    if out is None:
+        out = torch.empty(num_out, H, dtype=x.dtype, device=x.device)
+    if pc is not None and permuted_probs is None:
+        permuted_probs = torch.empty(num_out, dtype=torch.float32, device=x.device)
+    ws = None
+    ws_bytes = 0
+    if zero_tail:
+        ws_bytes = _lib.lib().moe_permute_workspace_size(T)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    call("moe_permute", ptr(xc), T, H, ptr(mc), _IDX[mc.dtype], _LAYOUTS[layout], E, ptr(pc), ptr(out),
+         ptr(permuted_probs) if pc is not None else None, num_out, int(zero_tail), ptr(ws), ws_bytes,
+         stream_handle())
+    return out, (permuted_probs if pc is not None else None)
+
+
+# ----------------------------------------------------------------- unpermute
+def unpermute(pin: torch.Tensor, row_id_map: torch.Tensor, merge_probs: Optional[torch.Tensor] = None, *,
+              layout: str = EXPERT_MAJOR, out: Optional[torch.Tensor] = None, with_acc: bool = False):
+    """out[t] = bf16(sum_{e asc} [merge_probs[t,e] *] float(pin[map(t,e)])), fp32 accumulate.
+
+    Returns out, or (acc fp32 [T,H], out) with `with_acc`.
+    """
+    _on_gpu("pin", pin)
+    _on_gpu("row_id_map", row_id_map)
+    _dtype("pin", pin, torch.bfloat16)
+    _dtype("row_id_map", row_id_map, torch.int32, torch.int64)
+    if pin.ndim != 2:
+        raise ValueError(f"pin must be [R,H], got {tuple(pin.shape)}")
+    T, E = _map_dims(row_id_map, layout)
+    R, H = pin.shape
+    pc, mc = pin.contiguous(), row_id_map.contiguous()
+    wc = None
+    if merge_probs is not None:
+        _on_gpu("merge_probs", merge_probs)
+        if tuple(merge_probs.shape) != (T, E):
+            raise ValueError(f"merge_probs {tuple(merge_probs.shape)} expected {(T, E)}")
+        wc = merge_probs.contiguous().to(torch.float32)
+    if out is None:
+        out = torch.empty(T, H, dtype=pin.dtype, device=pin.device)
+    acc = torch.empty(T, H, dtype=torch.float32, device=pin.device) if with_acc else None
+    call("moe_unpermute", ptr(pc), R, H, ptr(mc), _IDX[mc.dtype], _LAYOUTS[layout], E, T, ptr(wc), ptr(out),
+         ptr(acc), stream_handle())
+    return (acc, out) if with_acc else out
+
+
+def permute_bwd(dperm_act: torch.Tensor, dpp: torch.Tensor, row_id_map: torch.Tensor, *,
+                layout: str = EXPERT_MAJOR, with_acc: bool = False):
+    """(dact [T,H] bf16, dprobs [T,E] fp32) of the permute backward (case18 math).
+
+    With `with_acc`: (acc fp32 [T,H], dact, dprobs).
+    """
+    _on_gpu("dperm_act", dperm_act)
+    _on_gpu("dpp", dpp)
+    _on_gpu("row_id_map", row_id_map)
+    _dtype("dperm_act", dperm_act, torch.bfloat16)
+    _dtype("dpp", dpp, torch.float32)
+    _dtype("row_id_map", row_id_map, torch.int32, torch.int64)
+    if dperm_act.ndim != 2:
+        raise ValueError(f"dperm_act must be [R,H], got {tuple(dperm_act.shape)}")
+    T, E = _map_dims(row_id_map, layout)
+    R, H = dperm_act.shape
+    if dpp.ndim != 1 or dpp.shape[0] != R:
+        raise ValueError(f"dpp {tuple(dpp.shape)} does not match dperm_act {tuple(dperm_act.shape)}")
+    ac, pc, mc = dperm_act.contiguous(), dpp.contiguous(), row_id_map.contiguous()
+    dact = torch.empty(T, H, dtype=dperm_act.dtype, device=dperm_act.device)
+    dprobs = torch.empty(T, E, dtype=torch.float32, device=dperm_act.device)
+    acc = torch.empty(T, H, dtype=torch.float32, device=dperm_act.device) if with_acc else None
+    call("moe_permute_bwd", ptr(ac), R, H, ptr(pc), ptr(mc), _IDX[mc.dtype], _LAYOUTS[layout], E, T,
+         ptr(dact), ptr(dprobs), ptr(acc), stream_handle())
+    return (acc, dact, dprobs) if with_acc else (dact, dprobs)
+
+
+# -------------------------------------------------------------- index_select
+def index_select(src: torch.Tensor, index: torch.Tensor) -> torch.Tensor:
+    """torch.index_select(src, 0, index) for bf16 src and int32/int64 index."""
+    _on_gpu("src", src)
+    _on_gpu("index", index)
+    _dtype("src", src, torch.bfloat16)
+    _dtype("index", index, torch.int32, torch.int64)
+    if src.ndim < 1:
+        raise ValueError("src must have at least one dimension")
+    if index.ndim != 1:
+        raise ValueError("index must be one-dimensional")
+    sc, ic = src.contiguous(), index.contiguous()
+    row = 1
+    for d in sc.shape[1:]:
+        row *= d
+    out = torch.empty((ic.shape[0], *sc.shape[1:]), dtype=sc.dtype, device=sc.device)
+    call("moe_index_select", ptr(sc), sc.shape[0], row, ptr(ic), _IDX[ic.dtype], ic.shape[0], ptr(out),
+         stream_handle())
+    return out
+
+
+# -------------------------------------------------------------- grouped GEMM
+def group_offsets_from_splits(m_splits: Sequence[int], device) -> torch.Tensor:
+    """int32 [G+1] exclusive prefix of host m_splits, on `device`."""
+    offs = [0]
+    for m in m_splits:
+        if m < 0:
+            raise ValueError(f"negative group size {m}")
+        offs.append(offs[-1] + int(m))
+    return torch.tensor(offs, dtype=torch.int32).to(device, non_blocking=True)
+
+
+def grouped_gemm(a: torch.Tensor, w: torch.Tensor, group_offsets: torch.Tensor, *, swiglu: bool = False,
+                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out[rows of g] = a[rows of g] @ w[g]^T (bf16 in, fp32 accumulate, bf16 out).
+
+    a bf16 [M, K]; w bf16 [G, N, K]; group_offsets int32 [G+1] on the device.
+    With swiglu, out[:, j] = silu(y[:, j]) * y[:, N/2 + j] and out is [M, N/2].
+    """
+    _on_gpu("a", a)
+    _on_gpu("w", w)
+    _on_gpu("group_offsets", group_offsets)
+    _dtype("a", a, torch.bfloat16)
+    _dtype("w", w, torch.bfloat16)
+    _dtype("group_offsets", group_offsets, torch.int32)
+    if a.ndim != 2 or w.ndim != 3 or a.shape[1] != w.shape[2]:
+        raise ValueError(f"shapes a {tuple(a.shape)} w {tuple(w.shape)}: need a [M,K], w [G,N,K]")
+    G, N, K = w.shape
+    if group_offsets.shape != (G + 1,):
+        raise ValueError(f"group_offsets {tuple(group_offsets.shape)} expected ({G + 1},)")
+    M = a.shape[0]
+    ac, wc, oc = a.contiguous(), w.contiguous(), group_offsets.contiguous()
+    ncols = N // 2 if swiglu else N
+    if out is None:
+        out = torch.empty(M, ncols, dtype=torch.bfloat16, device=a.device)
+    call("moe_grouped_gemm", ptr(ac), M, K, ptr(wc), G, N, ptr(oc),
+         MOE_EPILOGUE_SWIGLU if swiglu else MOE_EPILOGUE_NONE, ptr(out), None, 0, stream_handle())
+    return out

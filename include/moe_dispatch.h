@@ -1,0 +1,197 @@
+/*
+ * moe_dispatch.h -- C ABI of the MI355X (gfx950) MoE expert-dispatch library
+ * (libmoe_dispatch.so).
+ *
+ * Every entry point:
+ *   - takes device pointers, int64_t sizes and enum selectors, plus a
+ *     hipStream_t passed as `void *stream` (NULL = the null stream);
+ *   - validates its arguments on the host before any HIP call and returns a
+ *     non-zero moe_status_t on failure (the message is available from
+ *     moe_last_error(), thread-local);
+ *   - never allocates device memory and never synchronises the host: scratch
+ *     memory comes from the caller through (workspace, workspace_bytes), sized
+ *     by the matching *_workspace_size() query;
+ *   - enqueues its kernels on `stream` and returns MOE_ERR_LAUNCH if the launch
+ *     itself fails.
+ *
+ * Device-side index safety: a map entry or index that points outside the
+ * destination/source buffer is skipped (never dereferenced); kernels do not
+ * fault on bad indices.  Callers that need the reference's IndexError /
+ * ValueError on such inputs validate them first (the Python layer does).
+ *
+ * Types: bf16 tensors are raw bit patterns (moe_bf16_t); routing masks are one
+ * byte per element (torch.bool / uint8, non-zero = selected); fp32 is float.
+ * All tensors are dense row-major (C-contiguous).
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   case12 kernel_results/case12_moe_row_id_map_pass2/binding.cpp:11-34
+ *   case17 kernel_results/case17_moe_permute_with_mask_map/binding.cpp:8-32
+ *   case15 kernel_results/case15_moe_unpermute_mask_fwd/binding.cpp:10-20
+ *   case23 kernel_results/case23_aten_topk/binding.cpp:6-24
+ *   case06 kernel_results/case06_cp_seq_chunk_index_select/binding.cpp:13-49
+ *   case18 kernel_cases/case18_moe_permute_bwd_unpermute_mask.py:68-78 (no bundle)
+ *   case03/case04 kernel_cases/case03_moe_grouped_gemm_fc1_fwd.py:57-64,
+ *                 kernel_cases/case04_moe_grouped_gemm_fc2_fwd.py:57-64 (no bundle)
+ */
+#ifndef MOE_DISPATCH_H_
+#define MOE_DISPATCH_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOE_DISPATCH_ABI_VERSION 1
+
+typedef uint16_t moe_bf16_t;
+
+typedef enum {
+  MOE_OK = 0,
+  MOE_ERR_INVALID_ARG = 1, /* null pointer where one is required, bad enum  */
+  MOE_ERR_SHAPE = 2,       /* negative or inconsistent sizes                */
+  MOE_ERR_ALIGN = 3,       /* pointer alignment the kernel requires         */
+  MOE_ERR_CAPACITY = 4,    /* size beyond what this build supports (e.g. k) */
+  MOE_ERR_WORKSPACE = 5,   /* workspace missing or too small                */
+  MOE_ERR_LAUNCH = 6,      /* hipGetLastError() after the launch            */
+} moe_status_t;
+
+/* Index dtype of a row-id map or index vector. */
+typedef enum { MOE_IDX_I32 = 0, MOE_IDX_I64 = 1 } moe_idx_dtype_t;
+
+/* Layout of a row-id map.
+ *   MOE_MAP_TOKEN_MAJOR  : map[t * E + e]  ([T, E], "non-trans", case12/case17)
+ *   MOE_MAP_EXPERT_MAJOR : map[e * T + t]  ([E, T], "trans", case15/18/21/22/24/30/32) */
+typedef enum { MOE_MAP_TOKEN_MAJOR = 0, MOE_MAP_EXPERT_MAJOR = 1 } moe_map_layout_t;
+
+/* Epilogue of the grouped GEMM. */
+typedef enum {
+  MOE_EPILOGUE_NONE = 0,   /* out[m, n] = bf16(acc[m, n]), out is [M, N]                     */
+  MOE_EPILOGUE_SWIGLU = 1, /* out[m, j] = bf16(silu(acc[m, j]) * acc[m, F + j]), F = N / 2    */
+} moe_epilogue_t;
+
+/* ---- library ---------------------------------------------------------- */
+int moe_abi_version(void);
+const char *moe_status_string(int status);
+/* Message of the last non-zero status returned on the calling thread. */
+const char *moe_last_error(void);
+
+/* ---- a1/a2: router top-k + mask map + merge probs ----------------------
+ * Replaces case23 kernel_function(input, k, dim=1, largest=True, sorted=True)
+ * (kernel_results/case23_aten_topk/kernel.py:14-25, binding.cpp:6-24), whose
+ * contract is torch.topk == first k of a stable descending sort
+ * (kernel_cases/case23_ref_aten_topk.py:47-62).
+ *   logits  fp32 [T, E]
+ *   values  fp32 [T, k]   descending; ties -> smaller index first; NaN largest
+ *   indices int64 [T, k]
+ *   routing_map (nullable) uint8 [T, E]: 1 at the k selected experts, else 0
+ *               (zeros(T,E,bool).scatter_(1, idx, True), case18...py:86-88)
+ *   probs (nullable) fp32 [T, E]: softmax over the k selected values, scattered
+ *               to the selected experts, 0 elsewhere (merge probs; no reference
+ *               function -- closed form torch.softmax(values, -1)).
+ * Limits: 1 <= k <= min(E, 64), E <= 1024. */
+int moe_topk(const float *logits, int64_t T, int64_t E, int64_t k, float *values,
+             int64_t *indices, uint8_t *routing_map, float *probs, void *stream);
+
+/* ---- a3: row-id map ---------------------------------------------------
+ * Replaces case12 kernel_function(routing_map) -> (row_id_map [E,T] int64,
+ * row_id_map_non_trans [T,E] int64)
+ * (kernel_results/case12_moe_row_id_map_pass2/kernel.py:4-6, binding.cpp:11-34;
+ *  math kernel_cases/case12_moe_row_id_map_pass2.py:43-61):
+ *   row[t, e] = offset[e] + #{t' < t : mask[t', e]}  if mask[t, e] else -1,
+ *   offset[e] = sum_{e' < e} count[e'].
+ * Every output is optional (nullable):
+ *   row_expert_major     int64 [E, T]
+ *   row_token_major      int64 [T, E]
+ *   row_expert_major_i32 int32 [E, T]   (deep_ep dtype, case24...py:71-84)
+ *   expert_offsets       int32 [E + 1]  offset[e]; [E] = R = total routed rows
+ * Workspace: moe_row_id_map_workspace_size(T, E) bytes.  E <= 4096. */
+size_t moe_row_id_map_workspace_size(int64_t T, int64_t E);
+int moe_row_id_map(const uint8_t *routing_map, int64_t T, int64_t E, int64_t *row_expert_major,
+                   int64_t *row_token_major, int32_t *row_expert_major_i32,
+                   int32_t *expert_offsets, void *workspace, size_t workspace_bytes,
+                   void *stream);
+
+/* ---- a4/a5: permute -----------------------------------------------------
+ * Replaces case17 kernel_function(x, row_id_map, probs) -> (out, permuted_probs)
+ * (kernel_results/case17_moe_permute_with_mask_map/binding.cpp:8-32; math
+ * kernel_cases/case17_moe_permute_with_mask_map.py:58-71) and the expert-major
+ * variants case21 (:52-68), case22 (:47-69), case30 (:44-58):
+ *   out[map(t, e)] = x[t]; permuted_probs[map(t, e)] = probs[t, e]  for map >= 0.
+ *   x     bf16 [T, H];  map [T, E] or [E, T] (layout), int32 or int64
+ *   probs fp32 [T, E] (nullable; then permuted_probs must be NULL too)
+ *   out   bf16 [num_out, H]; permuted_probs fp32 [num_out] (nullable)
+ * zero_tail != 0: rows of out / permuted_probs at index >= R (R = number of
+ *   map entries >= 0) are zero-filled, matching the reference's new_zeros
+ *   when num_out exceeds R.  Needs moe_permute_workspace_size(T) bytes of
+ *   workspace; with zero_tail == 0 the workspace may be NULL and num_out is
+ *   expected to equal R (the usual case: R = T * topk).
+ * Map entries >= num_out are skipped. */
+size_t moe_permute_workspace_size(int64_t T);
+int moe_permute(const moe_bf16_t *x, int64_t T, int64_t H, const void *row_id_map, int idx_dtype,
+                int map_layout, int64_t E, const float *probs, moe_bf16_t *out,
+                float *permuted_probs, int64_t num_out, int zero_tail, void *workspace,
+                size_t workspace_bytes, void *stream);
+
+/* ---- a8: unpermute (combine), optional probability-weighted merge ------
+ * Replaces case15 kernel_function(pin, row_id_map) -> out
+ * (kernel_results/case15_moe_unpermute_mask_fwd/binding.cpp:10-20; math
+ * kernel_cases/case15_moe_unpermute_mask_fwd.py:58-64, int32 variant
+ * kernel_cases/case24_ref_moe_unpermute_mask_kernel_false.py:45-68):
+ *   out[t] = bf16_rne( sum over e ascending, map(t,e) >= 0, of
+ *                      [merge_probs[t, e] *] float(pin[map(t, e)]) )
+ * fp32 accumulation starts at 0.0f, adds in ascending expert order, and the
+ * weighted form multiplies then adds (no fused multiply-add).
+ *   pin bf16 [R, H]; merge_probs fp32 [T, E] (nullable); out bf16 [T, H];
+ *   out_acc (nullable) fp32 [T, H]: the fp32 sums before rounding (the int32
+ *   reference reference_unpermute_mask returns them, case24...py:66-68).
+ * Map entries >= R are skipped. */
+int moe_unpermute(const moe_bf16_t *pin, int64_t R, int64_t H, const void *row_id_map,
+                  int idx_dtype, int map_layout, int64_t E, int64_t T, const float *merge_probs,
+                  moe_bf16_t *out, float *out_acc, void *stream);
+
+/* ---- a9: permute backward ----------------------------------------------
+ * Replaces case18 Model.forward(dperm_act, dpp, row_id_map) -> (dact, dprobs)
+ * (kernel_cases/case18_moe_permute_bwd_unpermute_mask.py:68-78; int32 variant
+ * kernel_cases/case32_ref_moe_unpermute_mask_kernel.py:46-76):
+ *   dact[t]      = bf16_rne( sum_e ascending float(dperm_act[map(t, e)]) )
+ *   dprobs[t, e] = dpp[map(t, e)] if map(t, e) >= 0 else 0
+ *   dperm_act bf16 [R, H]; dpp fp32 [R]; dact bf16 [T, H]; dprobs fp32 [T, E];
+ *   out_acc (nullable) fp32 [T, H]: the fp32 sums (case32...py:74-76 returns them). */
+int moe_permute_bwd(const moe_bf16_t *dperm_act, int64_t R, int64_t H, const float *dpp,
+                    const void *row_id_map, int idx_dtype, int map_layout, int64_t E, int64_t T,
+                    moe_bf16_t *dact, float *dprobs, float *out_acc, void *stream);
+
+/* ---- a10: row gather ------------------------------------------------------
+ * Replaces case06 index_select_bf16(x, index)
+ * (kernel_results/case06_cp_seq_chunk_index_select/binding.cpp:13-49; math
+ * kernel_cases/case06_cp_seq_chunk_index_select.py:38-40):
+ *   out[i, :] = src[index[i], :]  for i < n_index; row = row_elems bf16.
+ * An index outside [0, src_rows) zero-fills its output row. */
+int moe_index_select(const moe_bf16_t *src, int64_t src_rows, int64_t row_elems,
+                     const void *index, int idx_dtype, int64_t n_index, moe_bf16_t *out,
+                     void *stream);
+
+/* ---- a6/a7: grouped GEMM forward -----------------------------------------
+ * Replaces case03/case04 Model.forward(x, w) = cat_g( x[seg_g] @ w[g].T )
+ * (kernel_cases/case03_moe_grouped_gemm_fc1_fwd.py:57-64,
+ *  kernel_cases/case04_moe_grouped_gemm_fc2_fwd.py:57-64), "bf16 in / fp32
+ * accumulate / bf16 out" (case03...py:37), plus the fused SwiGLU epilogue.
+ *   a   bf16 [M_total, K] (rows of group g are group_offsets[g] .. [g+1]-1)
+ *   w   bf16 [G, N, K]     (out x in, "NT": out = a @ w[g]^T)
+ *   group_offsets int32 [G + 1] on the device, non-decreasing, [0] = 0,
+ *                 [G] <= M_total (rows beyond [G] are not written)
+ *   out bf16 [M_total, N] (MOE_EPILOGUE_NONE) or [M_total, N / 2] (SWIGLU:
+ *       gate = columns [0, N/2), up = [N/2, N); silu(g) = g / (1 + exp(-g)),
+ *       computed in fp32 on the fp32 accumulators, then one bf16 rounding).
+ * Limits: K % 8 == 0, N % 2 == 0 (SWIGLU: (N/2) % 8 == 0), 1 <= G <= 4096.
+ * Workspace: none (pass NULL, 0). */
+int moe_grouped_gemm(const moe_bf16_t *a, int64_t M_total, int64_t K, const moe_bf16_t *w,
+                     int64_t G, int64_t N, const int32_t *group_offsets, int epilogue,
+                     moe_bf16_t *out, void *workspace, size_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MOE_DISPATCH_H_ */

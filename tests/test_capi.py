@@ -1,0 +1,116 @@
+"""CPU checks of the C ABI library: it loads, exports every declared symbol, and
+rejects bad arguments before any HIP call (no GPU needed)."""
+from __future__ import annotations
+
+import ctypes
+import re
+
+import pytest
+import torch
+
+from conftest import load_pkg
+
+pkg = load_pkg()
+L = pkg._lib
+
+
+def test_library_loads_and_exports_header_symbols():
+    lib = L.lib()
+    declared = L.header_functions()
+    assert len(declared) == len(L.SIGNATURES) == 12
+    assert set(declared) == set(L.SIGNATURES)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.moe_abi_version() == L.ABI_VERSION
+
+
+def test_header_enums_match_python_mirror():
+    text = L.HEADER_PATH.read_text()
+    for name in ["MOE_OK", "MOE_ERR_INVALID_ARG", "MOE_ERR_SHAPE", "MOE_ERR_ALIGN", "MOE_ERR_CAPACITY",
+                 "MOE_ERR_WORKSPACE", "MOE_ERR_LAUNCH", "MOE_IDX_I32", "MOE_IDX_I64", "MOE_MAP_TOKEN_MAJOR",
+                 "MOE_MAP_EXPERT_MAJOR", "MOE_EPILOGUE_NONE", "MOE_EPILOGUE_SWIGLU"]:
+        m = re.search(rf"\b{name}\s*=\s*(\d+)", text)
+        assert m and int(m.group(1)) == getattr(L, name), name
+
+
+def _status(name, *args):
+    lib = L.lib()
+    st = getattr(lib, name)(*args)
+    return st, lib.moe_last_error().decode()
+
+
+FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+
+
+@pytest.mark.parametrize("name,args,code,needle", [
+    ("moe_permute", (None, -1, 8, None, 1, 0, 4, None, None, None, 0, 0, None, 0, None), L.MOE_ERR_SHAPE, "negative"),
+    ("moe_permute", (FAKE, 4, 8, FAKE, 7, 0, 4, None, FAKE, None, 16, 0, None, 0, None), L.MOE_ERR_INVALID_ARG, "idx_dtype"),
+    ("moe_permute", (FAKE, 4, 8, FAKE, 1, 3, 4, None, FAKE, None, 16, 0, None, 0, None), L.MOE_ERR_INVALID_ARG, "map_layout"),
+    ("moe_permute", (None, 4, 8, FAKE, 1, 0, 4, None, FAKE, None, 16, 0, None, 0, None), L.MOE_ERR_INVALID_ARG, "null"),
+    ("moe_permute", (FAKE, 4, 8, FAKE, 1, 0, 4, None, FAKE, FAKE, 16, 0, None, 0, None), L.MOE_ERR_INVALID_ARG, "without probs"),
+    ("moe_permute", (FAKE, 4, 8, FAKE, 1, 0, 4, None, FAKE, None, 16, 1, None, 0, None), L.MOE_ERR_WORKSPACE, "workspace"),
+    ("moe_unpermute", (FAKE, 8, 8, FAKE, 1, 1, 2000, 4, None, FAKE, None, None), L.MOE_ERR_CAPACITY, "1024"),
+    ("moe_unpermute", (FAKE, 8, -8, FAKE, 1, 1, 4, 4, None, FAKE, None, None), L.MOE_ERR_SHAPE, "negative"),
+    ("moe_permute_bwd", (FAKE, 8, 8, None, FAKE, 1, 1, 4, 4, FAKE, FAKE, None, None), L.MOE_ERR_INVALID_ARG, "dpp"),
+    ("moe_row_id_map", (FAKE, 16, 8000, None, None, None, None, None, 0, None), L.MOE_ERR_CAPACITY, "4096"),
+    ("moe_row_id_map", (FAKE, 16, 8, None, None, None, None, None, 0, None), L.MOE_ERR_WORKSPACE, "workspace"),
+    ("moe_row_id_map", (None, 16, 8, None, None, None, None, FAKE, 1 << 20, None), L.MOE_ERR_INVALID_ARG, "null"),
+    ("moe_topk", (FAKE, 4, 16, 0, FAKE, FAKE, None, None, None), L.MOE_ERR_SHAPE, "out of range"),
+    ("moe_topk", (FAKE, 4, 16, 17, FAKE, FAKE, None, None, None), L.MOE_ERR_SHAPE, "out of range"),
+    ("moe_topk", (FAKE, 4, 2048, 8, FAKE, FAKE, None, None, None), L.MOE_ERR_CAPACITY, "1024"),
+    ("moe_topk", (FAKE, 4, 128, 65, FAKE, FAKE, None, None, None), L.MOE_ERR_CAPACITY, "64"),
+    ("moe_index_select", (FAKE, 4, 8, FAKE, 5, 2, FAKE, None), L.MOE_ERR_INVALID_ARG, "idx_dtype"),
+    ("moe_index_select", (FAKE, 4, 8, None, 0, 2, FAKE, None), L.MOE_ERR_INVALID_ARG, "null"),
+    ("moe_grouped_gemm", (FAKE, 4, 12, FAKE, 1, 8, FAKE, 0, FAKE, None, 0, None), L.MOE_ERR_SHAPE, "multiple of 8"),
+    ("moe_grouped_gemm", (FAKE, 4, 16, FAKE, 0, 8, FAKE, 0, FAKE, None, 0, None), L.MOE_ERR_CAPACITY, "G=0"),
+    ("moe_grouped_gemm", (FAKE, 4, 16, FAKE, 1, 7, FAKE, 1, FAKE, None, 0, None), L.MOE_ERR_SHAPE, "even N"),
+    ("moe_grouped_gemm", (FAKE, 4, 16, FAKE, 1, 8, FAKE, 9, FAKE, None, 0, None), L.MOE_ERR_INVALID_ARG, "epilogue"),
+    ("moe_grouped_gemm", (FAKE, 4, 16, FAKE, 1, 8, None, 0, FAKE, None, 0, None), L.MOE_ERR_INVALID_ARG, "group_offsets"),
+    ("moe_grouped_gemm", (ctypes.c_void_p(0x1002), 4, 16, FAKE, 1, 8, FAKE, 0, FAKE, None, 0, None), L.MOE_ERR_ALIGN, "aligned"),
+])
+def test_argument_validation(name, args, code, needle):
+    st, msg = _status(name, *args)
+    assert st == code, (st, msg)
+    assert needle in msg, msg
+
+
+def test_empty_problems_are_no_ops():
+    # Nothing to do -> MOE_OK without touching the device.
+    assert _status("moe_permute", None, 0, 8, None, 1, 0, 4, None, None, None, 0, 0, None, 0, None)[0] == 0
+    assert _status("moe_unpermute", None, 0, 8, None, 1, 1, 4, 0, None, None, None, None)[0] == 0
+    assert _status("moe_topk", None, 0, 16, 4, None, None, None, None, None)[0] == 0
+    assert _status("moe_index_select", None, 0, 8, None, 1, 0, None, None)[0] == 0
+    assert _status("moe_grouped_gemm", None, 0, 16, None, 1, 8, FAKE, 0, None, None, 0, None)[0] == 0
+
+
+def test_workspace_sizes():
+    lib = L.lib()
+    assert lib.moe_row_id_map_workspace_size(16384, 64) >= 256 * 64 * 4
+    assert lib.moe_permute_workspace_size(16384) >= 4096 * 4
+    assert lib.moe_row_id_map_workspace_size(-1, 4) == 0
+
+
+def test_status_strings():
+    lib = L.lib()
+    for code in range(7):
+        assert lib.moe_status_string(code)
+    assert lib.moe_status_string(99) == b"unknown status"
+
+
+def test_ops_reject_cpu_tensors():
+    # There is no CPU path: host tensors are refused before any launch.
+    with pytest.raises(ValueError, match="GPU"):
+        pkg.ops.permute(torch.zeros(2, 8, dtype=torch.bfloat16), torch.zeros(2, 2, dtype=torch.int64), num_out=4)
+    with pytest.raises(ValueError, match="GPU"):
+        pkg.ops.topk(torch.zeros(2, 8), 2)
+    with pytest.raises(ValueError, match="GPU"):
+        pkg.ops.grouped_gemm(torch.zeros(2, 8, dtype=torch.bfloat16), torch.zeros(1, 8, 8, dtype=torch.bfloat16),
+                             torch.zeros(2, dtype=torch.int32))
+
+
+def test_inputs_generators_cpu():
+    sizes = pkg.inputs.zipf_group_sizes(32768, 16)
+    assert sum(sizes) == 32768 and sizes[-1] == 0 and sizes[0] == max(sizes)
+    assert pkg.inputs.uniform_group_sizes(4096, 40)[:2] == [103, 103] and sum(pkg.inputs.uniform_group_sizes(4096, 40)) == 4096
+    rm, sel = pkg.inputs.reference_routing_mask(64, 16)
+    assert rm.sum(1).tolist() == [6 if t % 4 == 1 else 5 for t in range(64)]
