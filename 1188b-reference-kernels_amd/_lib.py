@@ -15,7 +15,8 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the HIP library is loaded)
 
 PKG_DIR = Path(__file__).resolve().parent
-LIB_PATH = PKG_DIR / "libmoe_dispatch.so"
+# MOE_DISPATCH_LIB may name another build of the same library (e.g. a tuning variant).
+LIB_PATH = Path(os.environ.get("MOE_DISPATCH_LIB", PKG_DIR / "libmoe_dispatch.so"))
 HEADER_PATH = PKG_DIR.parent / "include" / "moe_dispatch.h"
 
 # Mirrors of the header's enums.

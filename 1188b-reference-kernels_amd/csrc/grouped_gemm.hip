@@ -9,37 +9,60 @@
 // fp32 accumulators, F = N / 2, rounded once to bf16.
 //
 // Kernel shape (gfx950):
-//   * one persistent workgroup per CU, 512 threads = 8 wavefronts;
-//   * output tile 256 x 256, K step 64, A and B tiles double-buffered in LDS
-//     (2 stages x 2 operands x 256 rows x 144 bytes = 144 KiB of the 160 KiB);
-//     the 16-byte row padding makes the MFMA operand reads conflict-free;
-//   * waves form a 2 (M) x 4 (N) grid, each owns 128 x 64 of the tile as
-//     4 x 2 blocks of v_mfma_f32_32x32x16_bf16 (128 fp32 accumulators/lane);
-//   * SwiGLU tiles load 128 gate rows and the matching 128 up rows of w, and
-//     each wave's two N blocks are the gate and up halves of the same 32
+//   * one persistent workgroup per CU; output tile 256 x 256, K step 64;
+//   * A and B tiles stream through a two-stage LDS ring (2 x 2 x 256 x 64
+//     bf16 = 128 KiB) filled by global_load_lds_dwordx4 (memory -> LDS without
+//     VGPRs), one K step ahead of the MFMAs;
+//   * LDS rows are XOR-swizzled in 16-byte chunks (chunk ^ (row / 2) % 8), which
+//     makes both the DMA writes (lane-linear 1 KiB blocks) and the MFMA operand
+//     reads (16 lanes x 16 B) bank-conflict-free;
+//   * kWavesM x kWavesN wavefronts, each owning a 128 x (256 / kWavesN) part of
+//     the tile as kMI x kNI blocks of v_mfma_f32_32x32x16_bf16; within a K step
+//     the operand fragments of 16-wide sub-step s+1 are read from LDS between
+//     the MFMAs of sub-step s (instruction-group scheduling);
+//   * SwiGLU tiles load 128 gate rows and the matching 128 up rows of w; each
+//     wave's N blocks are gate blocks followed by the up blocks of the same
 //     output columns, so the epilogue combines them in registers;
+//   * the epilogue rounds to bf16 into an LDS tile and writes 16-byte
+//     row-contiguous non-temporal stores;
 //   * tiles are numbered expert by expert, and inside an expert in groups of
 //     4 row tiles x all column tiles (row tile fastest), so 32 consecutive
 //     tile numbers form a 4 x 8 patch that shares A and B panels; workgroup b
 //     takes tile round * P + (b % 8) * (P / 8) + b / 8, which hands each XCD
 //     (workgroups are dealt round-robin to the 8 XCDs) one such patch per
 //     round, so the panels are reused from that XCD's L2.
+// Rows past a group's end and columns past N are loaded from a clamped (valid)
+// address and their results are discarded; a K tail (K % 64 != 0) is zeroed in
+// LDS before use.
 #include <algorithm>
 
 #include "moe_common.h"
+
+#ifndef MOE_GEMM_WAVES_N
+#define MOE_GEMM_WAVES_N 4
+#endif
 
 namespace moe {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) char lds_char;
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) uint16_t lds_u16;
+typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
 
 constexpr int kBM = 256, kBN = 256, kBK = 64;
-constexpr int kThreads = 512;
-constexpr int kLdsRow = kBK + 8;  // bf16 per LDS row (144 bytes)
-constexpr int kMI = 4, kNI = 2;   // 32x32 blocks per wave (M, N)
-constexpr int kGroupM = 4;        // row tiles per tile-order group
-constexpr int kVecPerThread = (kBM * kBK / 8) / kThreads;  // 16-byte vectors per operand per thread (4)
+constexpr int kWavesM = 2;
+constexpr int kGroupM = 4;                        // row tiles per tile-order group
+constexpr int kRowBytes = kBK * 2;                // 128: one tile row in LDS
+constexpr int kChunks = kBK / 8;                  // 8 chunks of 16 bytes per row
+constexpr int kOperandBytes = 256 * kRowBytes;    // 32 KiB: one 256-row operand tile
+constexpr int kStageBytes = 2 * kOperandBytes;    // A + B
+constexpr int kStages = 2;
+constexpr int kRowsPerKiB = 1024 / kRowBytes;     // 8 rows per DMA instruction
+constexpr int kSubSteps = kBK / 16;               // MFMA K sub-steps per K step
 
 struct GemmArgs {
   const uint16_t *a;
@@ -49,60 +72,128 @@ struct GemmArgs {
   int64_t M, K, N, G;
   int64_t ncols;   // output columns: N (NONE) or N / 2 (SWIGLU)
   int64_t ntiles;  // column tiles per expert
+  int vec_out;     // output rows are 16-byte aligned (ncols % 8 == 0, aligned base)
 };
 
-// Row of w[g] (in [0, N)) that B-tile row r of column tile nt reads.
-template <bool kSwiglu>
-__device__ __forceinline__ int64_t b_row(int64_t nt, int r, int64_t ncols) {
-  if constexpr (kSwiglu) {
-    // rows 0..127: gate columns j0 .. j0+127; rows 128..255: up columns F + j0 ..
-    const int64_t j = nt * (kBN / 2) + (r & 127);
-    return r < 128 ? j : ncols + j;
-  } else {
-    return nt * kBN + r;
-  }
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & (kChunks - 1); }
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt [3:0],[15:14]; expcnt [6:4]; lgkmcnt [11:8]).
+constexpr int kWaitVm0 = 0x0f70;    // vmcnt(0)
+constexpr int kWaitLgkm0 = 0xc07f;  // lgkmcnt(0)
+
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+
+// Workgroup barrier that neither the compiler nor the instruction scheduler
+// moves any instruction across.
+__device__ __forceinline__ void barrier() {
+  compiler_fence();
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  compiler_fence();
 }
 
-template <bool kSwiglu>
-__device__ __forceinline__ bool b_row_ok(int64_t nt, int r, int64_t ncols, int64_t N) {
-  if constexpr (kSwiglu) {
-    return nt * (kBN / 2) + (r & 127) < ncols;
-  } else {
-    return nt * kBN + r < N;
-  }
+// Waits for this thread's outstanding DMA (vector memory) or LDS operations.
+__device__ __forceinline__ void wait_dma() {
+  compiler_fence();
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  compiler_fence();
+}
+__device__ __forceinline__ void wait_lds() {
+  compiler_fence();
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  compiler_fence();
 }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
+// 16-byte global -> LDS copy (global_load_lds_dwordx4): lane i of the wave
+// writes bytes [16 i, 16 i + 16) of the 1 KiB block at `lds` (wave-uniform).
+// The builtin exists only for the device pass; the host pass only needs the
+// kernel's launch stub.
+__device__ __forceinline__ void dma16(const uint16_t *src, lds_void *lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+#else
+  (void)src;
+  (void)lds;
+#endif
+}
+
 template <bool kSwiglu>
-__global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(GemmArgs p) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][kBM * kLdsRow];
-  __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][kBN * kLdsRow];
+__device__ __forceinline__ int64_t b_row_clamped(int64_t nt, int r, int64_t ncols, int64_t N) {
+  if constexpr (kSwiglu) {
+    // rows 0..127: gate columns j0 .. j0+127; rows 128..255: up columns F + j0 ..
+    const int64_t j = std::min<int64_t>(nt * (kBN / 2) + (r & 127), ncols - 1);
+    return r < 128 ? j : ncols + j;
+  } else {
+    return std::min<int64_t>(nt * kBN + r, N - 1);
+  }
+}
+
+template <bool kSwiglu, int kWavesN>
+__global__ __launch_bounds__(kWavesM * kWavesN * 64) void grouped_gemm_kernel(GemmArgs p) {
+  constexpr int kWaves = kWavesM * kWavesN;
+  constexpr int kThreads = kWaves * 64;
+  constexpr int kMI = (kBM / kWavesM) / 32;            // 32-row blocks per wave (4)
+  constexpr int kNI = (kBN / kWavesN) / 32;            // 32-column blocks per wave (2 or 4)
+  constexpr int kDma = kOperandBytes / 1024 / kWaves;  // DMA instructions per operand per stage
+  constexpr int kEpiCols = kSwiglu ? kBN / 2 : kBN;    // output columns per tile
+  constexpr int kEpiRow = kEpiCols * 2 + 16;           // padded epilogue LDS row (bytes)
+  constexpr int kRingBytes = kStages * kStageBytes;
+  constexpr int kLdsBytes = kRingBytes > kBM * kEpiRow ? kRingBytes : kBM * kEpiRow;
+  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
+  lds_char *const sbase = (lds_char *)smem;  // address-space cast: LDS pointer arithmetic below
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 2;  // 0..1
-  const int wn = wave & 3;   // 0..3
+  const int wm = wave / kWavesN;
+  const int wn = wave % kWavesN;
   const int64_t P = gridDim.x;
   const int64_t b = blockIdx.x;
-  const int64_t ktiles = ceil_div(p.K, kBK);
+  const int64_t K = p.K;
+  const int ktiles = static_cast<int>(ceil_div(K, kBK));
 
-  // Group cursor: tiles before group g_cur, and group g_cur's row range.
-  int64_t g_cur = 0, tiles_before = 0;
   // Row ranges are clamped to [0, M] and made non-decreasing, so inconsistent
   // offsets can never send a load or store outside a and out.
   auto group_rows = [&](int64_t g, int64_t &lo, int64_t &hi) {
     lo = min(max(static_cast<int64_t>(p.offsets[g]), int64_t(0)), p.M);
     hi = min(max(static_cast<int64_t>(p.offsets[g + 1]), lo), p.M);
   };
-  int64_t m_lo, m_hi;
+  int64_t g_cur = 0, tiles_before = 0, m_lo, m_hi;
   group_rows(0, m_lo, m_hi);
   int64_t mt_g = ceil_div(m_hi - m_lo, kBM);
 
+  // DMA pattern: lane l fills 16 bytes of a lane-linear 1 KiB LDS block, i.e.
+  // row l / 8 of the block's 8 rows, physical chunk l % 8.
+  const int dma_row = lane / kChunks;
+  const int dma_pchunk = lane % kChunks;
+
+  // Fragment rows of this lane: byte offset of the row | (its swizzle << 4), so
+  // that logical chunk c of the row sits at (base ^ (c << 4)).
+  int fa_base[kMI], fb_base[kNI];
+#pragma unroll
+  for (int i = 0; i < kMI; ++i) {
+    const int r = wm * (kBM / kWavesM) + i * 32 + (lane & 31);
+    fa_base[i] = r * kRowBytes | (swz(r) << 4);
+  }
+#pragma unroll
+  for (int j = 0; j < kNI; ++j) {
+    int r;
+    if constexpr (kSwiglu) {
+      // gate blocks j < kNI/2, then the up blocks of the same output columns
+      const int jj = j % (kNI / 2);
+      r = (j < kNI / 2 ? 0 : 128) + wn * (128 / kWavesN) + jj * 32 + (lane & 31);
+    } else {
+      r = wn * (kBN / kWavesN) + j * 32 + (lane & 31);
+    }
+    fb_base[j] = r * kRowBytes | (swz(r) << 4);
+  }
+  const int khalf = lane >> 5;
+
   for (int64_t round = 0;; ++round) {
     const int64_t L = round * P + (b % 8) * (P / 8) + b / 8;
-    // Advance the cursor to the group holding logical tile L.
     while (g_cur < p.G && L >= tiles_before + mt_g * p.ntiles) {
       tiles_before += mt_g * p.ntiles;
       ++g_cur;
@@ -113,7 +204,6 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(GemmArgs p) {
     }
     if (g_cur >= p.G) break;
 
-    // Tile (row tile mt, column tile nt) inside group g_cur.
     const int64_t q = L - tiles_before;
     const int64_t full = mt_g / kGroupM;
     int64_t mt, nt;
@@ -126,33 +216,31 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(GemmArgs p) {
       nt = r / gm;
       mt = full * kGroupM + r % gm;
     }
-    const int64_t row0 = m_lo + mt * kBM;  // first A row of the tile
-    const uint16_t *wg = p.w + g_cur * p.N * p.K;
+    const int64_t row0 = m_lo + mt * kBM;
+    const uint16_t *wg = p.w + g_cur * p.N * K;
 
-    // Global -> register staging for one K step.
-    u32x4 ra[kVecPerThread], rb[kVecPerThread];
-    auto load_tile = [&](int64_t kt) {
-      const int64_t k0 = kt * kBK;
+    // Global source rows of this thread's DMA instructions (clamped, so always
+    // valid) and their logical chunk.
+    const uint16_t *a_src[kDma];
+    const uint16_t *b_src[kDma];
+    int dma_chunk[kDma];
 #pragma unroll
-      for (int i = 0; i < kVecPerThread; ++i) {
-        const int v = tid + i * kThreads;
-        const int r = v >> 3, c = v & 7;
-        const int64_t kk = k0 + c * 8;
-        const int64_t arow = row0 + r;
-        ra[i] = u32x4{0u, 0u, 0u, 0u};
-        rb[i] = u32x4{0u, 0u, 0u, 0u};
-        if (arow < m_hi && kk < p.K) ra[i] = *reinterpret_cast<const u32x4 *>(p.a + arow * p.K + kk);
-        if (b_row_ok<kSwiglu>(nt, r, p.ncols, p.N) && kk < p.K)
-          rb[i] = *reinterpret_cast<const u32x4 *>(wg + b_row<kSwiglu>(nt, r, p.ncols) * p.K + kk);
-      }
-    };
-    auto store_tile = [&](int buf) {
+    for (int j = 0; j < kDma; ++j) {
+      const int blk = j * kWaves + wave;
+      const int r = blk * kRowsPerKiB + dma_row;
+      dma_chunk[j] = dma_pchunk ^ swz(r);
+      a_src[j] = p.a + std::min<int64_t>(row0 + r, m_hi - 1) * K;
+      b_src[j] = wg + b_row_clamped<kSwiglu>(nt, r, p.ncols, p.N) * K;
+    }
+    auto issue_stage = [&](int kt) {
+      lds_char *st = sbase + (kt % kStages) * kStageBytes;
 #pragma unroll
-      for (int i = 0; i < kVecPerThread; ++i) {
-        const int v = tid + i * kThreads;
-        const int r = v >> 3, c = v & 7;
-        *reinterpret_cast<u32x4 *>(&lds_a[buf][r * kLdsRow + c * 8]) = ra[i];
-        *reinterpret_cast<u32x4 *>(&lds_b[buf][r * kLdsRow + c * 8]) = rb[i];
+      for (int j = 0; j < kDma; ++j) {
+        const int blk = j * kWaves + wave;
+        // A chunk in the K tail reads the row's last valid chunk instead (zeroed before use).
+        const int64_t k = std::min<int64_t>(static_cast<int64_t>(kt) * kBK + dma_chunk[j] * 8, K - 8);
+        dma16(a_src[j] + k, reinterpret_cast<lds_void *>(st + blk * 1024));
+        dma16(b_src[j] + k, reinterpret_cast<lds_void *>(st + kOperandBytes + blk * 1024));
       }
     };
 
@@ -162,59 +250,106 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(GemmArgs p) {
 #pragma unroll
       for (int j = 0; j < kNI; ++j) acc[i][j] = f32x16{};
 
-    // B-tile row of this wave's N block j.
-    int bro[kNI];
-#pragma unroll
-    for (int j = 0; j < kNI; ++j) bro[j] = kSwiglu ? j * 128 + wn * 32 : wn * 64 + j * 32;
+    barrier();  // the previous tile's epilogue is done with the LDS
+    issue_stage(0);
 
-    __syncthreads();  // previous tile's readers are done with both buffers
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
-    for (int64_t kt = 0; kt < ktiles; ++kt) {
-      const int cur = kt & 1;
-      if (kt + 1 < ktiles) load_tile(kt + 1);
+    for (int kt = 0; kt < ktiles; ++kt) {
+      wait_dma();  // this thread's DMA of stage kt has landed
+      barrier();   // ... and everyone's; stage kt-1's buffer is free
+      lds_char *st = sbase + (kt % kStages) * kStageBytes;
+      if (K % kBK != 0 && kt == ktiles - 1) {
+        // Zero the chunks of the K tail.
+        const int kvalid = static_cast<int>(K - static_cast<int64_t>(kt) * kBK);
+        for (int idx = tid; idx < 2 * kBM * kChunks; idx += kThreads) {
+          const int op = idx / (kBM * kChunks), rem = idx % (kBM * kChunks);
+          const int r = rem / kChunks, c = rem % kChunks;
+          if (c * 8 >= kvalid) {
+            *reinterpret_cast<lds_u32x4 *>(st + op * kOperandBytes + r * kRowBytes + ((c ^ swz(r)) * 16)) =
+                u32x4{0u, 0u, 0u, 0u};
+          }
+        }
+        wait_lds();
+        barrier();
+      }
+      if (kt + 1 < ktiles) issue_stage(kt + 1);
+
+      const lds_char *sa = st;
+      const lds_char *sb = st + kOperandBytes;
+      bf16x8 fa[2][kMI], fb[2][kNI];
+      auto load_frags = [&](int ks, int buf) {
+        const int c = ks * 2 + khalf;
 #pragma unroll
-      for (int ks = 0; ks < kBK / 16; ++ks) {
-        const int kcol = ks * 16 + (lane >> 5) * 8;
-        bf16x8 fa[kMI], fb[kNI];
+        for (int i = 0; i < kMI; ++i) fa[buf][i] = *reinterpret_cast<const lds_bf16x8 *>(sa + (fa_base[i] ^ (c << 4)));
 #pragma unroll
-        for (int i = 0; i < kMI; ++i)
-          fa[i] = *reinterpret_cast<const bf16x8 *>(&lds_a[cur][(wm * 128 + i * 32 + (lane & 31)) * kLdsRow + kcol]);
+        for (int j = 0; j < kNI; ++j) fb[buf][j] = *reinterpret_cast<const lds_bf16x8 *>(sb + (fb_base[j] ^ (c << 4)));
+      };
+      load_frags(0, 0);
 #pragma unroll
-        for (int j = 0; j < kNI; ++j)
-          fb[j] = *reinterpret_cast<const bf16x8 *>(&lds_b[cur][(bro[j] + (lane & 31)) * kLdsRow + kcol]);
+      for (int ks = 0; ks < kSubSteps; ++ks) {
+        if (ks + 1 < kSubSteps) load_frags(ks + 1, (ks + 1) & 1);
 #pragma unroll
         for (int i = 0; i < kMI; ++i)
 #pragma unroll
           for (int j = 0; j < kNI; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks & 1][i], fb[ks & 1][j], acc[i][j], 0, 0, 0);
       }
-      if (kt + 1 < ktiles) store_tile(cur ^ 1);
-      __syncthreads();
+      // Instruction groups for the unrolled K step: the reads of sub-step 0,
+      // then for each sub-step one MFMA after each read of the next sub-step.
+      __builtin_amdgcn_sched_group_barrier(0x100, kMI + kNI, 0);
+#pragma unroll
+      for (int ks = 0; ks + 1 < kSubSteps; ++ks) {
+#pragma unroll
+        for (int r = 0; r < kMI + kNI; ++r) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, kMI * kNI - (kMI + kNI), 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, kMI * kNI, 0);
     }
 
-    // Epilogue.  Accumulator register r of lane l in a 32x32 block holds
-    // row (r / 4) * 8 + (l / 32) * 4 + (r % 4), column l % 32.
+    // Epilogue: bf16 tile into LDS (accumulator register r of lane l in a 32x32
+    // block holds row (r / 4) * 8 + (l / 32) * 4 + (r % 4), column l % 32), then
+    // 16-byte row-contiguous stores.
+    barrier();  // every wave is done reading the last stage
 #pragma unroll
     for (int i = 0; i < kMI; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = row0 + wm * 128 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        if (row >= m_hi) continue;
+        const int row = wm * (kBM / kWavesM) + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
         if constexpr (kSwiglu) {
-          const int64_t col = nt * (kBN / 2) + wn * 32 + (lane & 31);
-          if (col < p.ncols) {
-            const float h = silu(acc[i][0][r]) * acc[i][1][r];
-            p.out[row * p.ncols + col] = static_cast<uint16_t>(f32_to_bf16_rne(h));
+#pragma unroll
+          for (int j = 0; j < kNI / 2; ++j) {
+            const int col = wn * (128 / kWavesN) + j * 32 + (lane & 31);
+            const float h = silu(acc[i][j][r]) * acc[i][j + kNI / 2][r];
+            *reinterpret_cast<lds_u16 *>(sbase + row * kEpiRow + col * 2) = static_cast<uint16_t>(f32_to_bf16_rne(h));
           }
         } else {
 #pragma unroll
           for (int j = 0; j < kNI; ++j) {
-            const int64_t col = nt * kBN + wn * 64 + j * 32 + (lane & 31);
-            if (col < p.N) p.out[row * p.N + col] = static_cast<uint16_t>(f32_to_bf16_rne(acc[i][j][r]));
+            const int col = wn * (kBN / kWavesN) + j * 32 + (lane & 31);
+            *reinterpret_cast<lds_u16 *>(sbase + row * kEpiRow + col * 2) =
+                static_cast<uint16_t>(f32_to_bf16_rne(acc[i][j][r]));
           }
         }
+      }
+    }
+    wait_lds();  // this wave's LDS writes are done
+    barrier();
+    const int64_t col0 = nt * kEpiCols;
+    constexpr int kChunksPerRow = kEpiCols / 8;
+#pragma unroll 4
+    for (int idx = tid; idx < kBM * kChunksPerRow; idx += kThreads) {
+      const int r = idx / kChunksPerRow, c = idx % kChunksPerRow;
+      const int64_t grow = row0 + r;
+      const int64_t gcol = col0 + c * 8;
+      if (grow >= m_hi || gcol >= p.ncols) continue;
+      const lds_char *src = sbase + r * kEpiRow + c * 16;
+      uint16_t *dst = p.out + grow * p.ncols + gcol;
+      if (p.vec_out && gcol + 8 <= p.ncols) {
+        __builtin_nontemporal_store(*reinterpret_cast<const lds_u32x4 *>(src), reinterpret_cast<u32x4 *>(dst));
+      } else {
+        for (int e = 0; e < 8 && gcol + e < p.ncols; ++e) dst[e] = *reinterpret_cast<const lds_u16 *>(src + 2 * e);
       }
     }
   }
@@ -252,7 +387,7 @@ int moe_grouped_gemm(const moe_bf16_t *a, int64_t M_total, int64_t K, const moe_
     return fail(MOE_ERR_INVALID_ARG, "moe_grouped_gemm: epilogue %d is not a moe_epilogue_t", epilogue);
   }
   if (G < 1 || G > 4096) return fail(MOE_ERR_CAPACITY, "moe_grouped_gemm: G=%lld outside [1, 4096]", (long long)G);
-  if (K % 8 != 0) return fail(MOE_ERR_SHAPE, "moe_grouped_gemm: K=%lld must be a multiple of 8", (long long)K);
+  if (K % 8 != 0 || K == 0) return fail(MOE_ERR_SHAPE, "moe_grouped_gemm: K=%lld must be a positive multiple of 8", (long long)K);
   const bool swiglu = epilogue == MOE_EPILOGUE_SWIGLU;
   if (swiglu && (N % 2 != 0)) return fail(MOE_ERR_SHAPE, "moe_grouped_gemm: SWIGLU needs an even N (got %lld)", (long long)N);
   if (group_offsets == nullptr) return fail(MOE_ERR_INVALID_ARG, "moe_grouped_gemm: null group_offsets");
@@ -275,14 +410,17 @@ int moe_grouped_gemm(const moe_bf16_t *a, int64_t M_total, int64_t K, const moe_
   p.G = G;
   p.ncols = ncols;
   p.ntiles = swiglu ? ceil_div(ncols, kBN / 2) : ceil_div(N, kBN);
+  p.vec_out = (ncols % 8 == 0) && is_aligned(out, 16);
   // Persistent grid: one workgroup per CU, a multiple of the 8 XCDs, no more
   // than an upper bound on the tile count.
   const int64_t max_tiles = (ceil_div(M_total, kBM) + G) * p.ntiles;
   int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
   grid = std::max<int64_t>(8, (grid + 7) / 8 * 8);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (swiglu) grouped_gemm_kernel<true><<<dim3(grid), dim3(kThreads), 0, s>>>(p);
-  else grouped_gemm_kernel<false><<<dim3(grid), dim3(kThreads), 0, s>>>(p);
+  constexpr int kWN = MOE_GEMM_WAVES_N;
+  constexpr int kThreads = kWavesM * kWN * 64;
+  if (swiglu) grouped_gemm_kernel<true, kWN><<<dim3(grid), dim3(kThreads), 0, s>>>(p);
+  else grouped_gemm_kernel<false, kWN><<<dim3(grid), dim3(kThreads), 0, s>>>(p);
   return check_launch("moe_grouped_gemm");
 }
 
