@@ -18,9 +18,16 @@
 namespace moe {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWavesPerBlock = kThreads / kWave;
-constexpr int kMaxVecPerLane = 16;  // 16 x 16 B per lane -> rows up to 8192 bf16 per pass
+#ifndef MOE_PERMUTE_THREADS
+#define MOE_PERMUTE_THREADS 512
+#endif
+#ifndef MOE_PERMUTE_SPLIT
+#define MOE_PERMUTE_SPLIT 2
+#endif
+constexpr int kThreads = MOE_PERMUTE_THREADS;
+constexpr int kSplit = MOE_PERMUTE_SPLIT;            // wavefronts sharing one token row
+constexpr int kTokensPerBlock = kThreads / kWave / kSplit;
+constexpr int kMaxVecPerLane = 16 / kSplit;         // 16-byte vectors per lane per pass
 
 struct PermuteArgs {
   const uint16_t *x;
@@ -42,25 +49,26 @@ template <bool kI64, bool kExpertMajor, bool kProbs, bool kVec>
 __global__ __launch_bounds__(kThreads) void permute_kernel(PermuteArgs a) {
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave;
+  const int part = wave % kSplit;  // which share of the row this wave copies
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kTokensPerBlock + wave / kSplit;
   int routed = 0;
 
   if (t < a.T) {
     if constexpr (kVec) {
       const int64_t nvec = a.H / 8;  // 16-byte vectors per row
       const u32x4 *src = reinterpret_cast<const u32x4 *>(a.x + t * a.H);
-      for (int64_t seg = 0; seg < nvec || seg == 0; seg += kMaxVecPerLane * kWave) {
+      for (int64_t seg = 0; seg < nvec || seg == 0; seg += kMaxVecPerLane * kWave * kSplit) {
         u32x4 buf[kMaxVecPerLane];
 #pragma unroll
         for (int j = 0; j < kMaxVecPerLane; ++j) {
-          const int64_t v = seg + j * kWave + lane;
+          const int64_t v = seg + (j * kSplit + part) * kWave + lane;
           if (v < nvec) buf[j] = __builtin_nontemporal_load(src + v);
         }
         for (int64_t e0 = 0; e0 < a.E; e0 += kWave) {
           const int64_t e = e0 + lane;
           const int64_t dst = e < a.E ? map_at<kI64, kExpertMajor>(a, t, e) : -1;
           uint64_t mask = __ballot(dst >= 0 && dst < a.num_out);
-          if (seg == 0) {
+          if (seg == 0 && part == 0) {
             routed += __popcll(__ballot(dst >= 0));
             if constexpr (kProbs) {
               if (dst >= 0 && dst < a.num_out && a.pp != nullptr) a.pp[dst] = a.probs[t * a.E + e];
@@ -73,7 +81,7 @@ __global__ __launch_bounds__(kThreads) void permute_kernel(PermuteArgs a) {
             u32x4 *o = reinterpret_cast<u32x4 *>(a.out + d * a.H);
 #pragma unroll
             for (int j = 0; j < kMaxVecPerLane; ++j) {
-              const int64_t v = seg + j * kWave + lane;
+              const int64_t v = seg + (j * kSplit + part) * kWave + lane;
               if (v < nvec) __builtin_nontemporal_store(buf[j], o + v);
             }
           }
@@ -87,28 +95,30 @@ __global__ __launch_bounds__(kThreads) void permute_kernel(PermuteArgs a) {
         const int64_t e = e0 + lane;
         const int64_t dst = e < a.E ? map_at<kI64, kExpertMajor>(a, t, e) : -1;
         uint64_t mask = __ballot(dst >= 0 && dst < a.num_out);
-        routed += __popcll(__ballot(dst >= 0));
-        if constexpr (kProbs) {
-          if (dst >= 0 && dst < a.num_out && a.pp != nullptr) a.pp[dst] = a.probs[t * a.E + e];
+        if (part == 0) {
+          routed += __popcll(__ballot(dst >= 0));
+          if constexpr (kProbs) {
+            if (dst >= 0 && dst < a.num_out && a.pp != nullptr) a.pp[dst] = a.probs[t * a.E + e];
+          }
         }
         while (mask) {
           const int b = __builtin_ctzll(mask);
           mask &= mask - 1;
           const int64_t d = readlane64(dst, b);
           uint16_t *o = a.out + d * a.H;
-          for (int64_t i = lane; i < a.H; i += kWave) o[i] = src[i];
+          for (int64_t i = part * kWave + lane; i < a.H; i += kWave * kSplit) o[i] = src[i];
         }
       }
     }
   }
 
   if (a.block_counts != nullptr) {
-    __shared__ int wave_routed[kWavesPerBlock];
+    __shared__ int wave_routed[kThreads / kWave];
     if (lane == 0) wave_routed[wave] = routed;
     __syncthreads();
     if (threadIdx.x == 0) {
       int s = 0;
-      for (int w = 0; w < kWavesPerBlock; ++w) s += wave_routed[w];
+      for (int w = 0; w < kThreads / kWave; ++w) s += wave_routed[w];
       a.block_counts[blockIdx.x] = s;
     }
   }
@@ -173,7 +183,7 @@ extern "C" {
 
 size_t moe_permute_workspace_size(int64_t T) {
   if (T < 0) return 0;
-  return static_cast<size_t>(moe::ceil_div(T, moe::kWavesPerBlock)) * sizeof(int32_t) + 256;
+  return static_cast<size_t>(moe::ceil_div(T, moe::kTokensPerBlock)) * sizeof(int32_t) + 256;
 }
 
 int moe_permute(const moe_bf16_t *x, int64_t T, int64_t H, const void *row_id_map, int idx_dtype,
@@ -198,7 +208,7 @@ int moe_permute(const moe_bf16_t *x, int64_t T, int64_t H, const void *row_id_ma
   if (permuted_probs != nullptr && probs == nullptr && T * E > 0) {
     return fail(MOE_ERR_INVALID_ARG, "moe_permute: permuted_probs given without probs");
   }
-  const int64_t nblocks = ceil_div(T, kWavesPerBlock);
+  const int64_t nblocks = ceil_div(T, kTokensPerBlock);
   if (nblocks > 0x7fffffff) return fail(MOE_ERR_CAPACITY, "moe_permute: T=%lld too large", (long long)T);
   if (zero_tail && (workspace == nullptr || workspace_bytes < moe_permute_workspace_size(T))) {
     return fail(MOE_ERR_WORKSPACE, "moe_permute: zero_tail needs %zu bytes of workspace, got %zu",

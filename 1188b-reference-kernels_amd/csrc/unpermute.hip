@@ -27,8 +27,15 @@
 namespace moe {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWavesPerBlock = kThreads / kWave;
+#ifndef MOE_UNPERMUTE_THREADS
+#define MOE_UNPERMUTE_THREADS 512
+#endif
+#ifndef MOE_UNPERMUTE_SPLIT
+#define MOE_UNPERMUTE_SPLIT 2
+#endif
+constexpr int kThreads = MOE_UNPERMUTE_THREADS;
+constexpr int kSplit = MOE_UNPERMUTE_SPLIT;  // wavefronts sharing one token row
+constexpr int kWavesPerBlock = kThreads / kWave / kSplit;  // tokens per workgroup
 constexpr int kBatch = 8;
 
 enum Mode { kPlain = 0, kMerge = 1, kBwd = 2 };
@@ -68,7 +75,8 @@ template <bool kI64, bool kExpertMajor, int kMode, int kChunks, bool kVec>
 __global__ __launch_bounds__(kThreads) void unpermute_kernel(UnpermuteArgs a) {
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave;
+  const int part = wave % kSplit;  // which share of the row this wave sums
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave / kSplit;
   if (t >= a.T) return;
 
   // Map entries of this token, 64 experts per chunk, ascending expert order.
@@ -88,13 +96,13 @@ __global__ __launch_bounds__(kThreads) void unpermute_kernel(UnpermuteArgs a) {
       if (ok) w[c] = a.probs[t * a.E + e];
     }
     if constexpr (kMode == kBwd) {
-      if (e < a.E) a.dprobs[t * a.E + e] = ok ? a.probs[s] : 0.0f;
+      if (e < a.E && part == 0) a.dprobs[t * a.E + e] = ok ? a.probs[s] : 0.0f;
     }
   }
 
   if constexpr (kVec) {
     const int64_t nvec = a.H / 8;
-    for (int64_t v = lane; v < nvec; v += kWave) {
+    for (int64_t v = part * kWave + lane; v < nvec; v += kWave * kSplit) {
       float acc[8];
 #pragma unroll
       for (int q = 0; q < 8; ++q) acc[q] = 0.0f;
@@ -143,7 +151,7 @@ __global__ __launch_bounds__(kThreads) void unpermute_kernel(UnpermuteArgs a) {
       }
     }
   } else {
-    for (int64_t i = lane; i < a.H; i += kWave) {
+    for (int64_t i = part * kWave + lane; i < a.H; i += kWave * kSplit) {
       float acc = 0.0f;
 #pragma unroll
       for (int c = 0; c < kChunks; ++c) {
