@@ -89,6 +89,28 @@ def cpu_baseline(pkg, x, logits, w1, w2, k, run_s=2.5):
                       f"of {[round(v, 3) for v in times]} s"}
 
 
+def library_reference(m, kdim, n, groups, dev, reps=5):
+    """torch.bmm (hipBLASLt) on `groups` equal [m, kdim] @ [kdim, n] bf16 products; ms and TFLOP/s.
+
+    The right operand is materialised K-major ([groups, kdim, n], contiguous), the layout the
+    library's fastest kernel for this shape reads.
+    """
+    a = torch.randn(groups, m, kdim, device=dev, dtype=torch.bfloat16)
+    b = torch.randn(groups, n, kdim, device=dev, dtype=torch.bfloat16).transpose(1, 2).contiguous()
+    for _ in range(2):
+        torch.bmm(a, b)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record()
+    for _ in range(reps):
+        torch.bmm(a, b)
+    ev[1].record()
+    torch.cuda.synchronize()
+    ms = ev[0].elapsed_time(ev[1]) / reps
+    flops = 2 * groups * m * kdim * n
+    return {"op": f"torch.bmm bf16 {groups} x [{m}, {kdim}] @ [{kdim}, {n}]", "ms": round(ms, 4),
+            "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -98,6 +120,9 @@ def main():
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the timed steps, gather-copy this many MiB once (index_select_vec_kernel): "
                          "the known-size copy that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
+    ap.add_argument("--library-reference", action="store_true",
+                    help="also time torch.bmm (hipBLASLt) on the fc1 shape with equal groups "
+                         "(E x [R/E, H] @ [H, 2F]): a library GEMM of the same size, reported beside the stages")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the MoE dispatch path here has no multi-GPU (expert-parallel) "
@@ -182,6 +207,10 @@ def main():
         torch.cuda.synchronize()
         del src
 
+    library = None
+    if args.library_reference:
+        library = library_reference(T * k // E, H, 2 * F, E, dev)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(pkg, x, logits, w1, w2, k)
@@ -198,6 +227,8 @@ def main():
         "cpu_baseline": cpu,
         "device": torch.cuda.get_device_name(0),
     }
+    if library is not None:
+        line["library_reference"] = library
     print(json.dumps(line))
 
 
