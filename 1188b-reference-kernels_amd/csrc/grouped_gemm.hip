@@ -9,22 +9,29 @@
 // fp32 accumulators, F = N / 2, rounded once to bf16.
 //
 // Kernel shape (gfx950):
-//   * one persistent workgroup per CU; output tile 256 x 256, K step 64;
-//   * A and B tiles stream through a two-stage LDS ring (2 x 2 x 256 x 64
-//     bf16 = 128 KiB) filled by global_load_lds_dwordx4 (memory -> LDS without
-//     VGPRs), one K step ahead of the MFMAs;
+//   * one persistent workgroup of 4 wavefronts (one per SIMD) per CU; output
+//     tile 256 x 256, K step 64; each wavefront owns 128 x 128 of the tile as
+//     4 x 4 blocks of v_mfma_f32_32x32x16_bf16 (256 accumulator registers);
+//   * A and B tiles stream through a two-stage LDS ring (2 x 2 x 256 x 64 bf16
+//     = 128 KiB) filled by buffer_load_dwordx4 ... lds (memory -> LDS without
+//     VGPRs; buffer resources bound each load to the valid rows), one K step
+//     ahead of the MFMAs;
 //   * LDS rows are XOR-swizzled in 16-byte chunks (chunk ^ (row / 2) % 8), which
 //     makes both the DMA writes (lane-linear 1 KiB blocks) and the MFMA operand
 //     reads (16 lanes x 16 B) bank-conflict-free;
-//   * kWavesM x kWavesN wavefronts, each owning a 128 x (256 / kWavesN) part of
-//     the tile as kMI x kNI blocks of v_mfma_f32_32x32x16_bf16; within a K step
-//     the operand fragments of 16-wide sub-step s+1 are read from LDS between
-//     the MFMAs of sub-step s (instruction-group scheduling);
+//   * the operand fragments of a whole K step live in VGPRs: while the MFMAs of
+//     step kt run from them, the fragments of step kt + 1 are read from LDS one
+//     sub-step at a time, and the DMA of step kt + 2 is issued, one instruction
+//     after each MFMA (instruction-group scheduling); one workgroup barrier per
+//     step, after the first sub-step's MFMAs;
+//   * w is the MFMA's first operand, so the accumulators hold the transposed
+//     block and each lane owns 4 consecutive output columns per 4 registers:
+//     the epilogue rounds them to bf16 in hardware (RNE) and writes 8-byte
+//     words into an LDS tile, then 16-byte row-contiguous non-temporal stores;
 //   * SwiGLU tiles load 128 gate rows and the matching 128 up rows of w; each
 //     wave's N blocks are gate blocks followed by the up blocks of the same
-//     output columns, so the epilogue combines them in registers;
-//   * the epilogue rounds to bf16 into an LDS tile and writes 16-byte
-//     row-contiguous non-temporal stores;
+//     output columns, so the epilogue combines them in registers
+//     (silu(g) = g / (1 + 2^(-g log2 e)) with the hardware exp2 and reciprocal);
 //   * tiles are numbered expert by expert, and inside an expert in groups of
 //     4 row tiles x all column tiles (row tile fastest), so 32 consecutive
 //     tile numbers form a 4 x 8 patch that shares A and B panels; workgroup b
@@ -32,15 +39,12 @@
 //     (workgroups are dealt round-robin to the 8 XCDs) one such patch per
 //     round, so the panels are reused from that XCD's L2.
 // Rows past a group's end and columns past N are loaded from a clamped (valid)
-// address and their results are discarded; a K tail (K % 64 != 0) is zeroed in
-// LDS before use.
+// row and their results are discarded; a K tail (K % 64 != 0) is zeroed in LDS
+// before use. Buffer offsets are 32-bit: the host requires 512 K and 2 N K to
+// stay below 2^32 bytes.
 #include <algorithm>
 
 #include "moe_common.h"
-
-#ifndef MOE_GEMM_WAVES_N
-#define MOE_GEMM_WAVES_N 4
-#endif
 
 namespace moe {
 namespace {
@@ -52,9 +56,10 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 typedef __attribute__((address_space(3))) uint16_t lds_u16;
 typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 
 constexpr int kBM = 256, kBN = 256, kBK = 64;
-constexpr int kWavesM = 2;
 constexpr int kGroupM = 4;                        // row tiles per tile-order group
 constexpr int kRowBytes = kBK * 2;                // 128: one tile row in LDS
 constexpr int kChunks = kBK / 8;                  // 8 chunks of 16 bytes per row
@@ -107,19 +112,6 @@ __device__ __forceinline__ void wait_lds() {
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
-// 16-byte global -> LDS copy (global_load_lds_dwordx4): lane i of the wave
-// writes bytes [16 i, 16 i + 16) of the 1 KiB block at `lds` (wave-uniform).
-// The builtin exists only for the device pass; the host pass only needs the
-// kernel's launch stub.
-__device__ __forceinline__ void dma16(const uint16_t *src, lds_void *lds) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
-#else
-  (void)src;
-  (void)lds;
-#endif
-}
-
 template <bool kSwiglu>
 __device__ __forceinline__ int64_t b_row_clamped(int64_t nt, int r, int64_t ncols, int64_t N) {
   if constexpr (kSwiglu) {
@@ -131,32 +123,80 @@ __device__ __forceinline__ int64_t b_row_clamped(int64_t nt, int r, int64_t ncol
   }
 }
 
-template <bool kSwiglu, int kWavesN>
-__global__ __launch_bounds__(kWavesM * kWavesN * 64) void grouped_gemm_kernel(GemmArgs p) {
-  constexpr int kWaves = kWavesM * kWavesN;
-  constexpr int kThreads = kWaves * 64;
-  constexpr int kMI = (kBM / kWavesM) / 32;            // 32-row blocks per wave (4)
-  constexpr int kNI = (kBN / kWavesN) / 32;            // 32-column blocks per wave (2 or 4)
-  constexpr int kDma = kOperandBytes / 1024 / kWaves;  // DMA instructions per operand per stage
-  constexpr int kEpiCols = kSwiglu ? kBN / 2 : kBN;    // output columns per tile
-  constexpr int kEpiRow = kEpiCols * 2 + 16;           // padded epilogue LDS row (bytes)
+
+// Buffer resource over [base, base + bytes): raw buffer loads past `bytes`
+// return zeros instead of touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+// 16-byte buffer -> LDS copy: lane i writes bytes [16 i, 16 i + 16) of the 1 KiB
+// block at `lds` (wave-uniform); the global address is rsrc base + voff + soff.
+__device__ __forceinline__ void dma16b(__amdgpu_buffer_rsrc_t rsrc, lds_void *lds, int voff, int soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds, 16, voff, soff, 0, 0);
+#else
+  (void)rsrc; (void)lds; (void)voff; (void)soff;
+#endif
+}
+template <int kN>
+__device__ __forceinline__ void wait_vm_n() {
+  compiler_fence();
+  __builtin_amdgcn_s_waitcnt((kN & 0xf) | ((kN >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+  compiler_fence();
+}
+
+// Instruction-group order for one sub-step: each of the first 8 MFMAs followed
+// by one instruction of kind kFirst (0x100 LDS read, 0x020 vector-memory read),
+// each of the last 8 by one of kind kSecond (0 = none).
+template <int kFirst, int kSecond>
+__device__ __forceinline__ void sched_pattern() {
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kFirst, 1, 0);
+  }
+  if constexpr (kSecond != 0) {
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSecond, 1, 0);
+    }
+  } else {
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+  }
+}
+
+// Four wavefronts (one per SIMD), each 128 x 128 of the 256 x 256 tile as 4 x 4
+// blocks of 32 x 32. The operand fragments of a whole K step (4 sub-steps x 8
+// fragments) live in VGPRs: while the MFMAs of step kt run from them, the
+// fragments of step kt + 1 are read from LDS sub-step by sub-step. One barrier
+// per step, after the first sub-step's MFMAs, publishes stage kt + 1 (its DMA
+// has landed) and frees the LDS slot of stage kt for the DMA of stage kt + 2.
+template <bool kSwiglu>
+__global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
+  constexpr int kWaves = 4;
+  constexpr int kThreads = 256;
+  constexpr int kMI = 4, kNI = 4;
+  constexpr int kDma = kOperandBytes / 1024 / kWaves;  // 8 DMA instructions per operand per stage
+  constexpr int kEpiCols = kSwiglu ? kBN / 2 : kBN;
+  constexpr int kEpiRow = kEpiCols * 2 + 16;
   constexpr int kRingBytes = kStages * kStageBytes;
   constexpr int kLdsBytes = kRingBytes > kBM * kEpiRow ? kRingBytes : kBM * kEpiRow;
   __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
-  lds_char *const sbase = (lds_char *)smem;  // address-space cast: LDS pointer arithmetic below
+  lds_char *const sbase = (lds_char *)smem;
+  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sbase));
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave / kWavesN;
-  const int wn = wave % kWavesN;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
   const int64_t P = gridDim.x;
   const int64_t b = blockIdx.x;
   const int64_t K = p.K;
   const int ktiles = static_cast<int>(ceil_div(K, kBK));
+  const bool ktail = (K % kBK) != 0;
 
-  // Row ranges are clamped to [0, M] and made non-decreasing, so inconsistent
-  // offsets can never send a load or store outside a and out.
   auto group_rows = [&](int64_t g, int64_t &lo, int64_t &hi) {
     lo = min(max(static_cast<int64_t>(p.offsets[g]), int64_t(0)), p.M);
     hi = min(max(static_cast<int64_t>(p.offsets[g + 1]), lo), p.M);
@@ -165,28 +205,23 @@ __global__ __launch_bounds__(kWavesM * kWavesN * 64) void grouped_gemm_kernel(Ge
   group_rows(0, m_lo, m_hi);
   int64_t mt_g = ceil_div(m_hi - m_lo, kBM);
 
-  // DMA pattern: lane l fills 16 bytes of a lane-linear 1 KiB LDS block, i.e.
-  // row l / 8 of the block's 8 rows, physical chunk l % 8.
   const int dma_row = lane / kChunks;
   const int dma_pchunk = lane % kChunks;
 
-  // Fragment rows of this lane: byte offset of the row | (its swizzle << 4), so
-  // that logical chunk c of the row sits at (base ^ (c << 4)).
   int fa_base[kMI], fb_base[kNI];
 #pragma unroll
   for (int i = 0; i < kMI; ++i) {
-    const int r = wm * (kBM / kWavesM) + i * 32 + (lane & 31);
+    const int r = wm * 128 + i * 32 + (lane & 31);
     fa_base[i] = r * kRowBytes | (swz(r) << 4);
   }
 #pragma unroll
   for (int j = 0; j < kNI; ++j) {
     int r;
     if constexpr (kSwiglu) {
-      // gate blocks j < kNI/2, then the up blocks of the same output columns
       const int jj = j % (kNI / 2);
-      r = (j < kNI / 2 ? 0 : 128) + wn * (128 / kWavesN) + jj * 32 + (lane & 31);
+      r = (j < kNI / 2 ? 0 : 128) + wn * 64 + jj * 32 + (lane & 31);
     } else {
-      r = wn * (kBN / kWavesN) + j * 32 + (lane & 31);
+      r = wn * 128 + j * 32 + (lane & 31);
     }
     fb_base[j] = r * kRowBytes | (swz(r) << 4);
   }
@@ -204,43 +239,72 @@ __global__ __launch_bounds__(kWavesM * kWavesN * 64) void grouped_gemm_kernel(Ge
     }
     if (g_cur >= p.G) break;
 
-    const int64_t q = L - tiles_before;
-    const int64_t full = mt_g / kGroupM;
-    int64_t mt, nt;
-    if (q < full * kGroupM * p.ntiles) {
-      const int64_t grp = q / (kGroupM * p.ntiles), r = q % (kGroupM * p.ntiles);
+    // Position inside the group (32-bit: a group's tile count exceeds 2^32 only
+    // for outputs of more than 2^48 elements).
+    const uint32_t q = static_cast<uint32_t>(L - tiles_before);
+    const uint32_t ntl = static_cast<uint32_t>(p.ntiles);
+    const uint32_t per_grp = kGroupM * ntl;
+    const uint32_t full = static_cast<uint32_t>(mt_g) / kGroupM;
+    uint32_t mt, nt;
+    if (q < full * per_grp) {
+      const uint32_t grp = q / per_grp, r = q - grp * per_grp;
       nt = r / kGroupM;
       mt = grp * kGroupM + r % kGroupM;
     } else {
-      const int64_t r = q - full * kGroupM * p.ntiles, gm = mt_g - full * kGroupM;
+      const uint32_t r = q - full * per_grp, gm = static_cast<uint32_t>(mt_g) - full * kGroupM;
       nt = r / gm;
-      mt = full * kGroupM + r % gm;
+      mt = full * kGroupM + (r - nt * gm);
     }
     const int64_t row0 = m_lo + mt * kBM;
+    const int rows_valid = static_cast<int>(min(m_hi - row0, int64_t(kBM)));
     const uint16_t *wg = p.w + g_cur * p.N * K;
 
-    // Global source rows of this thread's DMA instructions (clamped, so always
-    // valid) and their logical chunk.
-    const uint16_t *a_src[kDma];
-    const uint16_t *b_src[kDma];
-    int dma_chunk[kDma];
+    // Buffer resources: A over this tile's valid rows, B over this expert's matrix.
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + row0 * K, static_cast<uint32_t>(rows_valid * K * 2));
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(wg, static_cast<uint32_t>(p.N * K * 2));
+    int a_off[kDma], b_off[kDma];
 #pragma unroll
     for (int j = 0; j < kDma; ++j) {
       const int blk = j * kWaves + wave;
       const int r = blk * kRowsPerKiB + dma_row;
-      dma_chunk[j] = dma_pchunk ^ swz(r);
-      a_src[j] = p.a + std::min<int64_t>(row0 + r, m_hi - 1) * K;
-      b_src[j] = wg + b_row_clamped<kSwiglu>(nt, r, p.ncols, p.N) * K;
+      const int lchunk = dma_pchunk ^ swz(r);
+      const uint32_t row_bytes = static_cast<uint32_t>(K) * 2u;
+      a_off[j] = static_cast<int>(static_cast<uint32_t>(min(r, rows_valid - 1)) * row_bytes + lchunk * 16);
+      b_off[j] = static_cast<int>(static_cast<uint32_t>(b_row_clamped<kSwiglu>(nt, r, p.ncols, p.N)) * row_bytes +
+                                  lchunk * 16);
     }
+    // Stage kt into LDS slot kt % 2. Chunks past K read the next row (or zeros
+    // past the resource) and are zeroed in LDS before use.
     auto issue_stage = [&](int kt) {
-      lds_char *st = sbase + (kt % kStages) * kStageBytes;
+      const uint32_t st = lds_base + (kt % kStages) * kStageBytes;
+      const int soff = kt * kBK * 2;
 #pragma unroll
       for (int j = 0; j < kDma; ++j) {
-        const int blk = j * kWaves + wave;
-        // A chunk in the K tail reads the row's last valid chunk instead (zeroed before use).
-        const int64_t k = std::min<int64_t>(static_cast<int64_t>(kt) * kBK + dma_chunk[j] * 8, K - 8);
-        dma16(a_src[j] + k, reinterpret_cast<lds_void *>(st + blk * 1024));
-        dma16(b_src[j] + k, reinterpret_cast<lds_void *>(st + kOperandBytes + blk * 1024));
+        const uint32_t blk = j * kWaves + wave;
+        dma16b(ra, (lds_void *)(uintptr_t)(st + blk * 1024), a_off[j], soff);
+        dma16b(rb, (lds_void *)(uintptr_t)(st + kOperandBytes + blk * 1024), b_off[j], soff);
+      }
+    };
+    // Half of stage `kt` (operand `op`) into LDS slot `slot`.
+    auto issue_half = [&](int kt, int slot, int op) {
+      const uint32_t st = lds_base + (slot % kStages) * kStageBytes + op * kOperandBytes;
+      const int soff = kt * kBK * 2;
+#pragma unroll
+      for (int j = 0; j < kDma; ++j) {
+        const uint32_t blk = j * kWaves + wave;
+        dma16b(op ? rb : ra, (lds_void *)(uintptr_t)(st + blk * 1024), op ? b_off[j] : a_off[j], soff);
+      }
+    };
+    auto zero_ktail = [&](int kt) {
+      lds_char *st = sbase + (kt % kStages) * kStageBytes;
+      const int kvalid = static_cast<int>(K - static_cast<int64_t>(kt) * kBK);
+      for (int idx = tid; idx < 2 * kBM * kChunks; idx += kThreads) {
+        const int op = idx / (kBM * kChunks), rem = idx % (kBM * kChunks);
+        const int r = rem / kChunks, c = rem % kChunks;
+        if (c * 8 >= kvalid) {
+          *reinterpret_cast<lds_u32x4 *>(st + op * kOperandBytes + r * kRowBytes + ((c ^ swz(r)) * 16)) =
+              u32x4{0u, 0u, 0u, 0u};
+        }
       }
     };
 
@@ -250,91 +314,124 @@ __global__ __launch_bounds__(kWavesM * kWavesN * 64) void grouped_gemm_kernel(Ge
 #pragma unroll
       for (int j = 0; j < kNI; ++j) acc[i][j] = f32x16{};
 
+    // LDS byte addresses of this lane's fragment rows in the slot read next
+    // (logical chunk khalf); sub-step ks reads chunk 2 ks + khalf = addr ^ (ks << 5).
+    uint32_t rd_a[kMI], rd_b[kNI];
+    auto set_read_slot = [&](int kt) {
+      const uint32_t so = lds_base + (kt % kStages) * kStageBytes;
+#pragma unroll
+      for (int i = 0; i < kMI; ++i) rd_a[i] = so + (fa_base[i] ^ (khalf << 4));
+#pragma unroll
+      for (int j = 0; j < kNI; ++j) rd_b[j] = so + kOperandBytes + (fb_base[j] ^ (khalf << 4));
+    };
+    bf16x8 fa[kSubSteps][kMI], fb[kSubSteps][kNI];
+    auto read_frags = [&](int ks) {
+#pragma unroll
+      for (int i = 0; i < kMI; ++i)
+        fa[ks][i] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)(rd_a[i] ^ (ks << 5)));
+#pragma unroll
+      for (int j = 0; j < kNI; ++j)
+        fb[ks][j] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)(rd_b[j] ^ (ks << 5)));
+    };
+    auto mfma_ks = [&](int ks) {
+#pragma unroll
+      for (int i = 0; i < kMI; ++i)
+#pragma unroll
+        for (int j = 0; j < kNI; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks][j], fa[ks][i], acc[i][j], 0, 0, 0);
+    };
+    // Prologue: stages 0 and 1 in flight; stage 0 published and read into VGPRs.
     barrier();  // the previous tile's epilogue is done with the LDS
     issue_stage(0);
+    if (ktiles > 1) {
+      issue_stage(1);
+      wait_vm_n<2 * kDma>();
+    } else {
+      wait_dma();
+    }
+    barrier();
+    if (ktail && ktiles == 1) {
+      zero_ktail(0);
+      wait_lds();
+      barrier();
+    }
+    set_read_slot(0);
+#pragma unroll
+    for (int ks = 0; ks < kSubSteps; ++ks) read_frags(ks);
 
-    for (int kt = 0; kt < ktiles; ++kt) {
-      wait_dma();  // this thread's DMA of stage kt has landed
-      barrier();   // ... and everyone's; stage kt-1's buffer is free
-      lds_char *st = sbase + (kt % kStages) * kStageBytes;
-      if (K % kBK != 0 && kt == ktiles - 1) {
-        // Zero the chunks of the K tail.
-        const int kvalid = static_cast<int>(K - static_cast<int64_t>(kt) * kBK);
-        for (int idx = tid; idx < 2 * kBM * kChunks; idx += kThreads) {
-          const int op = idx / (kBM * kChunks), rem = idx % (kBM * kChunks);
-          const int r = rem / kChunks, c = rem % kChunks;
-          if (c * 8 >= kvalid) {
-            *reinterpret_cast<lds_u32x4 *>(st + op * kOperandBytes + r * kRowBytes + ((c ^ swz(r)) * 16)) =
-                u32x4{0u, 0u, 0u, 0u};
-          }
-        }
+    for (int kt = 0; kt + 1 < ktiles; ++kt) {
+      mfma_ks(0);
+      __builtin_amdgcn_sched_barrier(0);
+      // This thread's DMA of stage kt + 1 has landed and its reads of stage kt
+      // are done; after the barrier, everyone's.
+      wait_dma();
+      wait_lds();
+      barrier();
+      if (ktail && kt + 1 == ktiles - 1) {
+        zero_ktail(kt + 1);
         wait_lds();
         barrier();
       }
-      if (kt + 1 < ktiles) issue_stage(kt + 1);
-
-      const lds_char *sa = st;
-      const lds_char *sb = st + kOperandBytes;
-      bf16x8 fa[2][kMI], fb[2][kNI];
-      auto load_frags = [&](int ks, int buf) {
-        const int c = ks * 2 + khalf;
-#pragma unroll
-        for (int i = 0; i < kMI; ++i) fa[buf][i] = *reinterpret_cast<const lds_bf16x8 *>(sa + (fa_base[i] ^ (c << 4)));
-#pragma unroll
-        for (int j = 0; j < kNI; ++j) fb[buf][j] = *reinterpret_cast<const lds_bf16x8 *>(sb + (fb_base[j] ^ (c << 4)));
-      };
-      load_frags(0, 0);
-#pragma unroll
-      for (int ks = 0; ks < kSubSteps; ++ks) {
-        if (ks + 1 < kSubSteps) load_frags(ks + 1, (ks + 1) & 1);
-#pragma unroll
-        for (int i = 0; i < kMI; ++i)
-#pragma unroll
-          for (int j = 0; j < kNI; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks & 1][i], fb[ks & 1][j], acc[i][j], 0, 0, 0);
-      }
-      // Instruction groups for the unrolled K step: the reads of sub-step 0,
-      // then for each sub-step one MFMA after each read of the next sub-step.
-      __builtin_amdgcn_sched_group_barrier(0x100, kMI + kNI, 0);
-#pragma unroll
-      for (int ks = 0; ks + 1 < kSubSteps; ++ks) {
-#pragma unroll
-        for (int r = 0; r < kMI + kNI; ++r) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, kMI * kNI - (kMI + kNI), 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, kMI * kNI, 0);
+      // Stage kt + 2 into the slot of stage kt (the last steps re-read the
+      // final stage into that free slot, so the region below has no branch).
+      const int kdma = min(kt + 2, ktiles - 1);
+      set_read_slot(kt + 1);
+      read_frags(0);          // sub-step 0 of stage kt + 1 (its old fragments are used)
+      mfma_ks(1);
+      issue_half(kdma, kt + 2, 0);
+      sched_pattern<0x100, 0x020>();  // ks 1: the 8 reads above, then 8 DMAs of A
+      mfma_ks(2);
+      read_frags(1);
+      issue_half(kdma, kt + 2, 1);
+      sched_pattern<0x100, 0x020>();  // ks 2: reads of sub-step 1, then 8 DMAs of B
+      mfma_ks(3);
+      read_frags(2);
+      sched_pattern<0x100, 0>();      // ks 3: reads of sub-step 2
+      read_frags(3);
+      __builtin_amdgcn_sched_barrier(0);
     }
+    mfma_ks(0);
+    mfma_ks(1);
+    mfma_ks(2);
+    mfma_ks(3);
+    wait_dma();  // the re-reads of the last steps have landed before the LDS is reused
 
-    // Epilogue: bf16 tile into LDS (accumulator register r of lane l in a 32x32
-    // block holds row (r / 4) * 8 + (l / 32) * 4 + (r % 4), column l % 32), then
-    // 16-byte row-contiguous stores.
     barrier();  // every wave is done reading the last stage
+    // With w as the MFMA's first operand, register r of lane l in block (i, j)
+    // holds output row i * 32 + l % 32 and column j * 32 + (r / 4) * 8 + (l / 32) * 4
+    // + r % 4 of this wave's part: 4 consecutive columns per 4 registers, which
+    // are rounded (RNE, hardware) and written to the LDS tile as one 8-byte word.
 #pragma unroll
     for (int i = 0; i < kMI; ++i) {
+      const int row = wm * 128 + i * 32 + (lane & 31);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = wm * (kBM / kWavesM) + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+      for (int g = 0; g < 4; ++g) {
         if constexpr (kSwiglu) {
 #pragma unroll
           for (int j = 0; j < kNI / 2; ++j) {
-            const int col = wn * (128 / kWavesN) + j * 32 + (lane & 31);
-            const float h = silu(acc[i][j][r]) * acc[i][j + kNI / 2][r];
-            *reinterpret_cast<lds_u16 *>(sbase + row * kEpiRow + col * 2) = static_cast<uint16_t>(f32_to_bf16_rne(h));
+            const int col = wn * 64 + j * 32 + g * 8 + (lane >> 5) * 4;
+            float h[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const float gt = acc[i][j][4 * g + q];
+              h[q] = gt * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gt * -1.4426950408889634f)) *
+                     acc[i][j + kNI / 2][4 * g + q];
+            }
+            const bf16x4 v = {(__bf16)h[0], (__bf16)h[1], (__bf16)h[2], (__bf16)h[3]};
+            *reinterpret_cast<lds_bf16x4 *>(sbase + row * kEpiRow + col * 2) = v;
           }
         } else {
 #pragma unroll
           for (int j = 0; j < kNI; ++j) {
-            const int col = wn * (kBN / kWavesN) + j * 32 + (lane & 31);
-            *reinterpret_cast<lds_u16 *>(sbase + row * kEpiRow + col * 2) =
-                static_cast<uint16_t>(f32_to_bf16_rne(acc[i][j][r]));
+            const int col = wn * 128 + j * 32 + g * 8 + (lane >> 5) * 4;
+            const bf16x4 v = {(__bf16)acc[i][j][4 * g], (__bf16)acc[i][j][4 * g + 1], (__bf16)acc[i][j][4 * g + 2],
+                              (__bf16)acc[i][j][4 * g + 3]};
+            *reinterpret_cast<lds_bf16x4 *>(sbase + row * kEpiRow + col * 2) = v;
           }
         }
       }
     }
-    wait_lds();  // this wave's LDS writes are done
+    wait_lds();
     barrier();
     const int64_t col0 = nt * kEpiCols;
     constexpr int kChunksPerRow = kEpiCols / 8;
@@ -354,7 +451,6 @@ __global__ __launch_bounds__(kWavesM * kWavesN * 64) void grouped_gemm_kernel(Ge
     }
   }
 }
-
 int g_num_cus[64] = {0};
 
 int num_cus() {
@@ -388,6 +484,12 @@ int moe_grouped_gemm(const moe_bf16_t *a, int64_t M_total, int64_t K, const moe_
   }
   if (G < 1 || G > 4096) return fail(MOE_ERR_CAPACITY, "moe_grouped_gemm: G=%lld outside [1, 4096]", (long long)G);
   if (K % 8 != 0 || K == 0) return fail(MOE_ERR_SHAPE, "moe_grouped_gemm: K=%lld must be a positive multiple of 8", (long long)K);
+  // 32-bit buffer offsets: a 256-row panel of a and one expert's w must each
+  // span less than 4 GiB.
+  if (K > (int64_t(1) << 23) - 8 || N * K > (int64_t(1) << 31) - 1) {
+    return fail(MOE_ERR_CAPACITY, "moe_grouped_gemm: K=%lld N=%lld exceed the 32-bit panel offsets (K < 2^23, N*K < 2^31)",
+                (long long)K, (long long)N);
+  }
   const bool swiglu = epilogue == MOE_EPILOGUE_SWIGLU;
   if (swiglu && (N % 2 != 0)) return fail(MOE_ERR_SHAPE, "moe_grouped_gemm: SWIGLU needs an even N (got %lld)", (long long)N);
   if (group_offsets == nullptr) return fail(MOE_ERR_INVALID_ARG, "moe_grouped_gemm: null group_offsets");
@@ -417,10 +519,8 @@ int moe_grouped_gemm(const moe_bf16_t *a, int64_t M_total, int64_t K, const moe_
   int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
   grid = std::max<int64_t>(8, (grid + 7) / 8 * 8);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  constexpr int kWN = MOE_GEMM_WAVES_N;
-  constexpr int kThreads = kWavesM * kWN * 64;
-  if (swiglu) grouped_gemm_kernel<true, kWN><<<dim3(grid), dim3(kThreads), 0, s>>>(p);
-  else grouped_gemm_kernel<false, kWN><<<dim3(grid), dim3(kThreads), 0, s>>>(p);
+  if (swiglu) grouped_gemm_kernel<true><<<dim3(grid), dim3(256), 0, s>>>(p);
+  else grouped_gemm_kernel<false><<<dim3(grid), dim3(256), 0, s>>>(p);
   return check_launch("moe_grouped_gemm");
 }
 
