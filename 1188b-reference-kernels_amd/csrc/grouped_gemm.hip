@@ -33,15 +33,20 @@
 //     output columns, so the epilogue combines them in registers
 //     (silu(g) = g / (1 + 2^(-g log2 e)) with the hardware exp2 and reciprocal);
 //   * tiles are numbered expert by expert, and inside an expert in groups of
-//     4 row tiles x all column tiles (row tile fastest), so 32 consecutive
-//     tile numbers form a 4 x 8 patch that shares A and B panels; workgroup b
+//     8 row tiles x all column tiles (row tile fastest), so 32 consecutive
+//     tile numbers form an 8 x 4 patch that shares A and B panels; workgroup b
 //     takes tile round * P + (b % 8) * (P / 8) + b / 8, which hands each XCD
 //     (workgroups are dealt round-robin to the 8 XCDs) one such patch per
 //     round, so the panels are reused from that XCD's L2.
 // Rows past a group's end and columns past N are loaded from a clamped (valid)
 // row and their results are discarded; a K tail (K % 64 != 0) is zeroed in LDS
-// before use. Buffer offsets are 32-bit: the host requires 512 K and 2 N K to
-// stay below 2^32 bytes.
+// before use. Buffer offsets are 32-bit and an out-of-range sentinel sits at
+// 2^31: the host requires 512 K, 2 N K (and for the gather 2 x_rows K) bytes to
+// stay below 2^31.
+//
+// Gather variant (moe_grouped_gemm_gather): A row p is x[a_rows[p]]; each
+// lane's DMA offset is that source row's, so the permuted A operand of fc1 is
+// read straight from the token rows and never materialised.
 #include <algorithm>
 
 #include "moe_common.h"
@@ -60,7 +65,7 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 
 constexpr int kBM = 256, kBN = 256, kBK = 64;
-constexpr int kGroupM = 4;                        // row tiles per tile-order group
+constexpr int kGroupM = 8;                        // row tiles per tile-order group
 constexpr int kRowBytes = kBK * 2;                // 128: one tile row in LDS
 constexpr int kChunks = kBK / 8;                  // 8 chunks of 16 bytes per row
 constexpr int kOperandBytes = 256 * kRowBytes;    // 32 KiB: one 256-row operand tile
@@ -70,7 +75,9 @@ constexpr int kRowsPerKiB = 1024 / kRowBytes;     // 8 rows per DMA instruction
 constexpr int kSubSteps = kBK / 16;               // MFMA K sub-steps per K step
 
 struct GemmArgs {
-  const uint16_t *a;
+  const uint16_t *a;       // A rows, or the gather source x [a_src_rows, K]
+  const int32_t *a_rows;   // gather: A row p = a[a_rows[p]] (nullptr: A row p = a[p])
+  int64_t a_src_rows;      // gather: rows of x
   const uint16_t *w;
   const int32_t *offsets;
   uint16_t *out;
@@ -109,8 +116,6 @@ __device__ __forceinline__ void wait_lds() {
   __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
   compiler_fence();
 }
-
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
 template <bool kSwiglu>
 __device__ __forceinline__ int64_t b_row_clamped(int64_t nt, int r, int64_t ncols, int64_t N) {
@@ -172,7 +177,7 @@ __device__ __forceinline__ void sched_pattern() {
 // fragments of step kt + 1 are read from LDS sub-step by sub-step. One barrier
 // per step, after the first sub-step's MFMAs, publishes stage kt + 1 (its DMA
 // has landed) and frees the LDS slot of stage kt for the DMA of stage kt + 2.
-template <bool kSwiglu>
+template <bool kSwiglu, bool kGather>
 __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
   constexpr int kWaves = 4;
   constexpr int kThreads = 256;
@@ -259,8 +264,11 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
     const int rows_valid = static_cast<int>(min(m_hi - row0, int64_t(kBM)));
     const uint16_t *wg = p.w + g_cur * p.N * K;
 
-    // Buffer resources: A over this tile's valid rows, B over this expert's matrix.
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + row0 * K, static_cast<uint32_t>(rows_valid * K * 2));
+    // Buffer resources: A over this tile's valid rows (gather: over all of x),
+    // B over this expert's matrix.
+    const __amdgpu_buffer_rsrc_t ra =
+        kGather ? make_rsrc(p.a, static_cast<uint32_t>(p.a_src_rows * K * 2))
+                : make_rsrc(p.a + row0 * K, static_cast<uint32_t>(rows_valid * K * 2));
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(wg, static_cast<uint32_t>(p.N * K * 2));
     int a_off[kDma], b_off[kDma];
 #pragma unroll
@@ -269,7 +277,15 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
       const int r = blk * kRowsPerKiB + dma_row;
       const int lchunk = dma_pchunk ^ swz(r);
       const uint32_t row_bytes = static_cast<uint32_t>(K) * 2u;
-      a_off[j] = static_cast<int>(static_cast<uint32_t>(min(r, rows_valid - 1)) * row_bytes + lchunk * 16);
+      if constexpr (kGather) {
+        // Source row of x; an index outside x points past the resource (zeros).
+        const int32_t src = p.a_rows[row0 + min(r, rows_valid - 1)];
+        a_off[j] = (src >= 0 && src < p.a_src_rows)
+                       ? static_cast<int>(static_cast<uint32_t>(src) * row_bytes + lchunk * 16)
+                       : static_cast<int>(0x80000000u);
+      } else {
+        a_off[j] = static_cast<int>(static_cast<uint32_t>(min(r, rows_valid - 1)) * row_bytes + lchunk * 16);
+      }
       b_off[j] = static_cast<int>(static_cast<uint32_t>(b_row_clamped<kSwiglu>(nt, r, p.ncols, p.N)) * row_bytes +
                                   lchunk * 16);
     }
@@ -467,42 +483,41 @@ int num_cus() {
 }  // namespace
 }  // namespace moe
 
-extern "C" {
+namespace {
 
-int moe_grouped_gemm(const moe_bf16_t *a, int64_t M_total, int64_t K, const moe_bf16_t *w, int64_t G,
-                     int64_t N, const int32_t *group_offsets, int epilogue, moe_bf16_t *out,
-                     void *workspace, size_t workspace_bytes, void *stream) {
+int launch_grouped_gemm(const char *fn, const moe_bf16_t *a, int64_t a_src_rows, const int32_t *a_rows,
+                        int64_t M_total, int64_t K, const moe_bf16_t *w, int64_t G, int64_t N,
+                        const int32_t *group_offsets, int epilogue, moe_bf16_t *out, void *stream) {
   using namespace moe;
-  (void)workspace;
-  (void)workspace_bytes;
-  if (M_total < 0 || K < 0 || N < 0 || G < 0) {
-    return fail(MOE_ERR_SHAPE, "moe_grouped_gemm: negative size (M=%lld K=%lld N=%lld G=%lld)",
-                (long long)M_total, (long long)K, (long long)N, (long long)G);
+  const bool gather = a_rows != nullptr;
+  if (M_total < 0 || K < 0 || N < 0 || G < 0 || a_src_rows < 0) {
+    return fail(MOE_ERR_SHAPE, "%s: negative size (M=%lld K=%lld N=%lld G=%lld)", fn, (long long)M_total,
+                (long long)K, (long long)N, (long long)G);
   }
   if (epilogue != MOE_EPILOGUE_NONE && epilogue != MOE_EPILOGUE_SWIGLU) {
-    return fail(MOE_ERR_INVALID_ARG, "moe_grouped_gemm: epilogue %d is not a moe_epilogue_t", epilogue);
+    return fail(MOE_ERR_INVALID_ARG, "%s: epilogue %d is not a moe_epilogue_t", fn, epilogue);
   }
-  if (G < 1 || G > 4096) return fail(MOE_ERR_CAPACITY, "moe_grouped_gemm: G=%lld outside [1, 4096]", (long long)G);
-  if (K % 8 != 0 || K == 0) return fail(MOE_ERR_SHAPE, "moe_grouped_gemm: K=%lld must be a positive multiple of 8", (long long)K);
-  // 32-bit buffer offsets: a 256-row panel of a and one expert's w must each
-  // span less than 4 GiB.
-  if (K > (int64_t(1) << 23) - 8 || N * K > (int64_t(1) << 31) - 1) {
-    return fail(MOE_ERR_CAPACITY, "moe_grouped_gemm: K=%lld N=%lld exceed the 32-bit panel offsets (K < 2^23, N*K < 2^31)",
-                (long long)K, (long long)N);
+  if (G < 1 || G > 4096) return fail(MOE_ERR_CAPACITY, "%s: G=%lld outside [1, 4096]", fn, (long long)G);
+  if (K % 8 != 0 || K == 0) return fail(MOE_ERR_SHAPE, "%s: K=%lld must be a positive multiple of 8", fn, (long long)K);
+  // 32-bit buffer offsets: a 256-row panel of a (gather: all of x) and one
+  // expert's w must each span less than 2 GiB.
+  if (K > (int64_t(1) << 22) - 8 || N * K > (int64_t(1) << 30) - 1 || (gather && a_src_rows * K > (int64_t(1) << 30) - 1)) {
+    return fail(MOE_ERR_CAPACITY,
+                "%s: K=%lld N=%lld (x rows %lld) exceed the 32-bit panel offsets (K < 2^22, N*K and x_rows*K < 2^30)",
+                fn, (long long)K, (long long)N, (long long)a_src_rows);
   }
   const bool swiglu = epilogue == MOE_EPILOGUE_SWIGLU;
-  if (swiglu && (N % 2 != 0)) return fail(MOE_ERR_SHAPE, "moe_grouped_gemm: SWIGLU needs an even N (got %lld)", (long long)N);
-  if (group_offsets == nullptr) return fail(MOE_ERR_INVALID_ARG, "moe_grouped_gemm: null group_offsets");
+  if (swiglu && (N % 2 != 0)) return fail(MOE_ERR_SHAPE, "%s: SWIGLU needs an even N (got %lld)", fn, (long long)N);
+  if (group_offsets == nullptr) return fail(MOE_ERR_INVALID_ARG, "%s: null group_offsets", fn);
   const int64_t ncols = swiglu ? N / 2 : N;
   if (M_total == 0 || ncols == 0) return MOE_OK;
-  if (a == nullptr || w == nullptr || out == nullptr) {
-    return fail(MOE_ERR_INVALID_ARG, "moe_grouped_gemm: null a, w or out");
-  }
-  if (!is_aligned(a, 16) || !is_aligned(w, 16)) {
-    return fail(MOE_ERR_ALIGN, "moe_grouped_gemm: a and w must be 16-byte aligned");
-  }
+  if (a == nullptr || w == nullptr || out == nullptr) return fail(MOE_ERR_INVALID_ARG, "%s: null a, w or out", fn);
+  if (gather && a_src_rows == 0) return fail(MOE_ERR_SHAPE, "%s: x has no rows", fn);
+  if (!is_aligned(a, 16) || !is_aligned(w, 16)) return fail(MOE_ERR_ALIGN, "%s: a and w must be 16-byte aligned", fn);
   GemmArgs p;
   p.a = a;
+  p.a_rows = a_rows;
+  p.a_src_rows = a_src_rows;
   p.w = w;
   p.offsets = group_offsets;
   p.out = out;
@@ -519,9 +534,39 @@ int moe_grouped_gemm(const moe_bf16_t *a, int64_t M_total, int64_t K, const moe_
   int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
   grid = std::max<int64_t>(8, (grid + 7) / 8 * 8);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (swiglu) grouped_gemm_kernel<true><<<dim3(grid), dim3(256), 0, s>>>(p);
-  else grouped_gemm_kernel<false><<<dim3(grid), dim3(256), 0, s>>>(p);
-  return check_launch("moe_grouped_gemm");
+  if (swiglu) {
+    if (gather) grouped_gemm_kernel<true, true><<<dim3(grid), dim3(256), 0, s>>>(p);
+    else grouped_gemm_kernel<true, false><<<dim3(grid), dim3(256), 0, s>>>(p);
+  } else {
+    if (gather) grouped_gemm_kernel<false, true><<<dim3(grid), dim3(256), 0, s>>>(p);
+    else grouped_gemm_kernel<false, false><<<dim3(grid), dim3(256), 0, s>>>(p);
+  }
+  return check_launch(fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_grouped_gemm(const moe_bf16_t *a, int64_t M_total, int64_t K, const moe_bf16_t *w, int64_t G,
+                     int64_t N, const int32_t *group_offsets, int epilogue, moe_bf16_t *out,
+                     void *workspace, size_t workspace_bytes, void *stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  return launch_grouped_gemm("moe_grouped_gemm", a, 0, nullptr, M_total, K, w, G, N, group_offsets, epilogue, out,
+                             stream);
+}
+
+int moe_grouped_gemm_gather(const moe_bf16_t *x, int64_t x_rows, const int32_t *a_rows, int64_t M_total,
+                            int64_t K, const moe_bf16_t *w, int64_t G, int64_t N, const int32_t *group_offsets,
+                            int epilogue, moe_bf16_t *out, void *workspace, size_t workspace_bytes, void *stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  if (a_rows == nullptr && M_total > 0) {
+    return moe::fail(MOE_ERR_INVALID_ARG, "moe_grouped_gemm_gather: null a_rows");
+  }
+  return launch_grouped_gemm("moe_grouped_gemm_gather", x, x_rows, a_rows, M_total, K, w, G, N, group_offsets,
+                             epilogue, out, stream);
 }
 
 }  // extern "C"

@@ -176,6 +176,27 @@ void launch_permute_2(const PermuteArgs &a, bool vec, int64_t grid, hipStream_t 
   }
 }
 
+// Source token of each permuted row: the inverse of the row-id map. One thread
+// per map entry (coalesced over the map in its own layout); entries outside
+// [0, num_out) are skipped.
+template <bool kI64>
+__global__ __launch_bounds__(256) void permute_index_kernel(const void *map, int64_t T, int64_t E, bool expert_major,
+                                                            int32_t *src_token, int64_t num_out) {
+  const int64_t n = T * E;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t row = load_idx<kI64>(map, i);
+    if (row >= 0 && row < num_out) src_token[row] = static_cast<int32_t>(expert_major ? i % T : i / E);
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_i32_kernel(int32_t *p, int64_t n, int32_t v) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    p[i] = v;
+  }
+}
+
 }  // namespace
 }  // namespace moe
 
@@ -250,6 +271,41 @@ int moe_permute(const moe_bf16_t *x, int64_t T, int64_t H, const void *row_id_ma
     return check_launch("moe_permute(zero tail)");
   }
   return MOE_OK;
+}
+
+int moe_permute_index(const void *row_id_map, int idx_dtype, int map_layout, int64_t T, int64_t E,
+                      int32_t *src_token, int64_t num_out, int fill, void *stream) {
+  using namespace moe;
+  if (T < 0 || E < 0 || num_out < 0) {
+    return fail(MOE_ERR_SHAPE, "moe_permute_index: negative size (T=%lld E=%lld num_out=%lld)", (long long)T,
+                (long long)E, (long long)num_out);
+  }
+  if (idx_dtype != MOE_IDX_I32 && idx_dtype != MOE_IDX_I64) {
+    return fail(MOE_ERR_INVALID_ARG, "moe_permute_index: idx_dtype %d is not MOE_IDX_I32/I64", idx_dtype);
+  }
+  if (map_layout != MOE_MAP_TOKEN_MAJOR && map_layout != MOE_MAP_EXPERT_MAJOR) {
+    return fail(MOE_ERR_INVALID_ARG, "moe_permute_index: map_layout %d is not a moe_map_layout_t", map_layout);
+  }
+  if (T > 0x7fffffff) return fail(MOE_ERR_CAPACITY, "moe_permute_index: T=%lld exceeds int32 tokens", (long long)T);
+  if ((T * E > 0 && row_id_map == nullptr) || (num_out > 0 && src_token == nullptr)) {
+    return fail(MOE_ERR_INVALID_ARG, "moe_permute_index: null row_id_map or src_token");
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (fill && num_out > 0) {
+    const int64_t grid = std::min<int64_t>(1024, ceil_div(num_out, 256));
+    moe::fill_i32_kernel<<<dim3(grid), dim3(256), 0, s>>>(src_token, num_out, -1);
+    const int st = check_launch("moe_permute_index");
+    if (st != MOE_OK) return st;
+  }
+  if (T * E == 0 || num_out == 0) return MOE_OK;
+  const int64_t grid = std::min<int64_t>(4096, ceil_div(T * E, 256));
+  const bool em = map_layout == MOE_MAP_EXPERT_MAJOR;
+  if (idx_dtype == MOE_IDX_I64) {
+    moe::permute_index_kernel<true><<<dim3(grid), dim3(256), 0, s>>>(row_id_map, T, E, em, src_token, num_out);
+  } else {
+    moe::permute_index_kernel<false><<<dim3(grid), dim3(256), 0, s>>>(row_id_map, T, E, em, src_token, num_out);
+  }
+  return check_launch("moe_permute_index");
 }
 
 }  // extern "C"

@@ -12,7 +12,10 @@ Data layout in HBM (T tokens, H hidden, F ffn, E experts, k top-k, R = T*k):
   probs    fp32 [T, E]        softmax over the k selected logits, 0 elsewhere
   row_map  int64 [T, E]       token-major destination row, -1 if unselected
   offsets  int32 [E + 1]      first permuted row of each expert; offsets[E] = R
-  xp       bf16 [R, H]        permuted rows, expert-major (expert e = rows offsets[e]..)
+  src      int32 [R]          source token of each permuted row (inverse of row_map)
+  xp       bf16 [R, H]        permuted rows x[src], expert-major (expert e = rows offsets[e]..);
+                              only materialised with fused_permute=False — by default fc1
+                              gathers its A rows from x through src (moe_grouped_gemm_gather)
   h        bf16 [R, F]        silu(xp @ W1_gate^T) * (xp @ W1_up^T)
   z        bf16 [R, H]        h @ W2^T
   out      bf16 [T, H]        sum_e probs[t, e] * z[row_map[t, e]]  (fp32, ascending e)
@@ -31,7 +34,7 @@ from . import ops
 class MoEFFN:
     """forward(x, logits) -> out for fixed weights W1 [E, 2F, H], W2 [E, H, F]."""
 
-    def __init__(self, w1: torch.Tensor, w2: torch.Tensor, topk: int):
+    def __init__(self, w1: torch.Tensor, w2: torch.Tensor, topk: int, *, fused_permute: bool = True):
         if w1.ndim != 3 or w2.ndim != 3:
             raise ValueError("w1 must be [E, 2F, H] and w2 [E, H, F]")
         E, F2, H = w1.shape
@@ -39,6 +42,7 @@ class MoEFFN:
             raise ValueError(f"w2 {tuple(w2.shape)} does not match w1 {tuple(w1.shape)}")
         self.w1, self.w2 = w1, w2
         self.E, self.H, self.F, self.k = E, H, F2 // 2, topk
+        self.fused_permute = fused_permute
         self._bufs = None
         self.last = {}
 
@@ -48,7 +52,8 @@ class MoEFFN:
             bf = dict(dtype=torch.bfloat16, device=device)
             self._bufs = {
                 "T": T,
-                "xp": torch.empty(R, self.H, **bf),
+                "xp": None if self.fused_permute else torch.empty(R, self.H, **bf),
+                "src": torch.empty(R, dtype=torch.int32, device=device),
                 "h": torch.empty(R, self.F, **bf),
                 "z": torch.empty(R, self.H, **bf),
                 "out": torch.empty(T, self.H, **bf),
@@ -70,8 +75,13 @@ class MoEFFN:
             raise ValueError(f"logits {tuple(logits.shape)} expected {(T, self.E)}")
         b = self._buffers(T, x.device)
         mask, probs, row_map, offsets = self.route(logits)
-        ops.permute(x, row_map, num_out=T * self.k, layout=ops.TOKEN_MAJOR, zero_tail=False, out=b["xp"])
-        ops.grouped_gemm(b["xp"], self.w1, offsets, swiglu=True, out=b["h"])
+        if self.fused_permute:
+            # every permuted row is named by the map (R = T * k), so no -1 fill is needed
+            ops.permute_index(row_map, T * self.k, layout=ops.TOKEN_MAJOR, fill=False, out=b["src"])
+            ops.grouped_gemm_gather(x, b["src"], self.w1, offsets, swiglu=True, out=b["h"])
+        else:
+            ops.permute(x, row_map, num_out=T * self.k, layout=ops.TOKEN_MAJOR, zero_tail=False, out=b["xp"])
+            ops.grouped_gemm(b["xp"], self.w1, offsets, swiglu=True, out=b["h"])
         ops.grouped_gemm(b["h"], self.w2, offsets, out=b["z"])
         ops.unpermute(b["z"], row_map, probs, layout=ops.TOKEN_MAJOR, out=b["out"])
         self.last = {"mask": mask, "probs": probs, "row_map": row_map, "offsets": offsets}

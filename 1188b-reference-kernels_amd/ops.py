@@ -267,3 +267,54 @@ def grouped_gemm(a: torch.Tensor, w: torch.Tensor, group_offsets: torch.Tensor, 
     call("moe_grouped_gemm", ptr(ac), M, K, ptr(wc), G, N, ptr(oc),
          MOE_EPILOGUE_SWIGLU if swiglu else MOE_EPILOGUE_NONE, ptr(out), None, 0, stream_handle())
     return out
+
+
+def permute_index(row_id_map: torch.Tensor, num_out: int, *, layout: str = TOKEN_MAJOR, fill: bool = True,
+                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Source token of each permuted row: out[map(t, e)] = t (int32 [num_out]).
+
+    The inverse of a row-id map; with fill, rows that no map entry names are -1.
+    """
+    _on_gpu("row_id_map", row_id_map)
+    _dtype("row_id_map", row_id_map, torch.int32, torch.int64)
+    T, E = _map_dims(row_id_map, layout)
+    if num_out < 0:
+        raise ValueError(f"num_out must be >= 0, got {num_out}")
+    if out is None:
+        out = torch.empty(num_out, dtype=torch.int32, device=row_id_map.device)
+    elif out.dtype != torch.int32 or out.numel() < num_out or not out.is_contiguous():
+        raise ValueError("out must be a contiguous int32 tensor of at least num_out elements")
+    m = row_id_map.contiguous()
+    call("moe_permute_index", ptr(m), _IDX[m.dtype], _LAYOUTS[layout], T, E, ptr(out), num_out, int(fill),
+         stream_handle())
+    return out
+
+
+def grouped_gemm_gather(x: torch.Tensor, a_rows: torch.Tensor, w: torch.Tensor, group_offsets: torch.Tensor, *,
+                        swiglu: bool = False, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """grouped_gemm(x[a_rows], w, group_offsets) without materialising x[a_rows].
+
+    x bf16 [X, K]; a_rows int32 [M] (an index outside [0, X) reads a zero row).
+    """
+    _on_gpu("x", x)
+    _on_gpu("a_rows", a_rows)
+    _on_gpu("w", w)
+    _on_gpu("group_offsets", group_offsets)
+    _dtype("x", x, torch.bfloat16)
+    _dtype("a_rows", a_rows, torch.int32)
+    _dtype("w", w, torch.bfloat16)
+    _dtype("group_offsets", group_offsets, torch.int32)
+    if x.ndim != 2 or w.ndim != 3 or x.shape[1] != w.shape[2] or a_rows.ndim != 1:
+        raise ValueError(f"shapes x {tuple(x.shape)} a_rows {tuple(a_rows.shape)} w {tuple(w.shape)}: "
+                         "need x [X,K], a_rows [M], w [G,N,K]")
+    G, N, K = w.shape
+    if group_offsets.shape != (G + 1,):
+        raise ValueError(f"group_offsets {tuple(group_offsets.shape)} expected ({G + 1},)")
+    M = a_rows.shape[0]
+    xc, rc, wc, oc = x.contiguous(), a_rows.contiguous(), w.contiguous(), group_offsets.contiguous()
+    ncols = N // 2 if swiglu else N
+    if out is None:
+        out = torch.empty(M, ncols, dtype=torch.bfloat16, device=x.device)
+    call("moe_grouped_gemm_gather", ptr(xc), x.shape[0], ptr(rc), M, K, ptr(wc), G, N, ptr(oc),
+         MOE_EPILOGUE_SWIGLU if swiglu else MOE_EPILOGUE_NONE, ptr(out), None, 0, stream_handle())
+    return out

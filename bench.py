@@ -8,8 +8,11 @@ weights resident in HBM): T=16384 tokens, hidden H=7168, ffn F=2048, E=64
 experts, top-8 routing of N(0,1) logits plus a per-expert N(0, 1.5) skew;
 bf16 activations ~ N(0,1), bf16 weights ~ N(0, 0.02).  Stages, all HIP
 kernels of this repository on torch's current stream:
-  top-k + mask + merge probs -> row-id map -> permute -> fc1 + SwiGLU
-  (grouped GEMM) -> fc2 (grouped GEMM) -> merge unpermute.
+  top-k + mask + merge probs -> row-id map -> permuted-row source index ->
+  fc1 + SwiGLU (grouped GEMM gathering its A rows from x, i.e. the permute
+  fused into fc1) -> fc2 (grouped GEMM) -> merge unpermute.
+The stand-alone permute kernel (x -> permuted rows) is timed separately on the
+same map, after the timed steps, and reported under "standalone".
 
 Prints ONE JSON line: tokens/s of the whole step, per-stage device times
 (HIP events on the launch stream, averaged over the timed steps) with their
@@ -49,7 +52,9 @@ def stage_work(T, H, F, E, k):
         "topk": ("GB/s", 4 * T * E + 12 * T * k + T * E + 4 * T * E),
         # mask [T,E] u8 in; token-major int64 map [T,E] + offsets out
         "row_id_map": ("GB/s", T * E + 8 * T * E + 4 * (E + 1)),
-        # x [T,H] bf16 + map [T,E] int64 in; permuted rows [R,H] bf16 out
+        # map [T,E] int64 in; source token per permuted row int32 [R] out
+        "permute_index": ("GB/s", 8 * T * E + 4 * R),
+        # x [T,H] bf16 + map [T,E] int64 in; permuted rows [R,H] bf16 out (stand-alone)
         "permute": ("GB/s", 2 * T * H + 8 * T * E + 2 * R * H),
         "fc1_swiglu": ("TFLOP/s", 2 * R * H * (2 * F)),
         "fc2": ("TFLOP/s", 2 * R * F * H),
@@ -140,7 +145,7 @@ def main():
     layer = pkg.moe_ffn.MoEFFN(w1, w2, k)
     ops = pkg.ops
 
-    names = ["topk", "row_id_map", "permute", "fc1_swiglu", "fc2", "unpermute_merge"]
+    names = ["topk", "row_id_map", "permute_index", "fc1_swiglu", "fc2", "unpermute_merge"]
 
     def step(ev=None):
         b = layer._buffers(T, dev)
@@ -151,9 +156,9 @@ def main():
         maps = ops.row_id_map(mask, expert_major=False, token_major=True, expert_offsets=True, workspace=b["ws"])
         row_map, offs = maps["token_major"], maps["expert_offsets"]
         rec(2)
-        ops.permute(x, row_map, num_out=T * k, layout=ops.TOKEN_MAJOR, zero_tail=False, out=b["xp"])
+        ops.permute_index(row_map, T * k, layout=ops.TOKEN_MAJOR, fill=False, out=b["src"])
         rec(3)
-        ops.grouped_gemm(b["xp"], w1, offs, swiglu=True, out=b["h"])
+        ops.grouped_gemm_gather(x, b["src"], w1, offs, swiglu=True, out=b["h"])
         rec(4)
         ops.grouped_gemm(b["h"], w2, offs, out=b["z"])
         rec(5)
@@ -183,8 +188,25 @@ def main():
         stages[n] = {"ms": round(ms, 4), unit: round(rate, 2), "frac_of_peak": round(rate / peak, 4),
                      ("bytes" if unit == "GB/s" else "flops"): amount}
 
+    # Stand-alone permute (the unfused path's first kernel) on this step's map.
+    _, _, row_map, _ = layer.route(logits)
+    xp = torch.empty(T * k, H, dtype=torch.bfloat16, device=dev)
+    pev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    for _ in range(2):
+        ops.permute(x, row_map, num_out=T * k, layout=ops.TOKEN_MAJOR, zero_tail=False, out=xp)
+    pev[0].record()
+    for _ in range(5):
+        ops.permute(x, row_map, num_out=T * k, layout=ops.TOKEN_MAJOR, zero_tail=False, out=xp)
+    pev[1].record()
+    torch.cuda.synchronize()
+    pms = pev[0].elapsed_time(pev[1]) / 5
+    pbytes = work["permute"][1]
+    standalone = {"permute": {"ms": round(pms, 4), "GB/s": round(pbytes / (pms * 1e-3) / 1e9, 2),
+                              "frac_of_peak": round(pbytes / (pms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": pbytes}}
+    del xp
+
     fc1 = stages["fc1_swiglu"]
-    roofline = {"kernel": "grouped_gemm_kernel<swiglu> (fc1 + SwiGLU)", "bound": "mfma",
+    roofline = {"kernel": "grouped_gemm_kernel<swiglu, gather> (fc1 + SwiGLU)", "bound": "mfma",
                 "achieved": fc1["TFLOP/s"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(fc1["TFLOP/s"] / BF16_PEAK_TFLOPS, 4), "traffic": None,
                 "flops_per_launch": fc1["flops"], "avg_launch_ms": fc1["ms"]}
@@ -223,6 +245,7 @@ def main():
         "config": {"workload": "c5: MoE FFN forward, T=16384 H=7168 F=2048 E=64 top-8, one GPU",
                    "tokens": T, "hidden": H, "ffn": F, "experts": E, "topk": k, "routed_rows": T * k},
         "stages": stages,
+        "standalone": standalone,
         "roofline": roofline,
         "cpu_baseline": cpu,
         "device": torch.cuda.get_device_name(0),

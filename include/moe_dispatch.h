@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define MOE_DISPATCH_ABI_VERSION 1
+#define MOE_DISPATCH_ABI_VERSION 2
 
 typedef uint16_t moe_bf16_t;
 
@@ -134,6 +134,18 @@ int moe_permute(const moe_bf16_t *x, int64_t T, int64_t H, const void *row_id_ma
                 float *permuted_probs, int64_t num_out, int zero_tail, void *workspace,
                 size_t workspace_bytes, void *stream);
 
+/* ---- a4': source token of each permuted row (inverse row-id map) -------
+ * No function of its own in the reference: the token index that the permute
+ * (case17 kernel_function, kernel_results/case17_moe_permute_with_mask_map/
+ * binding.cpp; math kernel_cases/case17_moe_permute_with_mask_map.py) copies
+ * into each permuted row, i.e. the inverse of the row-id map built by
+ * kernel_cases/case12_moe_row_id_map_pass2.py:
+ *   src_token[map(t, e)] = t  for every map(t, e) in [0, num_out);
+ *   fill != 0: every row is first set to -1, so rows no map entry names stay -1.
+ * Feeds moe_grouped_gemm_gather, which then reads permuted rows straight from x. */
+int moe_permute_index(const void *row_id_map, int idx_dtype, int map_layout, int64_t T, int64_t E,
+                      int32_t *src_token, int64_t num_out, int fill, void *stream);
+
 /* ---- a8: unpermute (combine), optional probability-weighted merge ------
  * Replaces case15 kernel_function(pin, row_id_map) -> out
  * (kernel_results/case15_moe_unpermute_mask_fwd/binding.cpp:10-20; math
@@ -185,11 +197,24 @@ int moe_index_select(const moe_bf16_t *src, int64_t src_rows, int64_t row_elems,
  *   out bf16 [M_total, N] (MOE_EPILOGUE_NONE) or [M_total, N / 2] (SWIGLU:
  *       gate = columns [0, N/2), up = [N/2, N); silu(g) = g / (1 + exp(-g)),
  *       computed in fp32 on the fp32 accumulators, then one bf16 rounding).
- * Limits: K % 8 == 0, N % 2 == 0 (SWIGLU: (N/2) % 8 == 0), 1 <= G <= 4096.
+ * Limits: K % 8 == 0, N % 2 == 0 (SWIGLU), 1 <= G <= 4096, K < 2^22, N * K < 2^30.
  * Workspace: none (pass NULL, 0). */
 int moe_grouped_gemm(const moe_bf16_t *a, int64_t M_total, int64_t K, const moe_bf16_t *w,
                      int64_t G, int64_t N, const int32_t *group_offsets, int epilogue,
                      moe_bf16_t *out, void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---- a4+a6: permute fused into the grouped GEMM's A operand --------------
+ * Replaces the composition permute (case17 kernel_function, see moe_permute)
+ * followed by the fc1 grouped GEMM (case03 Model.forward, see
+ * moe_grouped_gemm) when the permuted activations are only the GEMM's input:
+ *   out = moe_grouped_gemm(a = x[a_rows], ...)
+ *   x bf16 [x_rows, K]; a_rows int32 [M_total] (moe_permute_index output):
+ *   row p of the GEMM is x[a_rows[p]]; an index outside [0, x_rows) reads zeros.
+ * Other arguments, results and limits as moe_grouped_gemm. */
+int moe_grouped_gemm_gather(const moe_bf16_t *x, int64_t x_rows, const int32_t *a_rows,
+                            int64_t M_total, int64_t K, const moe_bf16_t *w, int64_t G, int64_t N,
+                            const int32_t *group_offsets, int epilogue, moe_bf16_t *out,
+                            void *workspace, size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

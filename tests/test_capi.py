@@ -17,7 +17,7 @@ L = pkg._lib
 def test_library_loads_and_exports_header_symbols():
     lib = L.lib()
     declared = L.header_functions()
-    assert len(declared) == len(L.SIGNATURES) == 12
+    assert len(declared) == len(L.SIGNATURES) == 14
     assert set(declared) == set(L.SIGNATURES)
     for name in declared:
         assert hasattr(lib, name), name
@@ -67,6 +67,17 @@ FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
     ("moe_grouped_gemm", (FAKE, 4, 16, FAKE, 1, 8, FAKE, 9, FAKE, None, 0, None), L.MOE_ERR_INVALID_ARG, "epilogue"),
     ("moe_grouped_gemm", (FAKE, 4, 16, FAKE, 1, 8, None, 0, FAKE, None, 0, None), L.MOE_ERR_INVALID_ARG, "group_offsets"),
     ("moe_grouped_gemm", (ctypes.c_void_p(0x1002), 4, 16, FAKE, 1, 8, FAKE, 0, FAKE, None, 0, None), L.MOE_ERR_ALIGN, "aligned"),
+    ("moe_grouped_gemm", (FAKE, 4, 1 << 22, FAKE, 1, 8, FAKE, 0, FAKE, None, 0, None), L.MOE_ERR_CAPACITY, "32-bit"),
+    ("moe_grouped_gemm", (FAKE, 4, 8192, FAKE, 1, 1 << 17, FAKE, 0, FAKE, None, 0, None), L.MOE_ERR_CAPACITY, "32-bit"),
+    ("moe_grouped_gemm_gather", (FAKE, 8, None, 4, 16, FAKE, 1, 8, FAKE, 0, FAKE, None, 0, None), L.MOE_ERR_INVALID_ARG, "a_rows"),
+    ("moe_grouped_gemm_gather", (FAKE, 1 << 27, FAKE, 4, 16, FAKE, 1, 8, FAKE, 0, FAKE, None, 0, None), L.MOE_ERR_CAPACITY, "x rows"),
+    ("moe_grouped_gemm_gather", (FAKE, 0, FAKE, 4, 16, FAKE, 1, 8, FAKE, 0, FAKE, None, 0, None), L.MOE_ERR_SHAPE, "no rows"),
+    ("moe_grouped_gemm_gather", (FAKE, 8, FAKE, 4, 12, FAKE, 1, 8, FAKE, 0, FAKE, None, 0, None), L.MOE_ERR_SHAPE, "multiple of 8"),
+    ("moe_permute_index", (FAKE, 3, 0, 4, 8, FAKE, 32, 1, None), L.MOE_ERR_INVALID_ARG, "idx_dtype"),
+    ("moe_permute_index", (FAKE, 1, 2, 4, 8, FAKE, 32, 1, None), L.MOE_ERR_INVALID_ARG, "map_layout"),
+    ("moe_permute_index", (None, 1, 0, 4, 8, FAKE, 32, 1, None), L.MOE_ERR_INVALID_ARG, "null"),
+    ("moe_permute_index", (FAKE, 1, 0, -4, 8, FAKE, 32, 1, None), L.MOE_ERR_SHAPE, "negative"),
+    ("moe_permute_index", (FAKE, 1, 0, 1 << 31, 8, FAKE, 32, 1, None), L.MOE_ERR_CAPACITY, "int32"),
 ])
 def test_argument_validation(name, args, code, needle):
     st, msg = _status(name, *args)
@@ -81,6 +92,8 @@ def test_empty_problems_are_no_ops():
     assert _status("moe_topk", None, 0, 16, 4, None, None, None, None, None)[0] == 0
     assert _status("moe_index_select", None, 0, 8, None, 1, 0, None, None)[0] == 0
     assert _status("moe_grouped_gemm", None, 0, 16, None, 1, 8, FAKE, 0, None, None, 0, None)[0] == 0
+    assert _status("moe_grouped_gemm_gather", None, 4, None, 0, 16, None, 1, 8, FAKE, 0, None, None, 0, None)[0] == 0
+    assert _status("moe_permute_index", None, 1, 0, 0, 8, None, 0, 1, None)[0] == 0
 
 
 def test_workspace_sizes():
