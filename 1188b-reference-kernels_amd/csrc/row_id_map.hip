@@ -7,16 +7,19 @@
 // expert 1's, ...  The same construction appears in case15/17/18/21/22/24/30/32.
 //
 // Three launches, all integer work on a mask of T*E bytes:
-//   1. count: block = one 64-token chunk; per-expert popcounts of the chunk
-//      (wave ballots over 64 tokens) -> counts[chunk][e].
-//   2. scan (one workgroup): column-wise exclusive scan of counts over chunks,
-//      exclusive scan of the per-expert totals over experts; rewrites counts
-//      in place as the global base row of (chunk, expert) and emits
-//      expert_offsets[0..E].
-//   3. fill: block = one 64-token chunk; the mask tile goes through LDS, each
-//      wave ranks 64 tokens of one expert with ballot + mbcnt and writes the
-//      expert-major rows directly (512 contiguous bytes per wave store) and
-//      the token-major rows through an LDS transpose.
+//   1. count: block = one 64-token chunk; the chunk's mask tile is loaded into
+//      LDS with 16-byte vector loads (one per thread at E = 64), then
+//      per-expert popcounts (wave ballots over 64 tokens) -> counts[chunk][e].
+//   2. scan (one workgroup): per-expert sums over runs of chunks (loads issued
+//      in batches of 8), exclusive scans over the runs and over the experts'
+//      totals, then counts are rewritten in place as the global base row of
+//      (chunk, expert) and expert_offsets[0..E] is emitted.
+//   3. fill: block = one 64-token chunk; mask tile and the chunk's E bases go
+//      through LDS, each wave ranks 64 tokens of one expert with ballot +
+//      mbcnt and writes the expert-major rows directly (512 contiguous bytes
+//      per wave store) and the token-major rows through an LDS transpose.
+// Every global load of a thread is independent of its other loads, so a block
+// waits for memory about once per phase rather than once per element.
 #include "moe_common.h"
 
 namespace moe {
@@ -34,7 +37,23 @@ constexpr int kMaxE = 4096;
 constexpr int kTileStride = kEG + 4;
 
 __device__ __forceinline__ void load_mask_tile(uint8_t *tile, const uint8_t *mask, int64_t T,
-                                               int64_t E, int64_t t0, int64_t eg0, int eg_n) {
+                                               int64_t E, int64_t t0, int64_t eg0, int eg_n, bool vec) {
+  if (vec) {
+    // 16 mask bytes per thread (E % 16 == 0, 16-byte aligned mask), stored as
+    // four dwords (the tile row stride is a multiple of 4 bytes).
+    const int nv = eg_n / 16;
+    for (int i = threadIdx.x; i < kChunk * nv; i += kThreads) {
+      const int r = i / nv, q = i % nv;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (t0 + r < T) v = *reinterpret_cast<const u32x4 *>(mask + (t0 + r) * E + eg0 + q * 16);
+      uint32_t *dst = reinterpret_cast<uint32_t *>(tile + r * kTileStride + q * 16);
+      dst[0] = v.x;
+      dst[1] = v.y;
+      dst[2] = v.z;
+      dst[3] = v.w;
+    }
+    return;
+  }
   for (int i = threadIdx.x; i < kChunk * kEG; i += kThreads) {
     const int r = i / kEG, c = i % kEG;
     uint8_t v = 0;
@@ -48,15 +67,15 @@ __global__ __launch_bounds__(kThreads) void rim_zero_kernel(int32_t *p, int64_t 
 }
 
 __global__ __launch_bounds__(kThreads) void rim_count_kernel(const uint8_t *mask, int64_t T,
-                                                             int64_t E, int32_t *counts) {
-  __shared__ uint8_t tile[kChunk * kTileStride];
+                                                             int64_t E, int32_t *counts, bool vec) {
+  __shared__ __attribute__((aligned(16))) uint8_t tile[kChunk * kTileStride];
   const int64_t chunk = blockIdx.x;
   const int64_t t0 = chunk * kChunk;
   const int lane = lane_id(), wave = threadIdx.x / kWave;
   for (int64_t eg0 = 0; eg0 < E; eg0 += kEG) {
     const int eg_n = static_cast<int>(E - eg0 < kEG ? E - eg0 : kEG);
     __syncthreads();
-    load_mask_tile(tile, mask, T, E, t0, eg0, eg_n);
+    load_mask_tile(tile, mask, T, E, t0, eg0, eg_n, vec);
     __syncthreads();
     for (int c = wave; c < eg_n; c += kWaves) {
       const uint64_t m = __ballot(tile[lane * kTileStride + c] != 0);
@@ -99,25 +118,32 @@ __global__ __launch_bounds__(kScanThreads) void rim_scan_kernel(int32_t *counts,
   __shared__ int64_t totals[kMaxE];
   __shared__ int64_t wave_sums[kScanThreads / kWave];
   __shared__ int64_t grand_total;
-  // Column scans: threads = parts x experts; each part owns a run of chunks.
+  __shared__ int64_t part_sums[kScanThreads];
+  constexpr int kBatch = 8;
+  // Threads = parts x experts; each part owns a run of `per` chunks of one expert.
   const int64_t parts = E >= kScanThreads ? 1 : kScanThreads / E;
   const int64_t per = ceil_div(nc, parts);
-  __shared__ int64_t part_sums[kScanThreads];
+  // Pass 1: per-part sums, then exclusive scans over parts (per expert) -> totals.
   for (int64_t e0 = 0; e0 < E; e0 += kScanThreads) {
     const int64_t lin = threadIdx.x;
     const int64_t e = e0 + (parts > 1 ? lin % E : lin);
     const int64_t p = parts > 1 ? lin / E : 0;
     const bool active = e < E && p < parts;
-    int64_t s = 0;
+    int64_t sum = 0;
     if (active) {
       const int64_t c_begin = p * per, c_end = c_begin + per < nc ? c_begin + per : nc;
-      for (int64_t c = c_begin; c < c_end; ++c) s += counts[c * E + e];
+      for (int64_t c = c_begin; c < c_end; c += kBatch) {
+        int32_t v[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) v[j] = c + j < c_end ? counts[(c + j) * E + e] : 0;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) sum += v[j];
+      }
     }
     __syncthreads();
-    part_sums[threadIdx.x] = s;
+    part_sums[threadIdx.x] = sum;
     __syncthreads();
     if (active && p == 0) {
-      // Serial exclusive scan over the parts of expert e (parts <= 1024 / E).
       int64_t run = 0;
       for (int64_t q = 0; q < parts; ++q) {
         const int64_t idx = parts > 1 ? q * E + (e - e0) : threadIdx.x;
@@ -127,20 +153,12 @@ __global__ __launch_bounds__(kScanThreads) void rim_scan_kernel(int32_t *counts,
       }
       totals[e] = run;
     }
-    __syncthreads();
-    if (active) {
-      // Rewrite counts[c][e] for this part's chunks as the exclusive prefix.
-      int64_t run = part_sums[threadIdx.x];
-      const int64_t c_begin = p * per, c_end = c_begin + per < nc ? c_begin + per : nc;
-      for (int64_t c = c_begin; c < c_end; ++c) {
-        const int32_t v = counts[c * E + e];
-        counts[c * E + e] = static_cast<int32_t>(run);
-        run += v;
-      }
-    }
+    // With E < kScanThreads there is one sweep and part_sums keeps each part's
+    // exclusive prefix for pass 2; with E >= kScanThreads every part starts at
+    // chunk 0 (prefix 0).
     __syncthreads();
   }
-  // Exclusive scan of totals over experts: each thread owns a run of experts.
+  // Exclusive scan of totals over experts -> offsets (in totals).
   const int64_t per_e = ceil_div(E, kScanThreads);
   const int64_t eb = threadIdx.x * per_e;
   int64_t local = 0;
@@ -156,31 +174,51 @@ __global__ __launch_bounds__(kScanThreads) void rim_scan_kernel(int32_t *counts,
     for (int64_t e = threadIdx.x; e < E; e += kScanThreads) expert_offsets[e] = static_cast<int32_t>(totals[e]);
     if (threadIdx.x == 0) expert_offsets[E] = static_cast<int32_t>(grand_total);
   }
-  // Add each expert's offset to its column of chunk bases.
-  for (int64_t i = threadIdx.x; i < nc * E; i += kScanThreads) {
-    counts[i] += static_cast<int32_t>(totals[i % E]);
+  // Pass 2: rewrite counts as base rows = offset[e] + prefix over earlier chunks.
+  for (int64_t e0 = 0; e0 < E; e0 += kScanThreads) {
+    const int64_t lin = threadIdx.x;
+    const int64_t e = e0 + (parts > 1 ? lin % E : lin);
+    const int64_t p = parts > 1 ? lin / E : 0;
+    const bool active = e < E && p < parts;
+    if (active) {
+      int64_t run = totals[e] + (parts > 1 ? part_sums[threadIdx.x] : 0);
+      const int64_t c_begin = p * per, c_end = c_begin + per < nc ? c_begin + per : nc;
+      for (int64_t c = c_begin; c < c_end; c += kBatch) {
+        int32_t v[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) v[j] = c + j < c_end ? counts[(c + j) * E + e] : 0;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          if (c + j < c_end) counts[(c + j) * E + e] = static_cast<int32_t>(run);
+          run += v[j];
+        }
+      }
+    }
   }
 }
 
 __global__ __launch_bounds__(kThreads) void rim_fill_kernel(const uint8_t *mask, int64_t T, int64_t E,
                                                             const int32_t *base, int64_t *row_em,
-                                                            int64_t *row_tm, int32_t *row_em32) {
-  __shared__ uint8_t tile[kChunk * kTileStride];
+                                                            int64_t *row_tm, int32_t *row_em32, bool vec) {
+  __shared__ __attribute__((aligned(16))) uint8_t tile[kChunk * kTileStride];
   __shared__ int32_t out_tile[kChunk * (kEG + 1)];
+  __shared__ int32_t s_base[kMaxE];
   const int64_t chunk = blockIdx.x;
   const int64_t t0 = chunk * kChunk;
   const int lane = lane_id(), wave = threadIdx.x / kWave;
   const int64_t t = t0 + lane;
+  // This chunk's base row per expert, read once (independent loads).
+  for (int64_t e = threadIdx.x; e < E; e += kThreads) s_base[e] = base[chunk * E + e];
   for (int64_t eg0 = 0; eg0 < E; eg0 += kEG) {
     const int eg_n = static_cast<int>(E - eg0 < kEG ? E - eg0 : kEG);
     __syncthreads();
-    load_mask_tile(tile, mask, T, E, t0, eg0, eg_n);
+    load_mask_tile(tile, mask, T, E, t0, eg0, eg_n, vec);
     __syncthreads();
     for (int c = wave; c < eg_n; c += kWaves) {
       const int64_t e = eg0 + c;
       const bool sel = tile[lane * kTileStride + c] != 0;
       const uint64_t m = __ballot(sel);
-      const int32_t b = base[chunk * E + e];
+      const int32_t b = s_base[e];
       const int32_t v = sel ? b + lanes_below(m) : -1;
       if (t < T) {
         if (row_em != nullptr) row_em[e * T + t] = v;
@@ -238,14 +276,15 @@ int moe_row_id_map(const uint8_t *routing_map, int64_t T, int64_t E, int64_t *ro
     }
     return MOE_OK;
   }
-  rim_count_kernel<<<dim3(nc), dim3(kThreads), 0, s>>>(routing_map, T, E, counts);
+  const bool vec = (E % 16 == 0) && is_aligned(routing_map, 16);
+  rim_count_kernel<<<dim3(nc), dim3(kThreads), 0, s>>>(routing_map, T, E, counts, vec);
   int st = check_launch("moe_row_id_map(count)");
   if (st != MOE_OK) return st;
   rim_scan_kernel<<<dim3(1), dim3(kScanThreads), 0, s>>>(counts, nc, E, expert_offsets);
   st = check_launch("moe_row_id_map(scan)");
   if (st != MOE_OK) return st;
   rim_fill_kernel<<<dim3(nc), dim3(kThreads), 0, s>>>(routing_map, T, E, counts, row_expert_major,
-                                                       row_token_major, row_expert_major_i32);
+                                                       row_token_major, row_expert_major_i32, vec);
   return check_launch("moe_row_id_map(fill)");
 }
 

@@ -29,6 +29,7 @@ def _mask(T, E, k=None, p=None, seed=0):
 @pytest.mark.parametrize("T,E,k,p", [
     (1, 1, 1, None), (63, 3, None, 0.5), (64, 8, 2, None), (65, 7, None, 0.3), (1000, 130, None, 0.04),
     (4096, 8, 2, None), (16384, 64, 8, None), (300, 5, None, 0.0), (257, 1024, None, 0.01),
+    (200, 48, 4, None), (70, 2000, None, 0.01), (33, 4096, None, 0.002), (5000, 160, 8, None),
 ])
 def test_row_id_map_matches_oracle(pkg, dev, T, E, k, p):
     rm = _mask(T, E, k, p, seed=T + E)
