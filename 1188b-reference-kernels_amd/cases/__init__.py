@@ -8,6 +8,10 @@ tuple and error behaviour, plus the case's seeded input generator
 this package.  Generated inputs are returned on `device` (default "cuda").
 """
 from . import (case03_moe_grouped_gemm_fc1_fwd, case04_moe_grouped_gemm_fc2_fwd,  # noqa: F401
+               case05_moe_grouped_gemm_fc2_wgrad, case07_moe_grouped_gemm_fc1_dgrad,
+               case08_moe_grouped_gemm_fc2_dgrad, case09_moe_grouped_gemm_fc1_wgrad,
+               case13_grouped_gemm_single_group_fc1_dgrad, case19_grouped_gemm_single_group_fc2_dgrad,
+               case37_ref_musa_asm_bf16_gemm_nn_256x384,
                case06_cp_seq_chunk_index_select, case12_moe_row_id_map_pass2,
                case15_moe_unpermute_mask_fwd, case17_moe_permute_with_mask_map,
                case18_moe_permute_bwd_unpermute_mask, case21_permute_with_mask_map_trans,
@@ -15,7 +19,10 @@ from . import (case03_moe_grouped_gemm_fc1_fwd, case04_moe_grouped_gemm_fc2_fwd,
                case24_moe_unpermute_mask_kernel_false, case30_moe_permute_mask_kernel,
                case32_moe_unpermute_mask_kernel)
 
-ALL = [case03_moe_grouped_gemm_fc1_fwd, case04_moe_grouped_gemm_fc2_fwd, case06_cp_seq_chunk_index_select,
+ALL = [case03_moe_grouped_gemm_fc1_fwd, case04_moe_grouped_gemm_fc2_fwd, case05_moe_grouped_gemm_fc2_wgrad,
+       case07_moe_grouped_gemm_fc1_dgrad, case08_moe_grouped_gemm_fc2_dgrad, case09_moe_grouped_gemm_fc1_wgrad,
+       case13_grouped_gemm_single_group_fc1_dgrad, case19_grouped_gemm_single_group_fc2_dgrad,
+       case37_ref_musa_asm_bf16_gemm_nn_256x384, case06_cp_seq_chunk_index_select,
        case12_moe_row_id_map_pass2, case15_moe_unpermute_mask_fwd, case17_moe_permute_with_mask_map,
        case18_moe_permute_bwd_unpermute_mask, case21_permute_with_mask_map_trans,
        case22_moe_permute_mask_kernel_true, case23_aten_topk, case24_moe_unpermute_mask_kernel_false,

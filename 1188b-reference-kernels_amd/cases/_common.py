@@ -29,3 +29,23 @@ def expert_major_map(selected_em: torch.Tensor, dtype=torch.int64, device="cuda"
 def check_scatter_shapes(inp: torch.Tensor, row_id_map: torch.Tensor) -> None:
     if row_id_map.ndim != 2 or inp.ndim != 2 or row_id_map.shape[1] != inp.shape[0]:
         raise ValueError(f"shapes inp {tuple(inp.shape)} row_id_map {tuple(row_id_map.shape)}")
+
+
+def _split_offsets(m_splits, total: int, groups: int, what: str, device):
+    if len(m_splits) != groups or sum(m_splits) != total:
+        raise ValueError(f"m_splits (len {len(m_splits)}, sum {sum(m_splits)}) does not match {what}")
+    return ops.group_offsets_from_splits(m_splits, device)
+
+
+def grouped_dgrad(dy: torch.Tensor, w: torch.Tensor, m_splits) -> torch.Tensor:
+    """cat_g(dy[seg_g] @ w[g]) for consecutive row segments of sizes m_splits."""
+    offsets = _split_offsets(m_splits, dy.shape[0], w.shape[0], f"dy {tuple(dy.shape)} and w {tuple(w.shape)}",
+                             dy.device)
+    return ops.grouped_gemm_dgrad(dy, w, offsets)
+
+
+def grouped_wgrad(dy: torch.Tensor, x: torch.Tensor, m_splits) -> torch.Tensor:
+    """stack_g(dy[seg_g].T @ x[seg_g]) for consecutive row segments of sizes m_splits."""
+    offsets = _split_offsets(m_splits, dy.shape[0], len(m_splits), f"dy {tuple(dy.shape)} and x {tuple(x.shape)}",
+                             dy.device)
+    return ops.grouped_gemm_wgrad(dy, x, offsets)

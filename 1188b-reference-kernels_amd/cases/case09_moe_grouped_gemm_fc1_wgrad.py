@@ -1,0 +1,60 @@
+"""case09 moe_grouped_gemm_fc1_wgrad on gfx950.
+
+The case has no optimized bundle; this is the drop-in for its Model
+(kernel_cases/case09_moe_grouped_gemm_fc1_wgrad.py:49-64):
+`Model(num_groups, tokens).forward(dy [T,N], x [T,K]) -> stack_g(dy[seg_g].T @ x[seg_g])`
+(the weight gradient of a grouped linear layer, layout "TN") with the uniform
+group_sizes of :43-46, plus `kernel_function(dy, x, m_splits=None, num_groups=None)`
+for ragged groups (a group without rows gets a zero gradient).  bf16 in /
+fp32 accumulate / bf16 out (:37).  The reference get_inputs (:71-73) is
+unseeded; get_inputs here takes a seed.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import inputs
+from ._common import grouped_wgrad
+
+NUM_GROUPS = 40
+TOKENS = 4096
+N = 5120
+K = 8192
+
+CASE = {"id": 9, "name": "moe_grouped_gemm_fc1_wgrad", "dtype": "bf16 in / fp32 accumulate / bf16 out",
+        "backward": False}
+
+
+def group_sizes(total, groups):
+    return inputs.uniform_group_sizes(total, groups)
+
+
+def kernel_function(dy, x, m_splits=None, num_groups=NUM_GROUPS):
+    """dw[g] = dy[seg_g].T @ x[seg_g] for consecutive row segments of sizes m_splits."""
+    if m_splits is None:
+        m_splits = group_sizes(dy.shape[0], num_groups)
+    return grouped_wgrad(dy, x, m_splits)
+
+
+class Model:
+    """Model(num_groups, tokens).forward(dy, x) with uniform group sizes."""
+
+    def __init__(self, num_groups=NUM_GROUPS, tokens=TOKENS):
+        self.num_groups = num_groups
+        self.sizes = group_sizes(tokens, num_groups)
+
+    def __call__(self, dy, x):
+        return kernel_function(dy, x, self.sizes)
+
+    forward = __call__
+
+
+def get_init_inputs():
+    return [NUM_GROUPS, TOKENS]
+
+
+def get_inputs(device="cuda", seed: int = inputs.SEED_CONFIG_BASE + 59, tokens: int = TOKENS, n: int = N, k: int = K):
+    g = torch.Generator().manual_seed(seed)
+    dy = torch.randn(tokens, n, generator=g).to(torch.bfloat16)
+    x = torch.randn(tokens, k, generator=g).to(torch.bfloat16)
+    return [dy.to(device), x.to(device)]

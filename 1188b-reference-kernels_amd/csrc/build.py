@@ -29,6 +29,7 @@ SOURCES = [
     "unpermute.hip",
     "index_select.hip",
     "grouped_gemm.hip",
+    "grouped_gemm_bwd.hip",
 ]
 
 ARCH = os.environ.get("MOE_OFFLOAD_ARCH", "gfx950")

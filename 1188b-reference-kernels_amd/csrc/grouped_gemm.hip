@@ -49,22 +49,14 @@
 // read straight from the token rows and never materialised.
 #include <algorithm>
 
-#include "moe_common.h"
+#include "gemm_device.h"
 
 namespace moe {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef __attribute__((address_space(3))) char lds_char;
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
-typedef __attribute__((address_space(3))) uint16_t lds_u16;
-typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+using namespace gemm;
 
-constexpr int kBM = 256, kBN = 256, kBK = 64;
+constexpr int kBM = 256, kBN = 256;
 constexpr int kGroupM = 8;                        // row tiles per tile-order group
 constexpr int kRowBytes = kBK * 2;                // 128: one tile row in LDS
 constexpr int kChunks = kBK / 8;                  // 8 chunks of 16 bytes per row
@@ -89,34 +81,6 @@ struct GemmArgs {
 
 __device__ __forceinline__ int swz(int row) { return (row >> 1) & (kChunks - 1); }
 
-// s_waitcnt immediates (gfx9 encoding: vmcnt [3:0],[15:14]; expcnt [6:4]; lgkmcnt [11:8]).
-constexpr int kWaitVm0 = 0x0f70;    // vmcnt(0)
-constexpr int kWaitLgkm0 = 0xc07f;  // lgkmcnt(0)
-
-__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
-
-// Workgroup barrier that neither the compiler nor the instruction scheduler
-// moves any instruction across.
-__device__ __forceinline__ void barrier() {
-  compiler_fence();
-  __builtin_amdgcn_sched_barrier(0);
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_sched_barrier(0);
-  compiler_fence();
-}
-
-// Waits for this thread's outstanding DMA (vector memory) or LDS operations.
-__device__ __forceinline__ void wait_dma() {
-  compiler_fence();
-  __builtin_amdgcn_s_waitcnt(kWaitVm0);
-  compiler_fence();
-}
-__device__ __forceinline__ void wait_lds() {
-  compiler_fence();
-  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-  compiler_fence();
-}
-
 template <bool kSwiglu>
 __device__ __forceinline__ int64_t b_row_clamped(int64_t nt, int r, int64_t ncols, int64_t N) {
   if constexpr (kSwiglu) {
@@ -128,48 +92,6 @@ __device__ __forceinline__ int64_t b_row_clamped(int64_t nt, int r, int64_t ncol
   }
 }
 
-
-// Buffer resource over [base, base + bytes): raw buffer loads past `bytes`
-// return zeros instead of touching memory.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
-}
-// 16-byte buffer -> LDS copy: lane i writes bytes [16 i, 16 i + 16) of the 1 KiB
-// block at `lds` (wave-uniform); the global address is rsrc base + voff + soff.
-__device__ __forceinline__ void dma16b(__amdgpu_buffer_rsrc_t rsrc, lds_void *lds, int voff, int soff) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds, 16, voff, soff, 0, 0);
-#else
-  (void)rsrc; (void)lds; (void)voff; (void)soff;
-#endif
-}
-template <int kN>
-__device__ __forceinline__ void wait_vm_n() {
-  compiler_fence();
-  __builtin_amdgcn_s_waitcnt((kN & 0xf) | ((kN >> 4) << 14) | (0x7 << 4) | (0xf << 8));
-  compiler_fence();
-}
-
-// Instruction-group order for one sub-step: each of the first 8 MFMAs followed
-// by one instruction of kind kFirst (0x100 LDS read, 0x020 vector-memory read),
-// each of the last 8 by one of kind kSecond (0 = none).
-template <int kFirst, int kSecond>
-__device__ __forceinline__ void sched_pattern() {
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kFirst, 1, 0);
-  }
-  if constexpr (kSecond != 0) {
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSecond, 1, 0);
-    }
-  } else {
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-  }
-}
 
 // Four wavefronts (one per SIMD), each 128 x 128 of the 256 x 256 tile as 4 x 4
 // blocks of 32 x 32. The operand fragments of a whole K step (4 sub-steps x 8
@@ -467,19 +389,6 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
     }
   }
 }
-int g_num_cus[64] = {0};
-
-int num_cus() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (g_num_cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    g_num_cus[dev] = n;
-  }
-  return g_num_cus[dev];
-}
-
 }  // namespace
 }  // namespace moe
 

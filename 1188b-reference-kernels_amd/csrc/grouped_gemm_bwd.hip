@@ -1,0 +1,547 @@
+// Grouped GEMM backward over ragged expert groups: input gradient (dgrad, "NN")
+// and weight gradient (wgrad, "TN"), bf16 MFMA with fp32 accumulate, bf16 out.
+//
+// Math (paths relative to the reference repository):
+//   dgrad  kernel_cases/case07_moe_grouped_gemm_fc1_dgrad.py:57-64 (= case08,
+//          case13, case19 :57-64; case37_ref_musa_asm_bf16_gemm_nn_256x384.py:47-49
+//          for one group):  dx[rows of g] = dy[rows of g] @ w[g]
+//          dy [M, N], w [G, N, K] -> dx [M, K]
+//   wgrad  kernel_cases/case09_moe_grouped_gemm_fc1_wgrad.py:57-64 (= case05
+//          :57-64):  dw[g] = dy[rows of g]^T @ x[rows of g]
+//          dy [M, N], x [M, K] -> dw [G, N, K]  (a group without rows gets zeros)
+// "bf16 in / fp32 accumulate / bf16 out" (case07...py:37).
+//
+// Both products have an operand whose reduction index is the slow (row)
+// index in memory: w[g] is [N][K] with the reduction over N, and in wgrad both
+// dy and x are reduced over their rows. Such an operand ("reduction-major",
+// RM) is staged in LDS as it lies in memory, 64 reduction rows x 256 columns
+// per stage (512-byte rows, 16-byte chunks XOR-swizzled by (row % 4) * 4), and
+// its MFMA fragments are read with ds_read_b64_tr_b16: in each group of 16
+// lanes, lane 4j + q addresses row j, columns 4q .. 4q + 3 of a 4 x 16 block
+// and lane i receives column i of rows 0..3, so two such reads give a lane the
+// 8 consecutive reduction values of one column that v_mfma_f32_32x32x16_bf16
+// takes. dgrad's dy is reduced along its rows' contiguous axis ("KC") and is
+// staged like the forward kernel's operands (128-byte rows, ds_read_b128).
+//
+// Kernel shape: persistent, one workgroup of 4 wavefronts per CU; output tile
+// kBM x 256 (kBM = 256: 2 x 2 waves of 128 x 128; kBM = 128: 1 x 4 waves of
+// 128 x 64, for groups of at most ~128 rows); reduction step 64; two-stage LDS
+// ring filled by buffer_load ... lds one step ahead of the MFMAs; the next
+// step's fragments are read while the current step's MFMAs run (as in the
+// forward kernel). The accumulators hold the transposed block (the column
+// operand is the MFMA's first operand); the epilogue rounds to bf16 (RNE,
+// hardware), pairs register groups across the two half-waves with
+// v_permlane32_swap so each lane holds 8 consecutive columns, and stores 16
+// bytes per lane straight from registers through a buffer resource (stores
+// past the tile's valid rows or columns are dropped), while the next tile's
+// first stage is already loading. Reduction rows past the end come from past
+// the operand's buffer resource and read as zeros (dgrad's dy columns past N
+// are zeroed in LDS).
+//
+// Tiles are numbered group by group; inside a group in patches of 8 row tiles
+// x all column tiles; workgroup b takes tile round * P + (b % 8) * (P / 8) + b / 8
+// so each XCD works on one patch per round.
+#include <algorithm>
+
+#include "gemm_device.h"
+
+namespace moe {
+namespace {
+
+using namespace gemm;
+
+typedef __bf16 v4bf16 __attribute__((__vector_size__(8)));
+typedef __attribute__((address_space(3))) v4bf16 lds_v4bf16;
+
+constexpr int kBN = 256;            // output columns per tile
+constexpr int kGroupM = 8;          // row tiles per tile-order patch
+constexpr int kStages = 2;
+constexpr int kSubSteps = kBK / 16;
+constexpr int kKCRow = kBK * 2;     // 128-byte rows of a KC operand tile
+constexpr int kRMRow = 256 * 2;     // 512-byte rows of an RM operand tile (256 columns)
+
+struct BwdArgs {
+  const uint16_t *a;        // dy [M, N]
+  const uint16_t *b;        // dgrad: w [G, N, K]; wgrad: x [M, K]
+  const int32_t *offsets;   // [G + 1]
+  uint16_t *out;            // dgrad: dx [M, K]; wgrad: dw [G, N, K]
+  int64_t M, N, K, G;
+  int64_t ntiles;           // column tiles, ceil(K / 256)
+};
+
+__device__ __forceinline__ int kc_swz(int row) { return (row >> 1) & 7; }
+__device__ __forceinline__ int rm_swz(int krow) { return (krow & 3) << 2; }
+
+// One transposing LDS read. The restrict-qualified pointer gives the access
+// alias-scope information; without it the compiler assumes the read may
+// alias any LDS DMA in flight and waits for all of them (vmcnt(0)) before it.
+// The kernel orders its DMA and reads itself (wait + barrier per stage).
+__device__ __forceinline__ v4bf16 read_tr(lds_v4bf16 *__restrict__ p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(p);
+#else
+  (void)p;
+  return v4bf16{};
+#endif
+}
+
+// Fragment of an RM operand: 8 consecutive reduction values of one column per
+// lane, from two transposing LDS reads 4 rows apart.
+__device__ __forceinline__ bf16x8 read_rm_frag(uint32_t addr) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const v4bf16 lo = read_tr((lds_v4bf16 *)(uintptr_t)addr);
+  const v4bf16 hi = read_tr((lds_v4bf16 *)(uintptr_t)(addr + 4 * kRMRow));
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#else
+  (void)addr;
+  return bf16x8{};
+#endif
+}
+
+template <bool kWgrad, int kBM, int kWavesM>
+__global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
+  constexpr int kWaves = 4;
+  constexpr int kWavesN = kWaves / kWavesM;
+  constexpr int kWaveRows = kBM / kWavesM;
+  constexpr int kWaveCols = kBN / kWavesN;
+  constexpr int kMI = kWaveRows / 32, kNI = kWaveCols / 32;
+  constexpr bool kARM = kWgrad;                 // A (output rows) reduction-major
+  constexpr int kABytes = kBM * kBK * 2;
+  constexpr int kBBytes = kBN * kBK * 2;
+  constexpr int kStageBytes = kABytes + kBBytes;
+  constexpr int kDmaA = kABytes / 1024 / kWaves, kDmaB = kBBytes / 1024 / kWaves;
+  constexpr int kStores = kMI * kNI * 2;        // 16-byte stores per lane per tile
+  constexpr int kReads = (kARM ? 2 * kMI : kMI) + 2 * kNI;  // LDS reads per sub-step
+  constexpr int kMfma = kMI * kNI;              // MFMAs per sub-step
+  static_assert(kStages * kStageBytes <= 160 * 1024, "LDS budget");
+  static_assert(kStores + kDmaA + kDmaB <= 63, "vmcnt range");
+  static_assert(!kARM || kBM == 256, "a reduction-major A tile is 256 columns wide");
+  __shared__ __attribute__((aligned(1024))) char smem[kStages * kStageBytes];
+  lds_char *const sbase = (lds_char *)smem;
+  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sbase));
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / kWavesN;
+  const int wn = wave % kWavesN;
+  const int64_t P = gridDim.x;
+  const int64_t b = blockIdx.x;
+  const int64_t N = p.N, K = p.K;
+  const bool a_ktail = !kWgrad && (N % kBK) != 0;  // dgrad: dy columns past N in the last step
+
+  // ---- tile walker
+  auto group_range = [&](int64_t g, int64_t &lo, int64_t &hi) {
+    lo = min(max(static_cast<int64_t>(p.offsets[g]), int64_t(0)), p.M);
+    hi = min(max(static_cast<int64_t>(p.offsets[g + 1]), lo), p.M);
+  };
+  auto row_tiles = [&](int64_t lo, int64_t hi) -> int64_t {
+    return kWgrad ? ceil_div(N, kBM) : ceil_div(hi - lo, kBM);
+  };
+  int64_t g_cur = 0, tiles_before = 0, g_lo, g_hi;
+  group_range(0, g_lo, g_hi);
+  int64_t mt_g = row_tiles(g_lo, g_hi);
+  struct Tile {
+    int64_t g, lo, hi;  // group and its row range (dgrad: output rows; wgrad: reduction rows)
+    int64_t i0;         // first output row of the tile (dgrad: in dx; wgrad: in dw[g])
+    uint32_t nt;        // column tile
+    int ktiles;         // reduction steps (at least 1: an empty reduction reads zeros)
+  };
+  auto find_tile = [&](int64_t round, Tile &t) -> bool {
+    const int64_t L = round * P + (b % 8) * (P / 8) + b / 8;
+    while (g_cur < p.G && L >= tiles_before + mt_g * p.ntiles) {
+      tiles_before += mt_g * p.ntiles;
+      ++g_cur;
+      if (g_cur < p.G) {
+        group_range(g_cur, g_lo, g_hi);
+        mt_g = row_tiles(g_lo, g_hi);
+      }
+    }
+    if (g_cur >= p.G) return false;
+    const uint32_t q = static_cast<uint32_t>(L - tiles_before);
+    const uint32_t per_grp = kGroupM * static_cast<uint32_t>(p.ntiles);
+    const uint32_t full = static_cast<uint32_t>(mt_g) / kGroupM;
+    uint32_t mt, nt;
+    if (q < full * per_grp) {
+      const uint32_t grp = q / per_grp, r = q - grp * per_grp;
+      nt = r / kGroupM;
+      mt = grp * kGroupM + r % kGroupM;
+    } else {
+      const uint32_t r = q - full * per_grp, gm = static_cast<uint32_t>(mt_g) - full * kGroupM;
+      nt = r / gm;
+      mt = full * kGroupM + (r - nt * gm);
+    }
+    t.g = g_cur;
+    t.lo = g_lo;
+    t.hi = g_hi;
+    t.i0 = (kWgrad ? 0 : g_lo) + static_cast<int64_t>(mt) * kBM;
+    t.nt = nt;
+    const int64_t red = kWgrad ? g_hi - g_lo : N;
+    t.ktiles = static_cast<int>(max(ceil_div(red, kBK), int64_t(1)));
+    return true;
+  };
+
+  // ---- DMA sources of the tile being loaded
+  __amdgpu_buffer_rsrc_t ra, rb;
+  int a_off[kDmaA], b_off[kDmaB];
+  int a_step = 0, b_step = 0;  // bytes per reduction step
+  auto setup_dma = [&](const Tile &t) {
+    // RM operand lane map: DMA block blk holds reduction rows 2 blk, 2 blk + 1.
+    const int rm_krow = lane >> 5, rm_pchunk = lane & 31;
+    if constexpr (kWgrad) {
+      const uint32_t rows = static_cast<uint32_t>(t.hi - t.lo);
+      ra = make_rsrc(p.a + t.lo * N, rows * static_cast<uint32_t>(N) * 2u);
+      rb = make_rsrc(p.b + t.lo * K, rows * static_cast<uint32_t>(K) * 2u);
+      a_step = kBK * static_cast<int>(N) * 2;
+#pragma unroll
+      for (int j = 0; j < kDmaA; ++j) {
+        const int krow = (j * kWaves + wave) * 2 + rm_krow;
+        const int lchunk = rm_pchunk ^ rm_swz(krow);
+        a_off[j] = static_cast<int>(static_cast<uint32_t>(krow) * static_cast<uint32_t>(N) * 2u +
+                                    static_cast<uint32_t>(t.i0) * 2u + lchunk * 16);
+      }
+    } else {
+      const int rows_valid = static_cast<int>(min(t.hi - t.i0, int64_t(kBM)));
+      ra = make_rsrc(p.a + t.i0 * N, static_cast<uint32_t>(rows_valid) * static_cast<uint32_t>(N) * 2u);
+      rb = make_rsrc(p.b + t.g * N * K, static_cast<uint32_t>(N * K * 2));
+      a_step = kBK * 2;
+#pragma unroll
+      for (int j = 0; j < kDmaA; ++j) {
+        const int r = (j * kWaves + wave) * 8 + (lane >> 3);
+        const int lchunk = (lane & 7) ^ kc_swz(r);
+        a_off[j] = static_cast<int>(static_cast<uint32_t>(min(r, rows_valid - 1)) * static_cast<uint32_t>(N) * 2u +
+                                    lchunk * 16);
+      }
+    }
+    b_step = kBK * static_cast<int>(K) * 2;
+    const uint32_t col0 = t.nt * static_cast<uint32_t>(kBN);
+#pragma unroll
+    for (int j = 0; j < kDmaB; ++j) {
+      const int krow = (j * kWaves + wave) * 2 + rm_krow;
+      const int lchunk = rm_pchunk ^ rm_swz(krow);
+      b_off[j] = static_cast<int>(static_cast<uint32_t>(krow) * static_cast<uint32_t>(K) * 2u + col0 * 2u + lchunk * 16);
+    }
+  };
+  auto issue_a = [&](int kt, int slot) {
+    const uint32_t st = lds_base + (slot % kStages) * kStageBytes;
+#pragma unroll
+    for (int j = 0; j < kDmaA; ++j)
+      dma16b(ra, (lds_void *)(uintptr_t)(st + (j * kWaves + wave) * 1024), a_off[j], kt * a_step);
+  };
+  auto issue_b = [&](int kt, int slot) {
+    const uint32_t st = lds_base + (slot % kStages) * kStageBytes + kABytes;
+#pragma unroll
+    for (int j = 0; j < kDmaB; ++j)
+      dma16b(rb, (lds_void *)(uintptr_t)(st + (j * kWaves + wave) * 1024), b_off[j], kt * b_step);
+  };
+  // dgrad: zero dy's chunks past column N in the A tile of stage kt.
+  auto zero_ktail_a = [&](int kt) {
+    lds_char *st = sbase + (kt % kStages) * kStageBytes;
+    const int kvalid = static_cast<int>(N - static_cast<int64_t>(kt) * kBK);
+    for (int idx = tid; idx < kBM * 8; idx += kWaves * 64) {
+      const int r = idx >> 3, c = idx & 7;
+      if (c * 8 >= kvalid) *reinterpret_cast<lds_u32x4 *>(st + r * kKCRow + ((c ^ kc_swz(r)) * 16)) = u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+
+  // ---- fragment addresses (LDS bytes relative to a stage)
+  // RM: lane 16 G + 4 j + q reads row (G / 2) * 8 + j (+ 4 for the second
+  // read), bytes ((G & 1) * 16 + 4 q) * 2 of the 32-column block, swizzled.
+  const int rm_g = lane >> 4, rm_j = (lane >> 2) & 3, rm_q = lane & 3;
+  const int rm_lane = ((rm_g >> 1) * 8 + rm_j) * kRMRow + (((rm_g & 1) * 2 + (rm_q >> 1)) << 4) + (rm_q & 1) * 8;
+  auto rm_base = [&](int c0) { return rm_lane + ((c0 * 2) ^ (rm_j << 6)); };
+  const int khalf = lane >> 5;
+  int fa_base[kMI], fb_base[kNI];
+#pragma unroll
+  for (int i = 0; i < kMI; ++i) {
+    if constexpr (kARM) {
+      fa_base[i] = rm_base(wm * kWaveRows + i * 32);
+    } else {
+      const int r = wm * kWaveRows + i * 32 + (lane & 31);
+      fa_base[i] = (r * kKCRow | (kc_swz(r) << 4)) ^ (khalf << 4);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kNI; ++j) fb_base[j] = kABytes + rm_base(wn * kWaveCols + j * 32);
+
+  f32x16 acc[kMI][kNI];
+  uint32_t rd_a[kMI], rd_b[kNI];
+  auto set_read_slot = [&](int kt) {
+    const uint32_t so = lds_base + (kt % kStages) * kStageBytes;
+#pragma unroll
+    for (int i = 0; i < kMI; ++i) rd_a[i] = so + fa_base[i];
+#pragma unroll
+    for (int j = 0; j < kNI; ++j) rd_b[j] = so + fb_base[j];
+  };
+  bf16x8 fa[kSubSteps][kMI], fb[kSubSteps][kNI];
+  auto read_frags = [&](int ks) {
+#pragma unroll
+    for (int i = 0; i < kMI; ++i) {
+      if constexpr (kARM) {
+        fa[ks][i] = read_rm_frag(rd_a[i] + ks * 16 * kRMRow);
+      } else {
+        fa[ks][i] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)(rd_a[i] ^ (ks << 5)));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kNI; ++j) fb[ks][j] = read_rm_frag(rd_b[j] + ks * 16 * kRMRow);
+  };
+  auto mfma_ks = [&](int ks) {
+#pragma unroll
+    for (int i = 0; i < kMI; ++i)
+#pragma unroll
+      for (int j = 0; j < kNI; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks][j], fa[ks][i], acc[i][j], 0, 0, 0);
+  };
+
+  Tile cur;
+  if (!find_tile(0, cur)) return;
+  setup_dma(cur);
+  issue_a(0, 0);
+  issue_b(0, 0);
+  // Stage 1 (a re-read of stage 0 into the unused slot when there is one
+  // step, so the count of outstanding loads is the same for every tile).
+  issue_a(min(1, cur.ktiles - 1), 1);
+  issue_b(min(1, cur.ktiles - 1), 1);
+
+  for (int64_t round = 0;; ++round) {
+#pragma unroll
+    for (int i = 0; i < kMI; ++i)
+#pragma unroll
+      for (int j = 0; j < kNI; ++j) acc[i][j] = f32x16{};
+
+    // Stage 0 has landed. Younger: stage 1 and, after the first tile, the
+    // previous tile's output stores issued between the two stages.
+    if (round == 0) {
+      wait_vm_n<kDmaA + kDmaB>();
+    } else {
+      wait_vm_n<kStores + kDmaA + kDmaB>();
+    }
+    barrier();
+    const int ktiles = cur.ktiles;
+    if (a_ktail && ktiles == 1) {
+      zero_ktail_a(0);
+      wait_lds();
+      barrier();
+    }
+    set_read_slot(0);
+#pragma unroll
+    for (int ks = 0; ks < kSubSteps; ++ks) read_frags(ks);
+
+    for (int kt = 0; kt + 1 < ktiles; ++kt) {
+      mfma_ks(0);
+      __builtin_amdgcn_sched_barrier(0);
+      // This thread's DMA of stage kt + 1 has landed and its reads of stage kt
+      // are done; after the barrier, everyone's.
+      wait_dma();
+      wait_lds();
+      barrier();
+      if (a_ktail && kt + 1 == ktiles - 1) {
+        zero_ktail_a(kt + 1);
+        wait_lds();
+        barrier();
+      }
+      // Stage kt + 2 into the slot of stage kt (the last step re-reads the
+      // final stage into that free slot, so the region below has no branch).
+      const int kdma = min(kt + 2, ktiles - 1);
+      set_read_slot(kt + 1);
+      read_frags(0);
+      mfma_ks(1);
+      issue_a(kdma, kt + 2);
+      sched_mix<kMfma, kReads, kDmaA>();
+      mfma_ks(2);
+      read_frags(1);
+      issue_b(kdma, kt + 2);
+      sched_mix<kMfma, kReads, kDmaB>();
+      mfma_ks(3);
+      read_frags(2);
+      sched_mix<kMfma, kReads, 0>();
+      read_frags(3);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    mfma_ks(0);
+    mfma_ks(1);
+    mfma_ks(2);
+    mfma_ks(3);
+
+    // No DMA in flight and every wave done reading the ring: the next tile's
+    // stage 0 loads during this tile's epilogue, its stage 1 after the stores.
+    wait_dma();
+    wait_lds();
+    barrier();
+    Tile nxt;
+    const bool more = find_tile(round + 1, nxt);
+    if (more) {
+      setup_dma(nxt);
+      issue_a(0, 0);
+      issue_b(0, 0);
+    }
+
+    // Epilogue straight from registers. Register r of lane l in block (i, j)
+    // holds output row i * 32 + l % 32 and column j * 32 + (r / 4) * 8 +
+    // (l / 32) * 4 + r % 4 of this wave's part. After bf16 rounding each
+    // 4-register group is two packed words; v_permlane32_swap trades the upper
+    // half-wave's words of group g with the lower half-wave's of group g + 1, so
+    // a lower lane holds columns 8g .. 8g + 7 of its row and its upper partner
+    // 8g + 8 .. 8g + 15: one 16-byte store each.
+    {
+      const int64_t wrow0 = cur.i0 + wm * kWaveRows;
+      const int64_t row_end = kWgrad ? N : cur.hi;
+      const int rows_out = static_cast<int>(min(max(row_end - wrow0, int64_t(0)), int64_t(kWaveRows)));
+      const uint16_t *obase = kWgrad ? p.out + cur.g * N * K : p.out;
+      const uint32_t ld = static_cast<uint32_t>(K) * 2u;
+      const __amdgpu_buffer_rsrc_t ro =
+          make_rsrc(obase + (rows_out > 0 ? wrow0 * K : 0), static_cast<uint32_t>(rows_out) * ld);
+      const int64_t tcol0 = static_cast<int64_t>(cur.nt) * kBN + wn * kWaveCols;
+      const int half = lane >> 5;
+#pragma unroll
+      for (int i = 0; i < kMI; ++i) {
+        const int orow = i * 32 + (lane & 31);
+#pragma unroll
+        for (int j = 0; j < kNI; ++j) {
+          uint32_t w[4][2];
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const bf16x2 lo = {(__bf16)acc[i][j][4 * g], (__bf16)acc[i][j][4 * g + 1]};
+            const bf16x2 hi = {(__bf16)acc[i][j][4 * g + 2], (__bf16)acc[i][j][4 * g + 3]};
+            w[g][0] = __builtin_bit_cast(uint32_t, lo);
+            w[g][1] = __builtin_bit_cast(uint32_t, hi);
+          }
+#pragma unroll
+          for (int gp = 0; gp < 4; gp += 2) {
+            u32x4 o;
+#if defined(__HIP_DEVICE_COMPILE__)
+            const auto s0 = __builtin_amdgcn_permlane32_swap(w[gp][0], w[gp + 1][0], false, false);
+            const auto s1 = __builtin_amdgcn_permlane32_swap(w[gp][1], w[gp + 1][1], false, false);
+            o = u32x4{s0[0], s1[0], s0[1], s1[1]};
+#else
+            o = u32x4{0u, 0u, 0u, 0u};
+#endif
+            const int64_t gcol = tcol0 + j * 32 + (gp + half) * 8;
+            // Columns past K get an offset past the resource: the store is dropped.
+            const uint32_t off = gcol < K ? static_cast<uint32_t>(orow) * ld + static_cast<uint32_t>(gcol) * 2u : kNoAccess;
+#if defined(__HIP_DEVICE_COMPILE__)
+            __builtin_amdgcn_raw_buffer_store_b128(o, ro, static_cast<int>(off), 0, 0);
+#else
+            (void)off;
+            (void)ro;
+            (void)o;
+#endif
+          }
+        }
+      }
+    }
+    if (!more) break;
+    issue_a(min(1, nxt.ktiles - 1), 1);
+    issue_b(min(1, nxt.ktiles - 1), 1);
+    cur = nxt;
+  }
+}
+
+template <bool kWgrad, int kBM, int kWavesM>
+void launch(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
+  int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
+  grid = std::max<int64_t>(8, (grid + 7) / 8 * 8);
+  grouped_gemm_bwd_kernel<kWgrad, kBM, kWavesM><<<dim3(grid), dim3(256), 0, s>>>(p);
+}
+
+}  // namespace
+}  // namespace moe
+
+namespace {
+
+int check_common(const char *fn, int64_t M_total, int64_t N, int64_t K, int64_t G, const int32_t *group_offsets) {
+  using namespace moe;
+  if (M_total < 0 || N < 0 || K < 0 || G < 0) {
+    return fail(MOE_ERR_SHAPE, "%s: negative size (M=%lld N=%lld K=%lld G=%lld)", fn, (long long)M_total,
+                (long long)N, (long long)K, (long long)G);
+  }
+  if (G < 1 || G > 4096) return fail(MOE_ERR_CAPACITY, "%s: G=%lld outside [1, 4096]", fn, (long long)G);
+  if (N % 8 != 0 || K % 8 != 0) {
+    return fail(MOE_ERR_SHAPE, "%s: N=%lld and K=%lld must be multiples of 8", fn, (long long)N, (long long)K);
+  }
+  if (group_offsets == nullptr) return fail(MOE_ERR_INVALID_ARG, "%s: null group_offsets", fn);
+  return MOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, const moe_bf16_t *w, int64_t G,
+                           int64_t K, const int32_t *group_offsets, moe_bf16_t *dx, void *workspace,
+                           size_t workspace_bytes, void *stream) {
+  using namespace moe;
+  (void)workspace;
+  (void)workspace_bytes;
+  const char *fn = "moe_grouped_gemm_dgrad";
+  if (int rc = check_common(fn, M_total, N, K, G, group_offsets)) return rc;
+  // 32-bit buffer offsets: a 256-row panel of dy and one expert's w stay below 2 GiB.
+  if (N > (int64_t(1) << 22) - 8 || K > (int64_t(1) << 22) - 8 || N * K > (int64_t(1) << 30) - 1) {
+    return fail(MOE_ERR_CAPACITY, "%s: N=%lld K=%lld exceed the 32-bit panel offsets (N, K < 2^22, N*K < 2^30)", fn,
+                (long long)N, (long long)K);
+  }
+  if (M_total == 0 || K == 0) return MOE_OK;
+  if (dx == nullptr || (N > 0 && (dy == nullptr || w == nullptr))) {
+    return fail(MOE_ERR_INVALID_ARG, "%s: null dy, w or dx", fn);
+  }
+  if (!is_aligned(dy, 16) || !is_aligned(w, 16) || !is_aligned(dx, 16)) {
+    return fail(MOE_ERR_ALIGN, "%s: dy, w and dx must be 16-byte aligned", fn);
+  }
+  BwdArgs p;
+  p.a = dy;
+  p.b = w;
+  p.offsets = group_offsets;
+  p.out = dx;
+  p.M = M_total;
+  p.N = N;
+  p.K = K;
+  p.G = G;
+  p.ntiles = ceil_div(K, kBN);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // 128-row tiles when the groups average at most 160 rows (less padding in
+  // every group's last row tile), 256-row tiles otherwise.
+  if (M_total <= 160 * G) {
+    launch<false, 128, 1>(p, (ceil_div(M_total, 128) + G) * p.ntiles, s);
+  } else {
+    launch<false, 256, 2>(p, (ceil_div(M_total, 256) + G) * p.ntiles, s);
+  }
+  return check_launch(fn);
+}
+
+int moe_grouped_gemm_wgrad(const moe_bf16_t *dy, const moe_bf16_t *x, int64_t M_total, int64_t N, int64_t K,
+                           int64_t G, const int32_t *group_offsets, moe_bf16_t *dw, void *workspace,
+                           size_t workspace_bytes, void *stream) {
+  using namespace moe;
+  (void)workspace;
+  (void)workspace_bytes;
+  const char *fn = "moe_grouped_gemm_wgrad";
+  if (int rc = check_common(fn, M_total, N, K, G, group_offsets)) return rc;
+  // 32-bit buffer offsets: all of dy, all of x and one group's dw stay below 2 GiB.
+  if (M_total * N > (int64_t(1) << 30) - 1 || M_total * K > (int64_t(1) << 30) - 1 ||
+      N * K > (int64_t(1) << 30) - 1) {
+    return fail(MOE_ERR_CAPACITY, "%s: M=%lld N=%lld K=%lld exceed the 32-bit offsets (M*N, M*K, N*K < 2^30)", fn,
+                (long long)M_total, (long long)N, (long long)K);
+  }
+  if (N == 0 || K == 0) return MOE_OK;
+  if (dw == nullptr || (M_total > 0 && (dy == nullptr || x == nullptr))) {
+    return fail(MOE_ERR_INVALID_ARG, "%s: null dy, x or dw", fn);
+  }
+  if (!is_aligned(dy, 16) || !is_aligned(x, 16) || !is_aligned(dw, 16)) {
+    return fail(MOE_ERR_ALIGN, "%s: dy, x and dw must be 16-byte aligned", fn);
+  }
+  BwdArgs p;
+  p.a = dy;
+  p.b = x;
+  p.offsets = group_offsets;
+  p.out = dw;
+  p.M = M_total;
+  p.N = N;
+  p.K = K;
+  p.G = G;
+  p.ntiles = ceil_div(K, kBN);
+  launch<true, 256, 2>(p, G * ceil_div(N, 256) * p.ntiles, static_cast<hipStream_t>(stream));
+  return check_launch(fn);
+}
+
+}  // extern "C"

@@ -318,3 +318,52 @@ def grouped_gemm_gather(x: torch.Tensor, a_rows: torch.Tensor, w: torch.Tensor, 
     call("moe_grouped_gemm_gather", ptr(xc), x.shape[0], ptr(rc), M, K, ptr(wc), G, N, ptr(oc),
          MOE_EPILOGUE_SWIGLU if swiglu else MOE_EPILOGUE_NONE, ptr(out), None, 0, stream_handle())
     return out
+
+
+def grouped_gemm_dgrad(dy: torch.Tensor, w: torch.Tensor, group_offsets: torch.Tensor, *,
+                       out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """dx[rows of g] = dy[rows of g] @ w[g] (bf16 in, fp32 accumulate, bf16 out).
+
+    dy bf16 [M, N]; w bf16 [G, N, K] (the forward's weights); group_offsets int32 [G+1] on the device.
+    """
+    _on_gpu("dy", dy)
+    _on_gpu("w", w)
+    _on_gpu("group_offsets", group_offsets)
+    _dtype("dy", dy, torch.bfloat16)
+    _dtype("w", w, torch.bfloat16)
+    _dtype("group_offsets", group_offsets, torch.int32)
+    if dy.ndim != 2 or w.ndim != 3 or dy.shape[1] != w.shape[1]:
+        raise ValueError(f"shapes dy {tuple(dy.shape)} w {tuple(w.shape)}: need dy [M,N], w [G,N,K]")
+    G, N, K = w.shape
+    if group_offsets.shape != (G + 1,):
+        raise ValueError(f"group_offsets {tuple(group_offsets.shape)} expected ({G + 1},)")
+    M = dy.shape[0]
+    dyc, wc, oc = dy.contiguous(), w.contiguous(), group_offsets.contiguous()
+    if out is None:
+        out = torch.empty(M, K, dtype=torch.bfloat16, device=dy.device)
+    call("moe_grouped_gemm_dgrad", ptr(dyc), M, N, ptr(wc), G, K, ptr(oc), ptr(out), None, 0, stream_handle())
+    return out
+
+
+def grouped_gemm_wgrad(dy: torch.Tensor, x: torch.Tensor, group_offsets: torch.Tensor, *,
+                       out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """dw[g] = dy[rows of g]^T @ x[rows of g] (bf16 in, fp32 accumulate, bf16 out); empty groups give zeros.
+
+    dy bf16 [M, N]; x bf16 [M, K]; group_offsets int32 [G+1] on the device; returns dw bf16 [G, N, K].
+    """
+    _on_gpu("dy", dy)
+    _on_gpu("x", x)
+    _on_gpu("group_offsets", group_offsets)
+    _dtype("dy", dy, torch.bfloat16)
+    _dtype("x", x, torch.bfloat16)
+    _dtype("group_offsets", group_offsets, torch.int32)
+    if dy.ndim != 2 or x.ndim != 2 or dy.shape[0] != x.shape[0] or group_offsets.ndim != 1:
+        raise ValueError(f"shapes dy {tuple(dy.shape)} x {tuple(x.shape)}: need dy [M,N], x [M,K]")
+    G = group_offsets.shape[0] - 1
+    M, N = dy.shape
+    K = x.shape[1]
+    dyc, xc, oc = dy.contiguous(), x.contiguous(), group_offsets.contiguous()
+    if out is None:
+        out = torch.empty(G, N, K, dtype=torch.bfloat16, device=dy.device)
+    call("moe_grouped_gemm_wgrad", ptr(dyc), ptr(xc), M, N, K, G, ptr(oc), ptr(out), None, 0, stream_handle())
+    return out

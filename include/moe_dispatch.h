@@ -32,6 +32,9 @@
  *   case18 kernel_cases/case18_moe_permute_bwd_unpermute_mask.py:68-78 (no bundle)
  *   case03/case04 kernel_cases/case03_moe_grouped_gemm_fc1_fwd.py:57-64,
  *                 kernel_cases/case04_moe_grouped_gemm_fc2_fwd.py:57-64 (no bundle)
+ *   case07/08/13/19 (and case37) kernel_cases/case07_moe_grouped_gemm_fc1_dgrad.py:57-64
+ *                 (dgrad, no bundle)
+ *   case05/case09 kernel_cases/case09_moe_grouped_gemm_fc1_wgrad.py:57-64 (wgrad, no bundle)
  */
 #ifndef MOE_DISPATCH_H_
 #define MOE_DISPATCH_H_
@@ -43,7 +46,7 @@
 extern "C" {
 #endif
 
-#define MOE_DISPATCH_ABI_VERSION 2
+#define MOE_DISPATCH_ABI_VERSION 3
 
 typedef uint16_t moe_bf16_t;
 
@@ -215,6 +218,39 @@ int moe_grouped_gemm_gather(const moe_bf16_t *x, int64_t x_rows, const int32_t *
                             int64_t M_total, int64_t K, const moe_bf16_t *w, int64_t G, int64_t N,
                             const int32_t *group_offsets, int epilogue, moe_bf16_t *out,
                             void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---- grouped GEMM backward: input gradient ("NN") ------------------------
+ * Replaces case07/case08/case13/case19 Model.forward(dy, w) =
+ * cat_g( dy[seg_g] @ w[g] ) (kernel_cases/case07_moe_grouped_gemm_fc1_dgrad.py:57-64,
+ * case08_moe_grouped_gemm_fc2_dgrad.py:57-64, case13...:57-64, case19...:57-64)
+ * and, for one group, case37's NN GEMM (kernel_cases/
+ * case37_ref_musa_asm_bf16_gemm_nn_256x384.py:47-49); bf16 in / fp32
+ * accumulate / bf16 out (case07...py:37).
+ *   dy  bf16 [M_total, N] (rows of group g are group_offsets[g] .. [g+1]-1)
+ *   w   bf16 [G, N, K]    (the forward's [out, in] weights; dx = dy @ w[g])
+ *   group_offsets int32 [G + 1] on the device, as moe_grouped_gemm
+ *   dx  bf16 [M_total, K] (rows beyond group_offsets[G] are not written)
+ * Limits: N % 8 == 0, K % 8 == 0, 1 <= G <= 4096, N, K < 2^22, N * K < 2^30;
+ *   dy, w, dx 16-byte aligned. N == 0 gives zeros.
+ * Workspace: none (pass NULL, 0). */
+int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, const moe_bf16_t *w,
+                           int64_t G, int64_t K, const int32_t *group_offsets, moe_bf16_t *dx,
+                           void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---- grouped GEMM backward: weight gradient ("TN") -----------------------
+ * Replaces case05/case09 Model.forward(dy, x) = stack_g( dy[seg_g]^T @ x[seg_g] )
+ * (kernel_cases/case09_moe_grouped_gemm_fc1_wgrad.py:57-64,
+ *  kernel_cases/case05_moe_grouped_gemm_fc2_wgrad.py:57-64); bf16 in / fp32
+ * accumulate / bf16 out.
+ *   dy  bf16 [M_total, N]; x bf16 [M_total, K] (rows of group g as above)
+ *   dw  bf16 [G, N, K]: dw[g] = sum over the rows of g of dy[r]^T x[r]
+ *       (a group without rows gets zeros, like torch.mm over an empty K)
+ * Limits: N % 8 == 0, K % 8 == 0, 1 <= G <= 4096, M_total * N, M_total * K and
+ *   N * K < 2^30; dy, x, dw 16-byte aligned.
+ * Workspace: none (pass NULL, 0). */
+int moe_grouped_gemm_wgrad(const moe_bf16_t *dy, const moe_bf16_t *x, int64_t M_total, int64_t N,
+                           int64_t K, int64_t G, const int32_t *group_offsets, moe_bf16_t *dw,
+                           void *workspace, size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -267,6 +267,57 @@ def grouped_gemm_fp32(x: torch.Tensor, w: torch.Tensor, sizes: Sequence[int]) ->
     return torch.cat(outs, dim=0)
 
 
+def grouped_gemm_dgrad(dy: torch.Tensor, w: torch.Tensor, sizes: Sequence[int]) -> torch.Tensor:
+    """cat_g(dy[seg_g] @ w[g]) in the inputs' dtype (per-group torch.mm, then cat).
+
+    kernel_cases/case07_moe_grouped_gemm_fc1_dgrad.py:57-64 (= case08, case13, case19 :57-64).
+    """
+    outs, off = [], 0
+    for i, m in enumerate(sizes):
+        outs.append(torch.mm(dy[off:off + m], w[i]))
+        off += m
+    return torch.cat(outs, dim=0)
+
+
+def grouped_gemm_dgrad_fp32(dy: torch.Tensor, w: torch.Tensor, sizes: Sequence[int]) -> torch.Tensor:
+    """fp32-accumulated golden of the dgrad: cat_g(dy[seg_g].float() @ w[g].float()), fp32 out.
+
+    kernel_cases/case37_ref_musa_asm_bf16_gemm_nn_256x384.py:47-49 (reference_fp32, one group)
+    applied per group of case07's Model.forward.
+    """
+    outs, off = [], 0
+    for i, m in enumerate(sizes):
+        outs.append(dy[off:off + m].float().matmul(w[i].float()))
+        off += m
+    if not outs:
+        return torch.zeros(0, w.shape[2], dtype=torch.float32)
+    return torch.cat(outs, dim=0)
+
+
+def grouped_gemm_wgrad(dy: torch.Tensor, x: torch.Tensor, sizes: Sequence[int]) -> torch.Tensor:
+    """stack_g(dy[seg_g].T @ x[seg_g]) in the inputs' dtype (per-group torch.mm, then stack).
+
+    kernel_cases/case09_moe_grouped_gemm_fc1_wgrad.py:57-64 (= case05 :57-64).
+    """
+    outs, off = [], 0
+    for m in sizes:
+        outs.append(torch.mm(dy[off:off + m].t(), x[off:off + m]))
+        off += m
+    return torch.stack(outs, dim=0)
+
+
+def grouped_gemm_wgrad_fp32(dy: torch.Tensor, x: torch.Tensor, sizes: Sequence[int]) -> torch.Tensor:
+    """fp32-accumulated golden of the wgrad: stack_g(dy[seg_g].float().T @ x[seg_g].float()), fp32 out.
+
+    The fp32 form of case09's Model.forward (case37...:47-49's reference_fp32 rule).
+    """
+    outs, off = [], 0
+    for m in sizes:
+        outs.append(dy[off:off + m].float().t().matmul(x[off:off + m].float()))
+        off += m
+    return torch.stack(outs, dim=0)
+
+
 def swiglu(y: torch.Tensor) -> torch.Tensor:
     """silu(y[:, :F]) * y[:, F:] in fp32, F = N/2 (gate first).  No reference function."""
     f = y.shape[1] // 2

@@ -17,7 +17,7 @@ L = pkg._lib
 def test_library_loads_and_exports_header_symbols():
     lib = L.lib()
     declared = L.header_functions()
-    assert len(declared) == len(L.SIGNATURES) == 14
+    assert len(declared) == len(L.SIGNATURES) == 16
     assert set(declared) == set(L.SIGNATURES)
     for name in declared:
         assert hasattr(lib, name), name
@@ -78,6 +78,24 @@ FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
     ("moe_permute_index", (None, 1, 0, 4, 8, FAKE, 32, 1, None), L.MOE_ERR_INVALID_ARG, "null"),
     ("moe_permute_index", (FAKE, 1, 0, -4, 8, FAKE, 32, 1, None), L.MOE_ERR_SHAPE, "negative"),
     ("moe_permute_index", (FAKE, 1, 0, 1 << 31, 8, FAKE, 32, 1, None), L.MOE_ERR_CAPACITY, "int32"),
+    # dgrad (dy, M, N, w, G, K, offsets, dx, ws, ws_bytes, stream)
+    ("moe_grouped_gemm_dgrad", (FAKE, -4, 16, FAKE, 1, 16, FAKE, FAKE, None, 0, None), L.MOE_ERR_SHAPE, "negative"),
+    ("moe_grouped_gemm_dgrad", (FAKE, 4, 12, FAKE, 1, 16, FAKE, FAKE, None, 0, None), L.MOE_ERR_SHAPE, "multiples of 8"),
+    ("moe_grouped_gemm_dgrad", (FAKE, 4, 16, FAKE, 1, 20, FAKE, FAKE, None, 0, None), L.MOE_ERR_SHAPE, "multiples of 8"),
+    ("moe_grouped_gemm_dgrad", (FAKE, 4, 16, FAKE, 0, 16, FAKE, FAKE, None, 0, None), L.MOE_ERR_CAPACITY, "G=0"),
+    ("moe_grouped_gemm_dgrad", (FAKE, 4, 16, FAKE, 1, 16, None, FAKE, None, 0, None), L.MOE_ERR_INVALID_ARG, "group_offsets"),
+    ("moe_grouped_gemm_dgrad", (FAKE, 4, 16, None, 1, 16, FAKE, FAKE, None, 0, None), L.MOE_ERR_INVALID_ARG, "null"),
+    ("moe_grouped_gemm_dgrad", (ctypes.c_void_p(0x1008), 4, 16, FAKE, 1, 16, FAKE, FAKE, None, 0, None), L.MOE_ERR_ALIGN, "aligned"),
+    ("moe_grouped_gemm_dgrad", (FAKE, 4, 1 << 22, FAKE, 1, 16, FAKE, FAKE, None, 0, None), L.MOE_ERR_CAPACITY, "32-bit"),
+    ("moe_grouped_gemm_dgrad", (FAKE, 4, 1 << 16, FAKE, 1, 1 << 16, FAKE, FAKE, None, 0, None), L.MOE_ERR_CAPACITY, "32-bit"),
+    # wgrad (dy, x, M, N, K, G, offsets, dw, ws, ws_bytes, stream)
+    ("moe_grouped_gemm_wgrad", (FAKE, FAKE, 4, 16, 16, 5000, FAKE, FAKE, None, 0, None), L.MOE_ERR_CAPACITY, "4096"),
+    ("moe_grouped_gemm_wgrad", (FAKE, FAKE, 4, 16, 10, 1, FAKE, FAKE, None, 0, None), L.MOE_ERR_SHAPE, "multiples of 8"),
+    ("moe_grouped_gemm_wgrad", (FAKE, None, 4, 16, 16, 1, FAKE, FAKE, None, 0, None), L.MOE_ERR_INVALID_ARG, "null"),
+    ("moe_grouped_gemm_wgrad", (FAKE, FAKE, 4, 16, 16, 1, FAKE, None, None, 0, None), L.MOE_ERR_INVALID_ARG, "null"),
+    ("moe_grouped_gemm_wgrad", (FAKE, ctypes.c_void_p(0x1004), 4, 16, 16, 1, FAKE, FAKE, None, 0, None), L.MOE_ERR_ALIGN, "aligned"),
+    ("moe_grouped_gemm_wgrad", (FAKE, FAKE, 1 << 20, 1 << 12, 16, 1, FAKE, FAKE, None, 0, None), L.MOE_ERR_CAPACITY, "32-bit"),
+    ("moe_grouped_gemm_wgrad", (FAKE, FAKE, 16, 1 << 16, 1 << 16, 1, FAKE, FAKE, None, 0, None), L.MOE_ERR_CAPACITY, "32-bit"),
 ])
 def test_argument_validation(name, args, code, needle):
     st, msg = _status(name, *args)
@@ -94,6 +112,9 @@ def test_empty_problems_are_no_ops():
     assert _status("moe_grouped_gemm", None, 0, 16, None, 1, 8, FAKE, 0, None, None, 0, None)[0] == 0
     assert _status("moe_grouped_gemm_gather", None, 4, None, 0, 16, None, 1, 8, FAKE, 0, None, None, 0, None)[0] == 0
     assert _status("moe_permute_index", None, 1, 0, 0, 8, None, 0, 1, None)[0] == 0
+    assert _status("moe_grouped_gemm_dgrad", None, 0, 16, None, 1, 16, FAKE, None, None, 0, None)[0] == 0
+    assert _status("moe_grouped_gemm_dgrad", None, 4, 16, None, 1, 0, FAKE, None, None, 0, None)[0] == 0
+    assert _status("moe_grouped_gemm_wgrad", None, None, 4, 0, 16, 1, FAKE, None, None, 0, None)[0] == 0
 
 
 def test_workspace_sizes():

@@ -1,0 +1,168 @@
+"""GPU parity of the grouped GEMM backward (dgrad "NN", wgrad "TN") against the fp32 oracle.
+
+Tolerance: rtol 1.6e-2 / atol 1e-2 against the fp32-accumulated golden
+(per group dy.float() @ w.float() / dy.float().T @ x.float();
+kernel_cases/case37_ref_musa_asm_bf16_gemm_nn_256x384.py:47-49 is the same
+rule for one group) -- one bf16 rounding of an fp32 sum.  Small shapes are
+checked in full against the CPU oracle; the reference cases' own shapes
+(case05/07/08/09/13/19/37) in full against an fp32 torch reference on the GPU.
+Exact cases (scaled identities, one-row outer products) must be bit-identical.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import assert_bits_equal
+from oracle import ref_torch
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1.6e-2, 1e-2
+
+
+def _check(got, ref, what):
+    torch.testing.assert_close(got.float(), ref.float().to(got.device), rtol=RTOL, atol=ATOL,
+                               msg=lambda m: f"{what}: {m}")
+
+
+def _offsets(sizes, dev):
+    o = [0]
+    for s in sizes:
+        o.append(o[-1] + s)
+    return torch.tensor(o, dtype=torch.int32, device=dev)
+
+
+# ------------------------------------------------------------------ dgrad
+@pytest.mark.parametrize("sizes,N,K", [
+    ([128], 64, 256),                      # one 128-row tile
+    ([1], 8, 8),                           # degenerate
+    ([256, 256], 128, 256),                # 256-row tiles
+    ([300, 0, 17, 513], 200, 264),         # ragged, empty group, N % 64 and K % 256 tails (256-row tiles)
+    ([5, 7, 0, 100, 1], 136, 72),          # small groups (128-row tiles), tails
+    ([90] * 6, 512, 1032),                 # 128-row tiles, several column tiles
+    ([700, 3, 1200], 2048, 520),           # long reduction, 256-row tiles
+])
+def test_dgrad_small(pkg, dev, sizes, N, K):
+    g = torch.Generator().manual_seed(sum(sizes) + 7 * N + K)
+    dy = torch.randn(sum(sizes), N, generator=g).to(torch.bfloat16)
+    w = (torch.randn(len(sizes), N, K, generator=g) * 0.05).to(torch.bfloat16)
+    out = pkg.cases.case07_moe_grouped_gemm_fc1_dgrad.kernel_function(dy.to(dev), w.to(dev), sizes)
+    assert out.shape == (sum(sizes), K)
+    _check(out, ref_torch.grouped_gemm_dgrad_fp32(dy, w, sizes), f"dgrad sizes={sizes} N={N} K={K}")
+
+
+def test_dgrad_scaled_identity_exact(pkg, dev):
+    # dy @ (c I) with c a power of two is exact: bit-identical, on both tile heights.
+    for sizes in ([100, 300, 200], [40, 60, 20]):
+        dy = torch.randn(sum(sizes), 256).to(torch.bfloat16)
+        w = torch.stack([torch.eye(256), 4 * torch.eye(256), 0.5 * torch.eye(256)]).to(torch.bfloat16)
+        out = pkg.ops.grouped_gemm_dgrad(dy.to(dev), w.to(dev), _offsets(sizes, dev)).cpu()
+        a, b = sizes[0], sizes[0] + sizes[1]
+        assert_bits_equal(out[:a], dy[:a], f"identity {sizes}")
+        assert_bits_equal(out[a:b], (4 * dy[a:b].float()).to(torch.bfloat16), f"4I {sizes}")
+        assert_bits_equal(out[b:], (0.5 * dy[b:].float()).to(torch.bfloat16), f"I/2 {sizes}")
+
+
+def test_dgrad_writes_only_grouped_rows(pkg, dev):
+    # Rows past group_offsets[G] and bytes past dx keep their contents.
+    M, N, K = 300, 64, 40
+    dy = torch.randn(M, N, device=dev).to(torch.bfloat16)
+    w = torch.randn(2, N, K, device=dev).to(torch.bfloat16)
+    offs = torch.tensor([0, 100, 250], dtype=torch.int32, device=dev)
+    buf = torch.full((M * K + 4096,), 7.0, dtype=torch.bfloat16, device=dev)
+    out = buf[:M * K].view(M, K)
+    pkg.ops.grouped_gemm_dgrad(dy, w, offs, out=out)
+    assert torch.all(buf[250 * K:] == 7.0)
+    ref = ref_torch.grouped_gemm_dgrad_fp32(dy[:250].cpu(), w.cpu(), [100, 150])
+    _check(out[:250], ref, "dgrad rows")
+
+
+def test_dgrad_empty_reduction_gives_zeros(pkg, dev):
+    dy = torch.empty(10, 0, dtype=torch.bfloat16, device=dev)
+    w = torch.empty(2, 0, 16, dtype=torch.bfloat16, device=dev)
+    out = pkg.ops.grouped_gemm_dgrad(dy, w, _offsets([4, 6], dev), out=torch.full((10, 16), 3.0, dtype=torch.bfloat16,
+                                                                                     device=dev))
+    assert torch.count_nonzero(out) == 0
+
+
+@pytest.mark.parametrize("case_name", ["case07_moe_grouped_gemm_fc1_dgrad", "case08_moe_grouped_gemm_fc2_dgrad",
+                                       "case13_grouped_gemm_single_group_fc1_dgrad",
+                                       "case19_grouped_gemm_single_group_fc2_dgrad"])
+def test_dgrad_reference_case_shapes(pkg, dev, case_name):
+    # The case's own Model and shapes (T=4096), checked in full against fp32 torch on the GPU.
+    case = getattr(pkg.cases, case_name)
+    dy, w = case.get_inputs(dev)
+    out = case.Model()(dy, w)
+    assert out.shape == (case.TOKENS, case.K)
+    off = 0
+    for gi, m in enumerate(case.group_sizes(case.TOKENS, case.NUM_GROUPS)):
+        ref = dy[off:off + m].float() @ w[gi].float()
+        _check(out[off:off + m], ref, f"{case_name} group {gi}")
+        off += m
+
+
+def test_case37_single_expert_dgrad(pkg, dev):
+    # Seeded inputs identical to the reference's make_inputs; its fp32 golden and its own rule.
+    case = pkg.cases.case37_ref_musa_asm_bf16_gemm_nn_256x384
+    grad_output, weight = case.make_inputs(seed=0, device=dev)
+    got = case.kernel_function(grad_output, weight)
+    golden = grad_output.float() @ weight.float()
+    diff = (got.float() - golden).abs()
+    max_rel = (diff / golden.abs().clamp(min=1.0)).max().item()
+    assert not (max_rel > 2e-2 and diff.max().item() > 2e-1)
+    _check(got, golden, "case37")
+
+
+# ------------------------------------------------------------------ wgrad
+@pytest.mark.parametrize("sizes,N,K", [
+    ([64], 256, 256),                       # one tile, one step
+    ([1], 8, 8),                            # degenerate
+    ([300, 0, 17, 513], 200, 264),          # ragged, empty group, N and K tails
+    ([102] * 5, 520, 1024),                 # case05/09 group size, K tail in the reduction
+    ([2048, 5], 128, 264),                  # long reduction
+])
+def test_wgrad_small(pkg, dev, sizes, N, K):
+    g = torch.Generator().manual_seed(3 * sum(sizes) + N + 5 * K)
+    dy = torch.randn(sum(sizes), N, generator=g).to(torch.bfloat16)
+    x = torch.randn(sum(sizes), K, generator=g).to(torch.bfloat16)
+    out = pkg.cases.case09_moe_grouped_gemm_fc1_wgrad.kernel_function(dy.to(dev), x.to(dev), sizes, len(sizes))
+    assert out.shape == (len(sizes), N, K)
+    _check(out, ref_torch.grouped_gemm_wgrad_fp32(dy, x, sizes), f"wgrad sizes={sizes} N={N} K={K}")
+    for gi, m in enumerate(sizes):
+        if m == 0:
+            assert torch.count_nonzero(out[gi]) == 0
+
+
+def test_wgrad_one_row_groups_exact(pkg, dev):
+    # A group of one row is the outer product dy[r] x[r]^T: exact in fp32, one rounding.
+    g = torch.Generator().manual_seed(91)
+    dy = torch.randn(5, 264, generator=g).to(torch.bfloat16)
+    x = torch.randn(5, 520, generator=g).to(torch.bfloat16)
+    out = pkg.ops.grouped_gemm_wgrad(dy.to(dev), x.to(dev), _offsets([1] * 5, dev)).cpu()
+    for r in range(5):
+        assert_bits_equal(out[r], torch.outer(dy[r].float(), x[r].float()).to(torch.bfloat16), f"row {r}")
+
+
+def test_wgrad_no_rows_gives_zeros_and_stays_in_bounds(pkg, dev):
+    G, N, K = 3, 72, 40
+    dy = torch.empty(0, N, dtype=torch.bfloat16, device=dev)
+    x = torch.empty(0, K, dtype=torch.bfloat16, device=dev)
+    buf = torch.full((G * N * K + 4096,), 5.0, dtype=torch.bfloat16, device=dev)
+    out = buf[:G * N * K].view(G, N, K)
+    pkg.ops.grouped_gemm_wgrad(dy, x, torch.zeros(G + 1, dtype=torch.int32, device=dev), out=out)
+    assert torch.count_nonzero(out) == 0
+    assert torch.all(buf[G * N * K:] == 5.0)
+
+
+@pytest.mark.parametrize("case_name", ["case05_moe_grouped_gemm_fc2_wgrad", "case09_moe_grouped_gemm_fc1_wgrad"])
+def test_wgrad_reference_case_shapes(pkg, dev, case_name):
+    case = getattr(pkg.cases, case_name)
+    dy, x = case.get_inputs(dev)
+    out = case.Model()(dy, x)
+    assert out.shape == (case.NUM_GROUPS, case.N, case.K)
+    off = 0
+    for gi, m in enumerate(case.group_sizes(case.TOKENS, case.NUM_GROUPS)):
+        ref = dy[off:off + m].float().t() @ x[off:off + m].float()
+        _check(out[gi], ref, f"{case_name} group {gi}")
+        off += m

@@ -275,6 +275,74 @@ def test_grouped_gemm_identity_weights_exact():
     assert torch.equal(got[:3], x[:3].float()) and torch.equal(got[3:], 2 * x[3:].float())
 
 
+def test_grouped_gemm_dgrad_fp32_against_float64():
+    # Brute force in float64 per group; a transposed w or a dropped group fails it.
+    g = torch.Generator().manual_seed(52)
+    sizes = [5, 0, 17, 1]
+    N, K = 24, 10
+    dy = torch.randn(sum(sizes), N, generator=g).to(torch.bfloat16)
+    w = torch.randn(len(sizes), N, K, generator=g).to(torch.bfloat16)
+    got = ref_torch.grouped_gemm_dgrad_fp32(dy, w, sizes)
+    assert got.shape == (sum(sizes), K)
+    d, ws = dy.double().numpy(), w.double().numpy()
+    off = 0
+    for gi, m in enumerate(sizes):
+        for r in range(m):
+            for c in range(K):
+                ref = sum(d[off + r, n] * ws[gi, n, c] for n in range(N))
+                assert abs(float(got[off + r, c]) - ref) <= 1e-5 * (1 + abs(ref))
+        off += m
+    bf = ref_torch.grouped_gemm_dgrad(dy, w, sizes)
+    torch.testing.assert_close(bf.float(), got, rtol=1.6e-2, atol=1e-2)
+
+
+def test_grouped_gemm_dgrad_is_forward_with_transposed_weights():
+    # dgrad(dy, w) = forward(dy, w^T): ties the dgrad oracle to the pinned forward one.
+    g = torch.Generator().manual_seed(53)
+    sizes = [3, 9, 0, 4]
+    N, K = 16, 24
+    dy = torch.randn(sum(sizes), N, generator=g).to(torch.bfloat16)
+    w = torch.randn(len(sizes), N, K, generator=g).to(torch.bfloat16)
+    a = ref_torch.grouped_gemm_dgrad_fp32(dy, w, sizes)
+    b = ref_torch.grouped_gemm_fp32(dy, w.transpose(1, 2).contiguous(), sizes)
+    torch.testing.assert_close(a, b, rtol=1e-6, atol=1e-6)
+
+
+def test_grouped_gemm_wgrad_fp32_against_float64():
+    # Sum of per-row outer products in float64; an empty group must come out zero.
+    g = torch.Generator().manual_seed(54)
+    sizes = [5, 0, 11, 1]
+    N, K = 12, 8
+    dy = torch.randn(sum(sizes), N, generator=g).to(torch.bfloat16)
+    x = torch.randn(sum(sizes), K, generator=g).to(torch.bfloat16)
+    got = ref_torch.grouped_gemm_wgrad_fp32(dy, x, sizes)
+    assert got.shape == (len(sizes), N, K)
+    d, xs = dy.double().numpy(), x.double().numpy()
+    off = 0
+    for gi, m in enumerate(sizes):
+        ref = np.zeros((N, K))
+        for r in range(off, off + m):
+            ref += np.outer(d[r], xs[r])
+        assert np.allclose(got[gi].numpy(), ref, rtol=1e-5, atol=1e-5)
+        off += m
+    assert torch.count_nonzero(got[1]) == 0
+    bf = ref_torch.grouped_gemm_wgrad(dy, x, sizes)
+    torch.testing.assert_close(bf.float(), got, rtol=1.6e-2, atol=1e-2)
+
+
+def test_grouped_gemm_wgrad_closed_forms():
+    # One row per group: dw[g] is the outer product of that row (exact in fp32 for bf16 inputs);
+    # one group over all rows: dw[0] = dy^T x.
+    g = torch.Generator().manual_seed(55)
+    dy = torch.randn(3, 8, generator=g).to(torch.bfloat16)
+    x = torch.randn(3, 16, generator=g).to(torch.bfloat16)
+    got = ref_torch.grouped_gemm_wgrad_fp32(dy, x, [1, 1, 1])
+    for r in range(3):
+        assert torch.equal(got[r], torch.outer(dy[r].float(), x[r].float()))
+    whole = ref_torch.grouped_gemm_wgrad_fp32(dy, x, [3])
+    torch.testing.assert_close(whole[0], got.sum(0), rtol=1e-6, atol=1e-6)
+
+
 def test_swiglu_closed_form():
     y = torch.tensor([[0.0, 1.0, 2.0, -3.0], [-1.0, 4.0, 0.5, 0.25]])
     h = ref_torch.swiglu(y).double().numpy()
