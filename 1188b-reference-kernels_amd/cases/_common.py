@@ -31,10 +31,29 @@ def check_scatter_shapes(inp: torch.Tensor, row_id_map: torch.Tensor) -> None:
         raise ValueError(f"shapes inp {tuple(inp.shape)} row_id_map {tuple(row_id_map.shape)}")
 
 
+_OFFSETS_CACHE: dict = {}
+
+
+def cached_offsets(m_splits, device) -> torch.Tensor:
+    """Device int32 [G+1] offsets of host group sizes, uploaded once per (sizes, device).
+
+    The case Models call their kernels with the same fixed sizes every time; the kernels only
+    read the offsets, so one copy per device serves every call.
+    """
+    key = (tuple(int(m) for m in m_splits), str(torch.device(device)))
+    t = _OFFSETS_CACHE.get(key)
+    if t is None:
+        if len(_OFFSETS_CACHE) >= 64:
+            _OFFSETS_CACHE.clear()
+        t = ops.group_offsets_from_splits(m_splits, device)
+        _OFFSETS_CACHE[key] = t
+    return t
+
+
 def _split_offsets(m_splits, total: int, groups: int, what: str, device):
     if len(m_splits) != groups or sum(m_splits) != total:
         raise ValueError(f"m_splits (len {len(m_splits)}, sum {sum(m_splits)}) does not match {what}")
-    return ops.group_offsets_from_splits(m_splits, device)
+    return cached_offsets(m_splits, device)
 
 
 def grouped_dgrad(dy: torch.Tensor, w: torch.Tensor, m_splits) -> torch.Tensor:

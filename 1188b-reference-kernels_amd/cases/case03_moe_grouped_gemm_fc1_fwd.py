@@ -12,6 +12,7 @@ from __future__ import annotations
 import torch
 
 from .. import inputs, ops
+from ._common import cached_offsets
 
 NUM_GROUPS = 40
 TOKENS = 4096
@@ -33,7 +34,7 @@ def kernel_function(x, w, m_splits=None, swiglu=False):
     if len(m_splits) != w.shape[0] or sum(m_splits) != x.shape[0]:
         raise ValueError(f"m_splits (len {len(m_splits)}, sum {sum(m_splits)}) does not match x {tuple(x.shape)} "
                          f"and w {tuple(w.shape)}")
-    offsets = ops.group_offsets_from_splits(m_splits, x.device)
+    offsets = cached_offsets(m_splits, x.device)
     return ops.grouped_gemm(x, w, offsets, swiglu=swiglu)
 
 

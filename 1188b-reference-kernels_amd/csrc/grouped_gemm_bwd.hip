@@ -25,16 +25,17 @@
 //
 // Kernel shape: persistent, one workgroup of 4 wavefronts per CU; output tile
 // kBM x 256 (kBM = 256: 2 x 2 waves of 128 x 128; kBM = 128: 1 x 4 waves of
-// 128 x 64, for groups of at most ~128 rows); reduction step 64; two-stage LDS
-// ring filled by buffer_load ... lds one step ahead of the MFMAs; the next
+// 128 x 64, for groups of at most ~160 rows); reduction step 64; LDS ring of
+// two stages (three for 128-row tiles, whose stream of w is HBM-bound and needs
+// two stages in flight) filled by buffer_load ... lds ahead of the MFMAs; the next
 // step's fragments are read while the current step's MFMAs run (as in the
 // forward kernel). The accumulators hold the transposed block (the column
 // operand is the MFMA's first operand); the epilogue rounds to bf16 (RNE,
 // hardware), pairs register groups across the two half-waves with
 // v_permlane32_swap so each lane holds 8 consecutive columns, and stores 16
 // bytes per lane straight from registers through a buffer resource (stores
-// past the tile's valid rows or columns are dropped), while the next tile's
-// first stage is already loading. Reduction rows past the end come from past
+// past the tile's valid rows or columns are dropped), after the next tile's
+// first stages have been issued. Reduction rows past the end come from past
 // the operand's buffer resource and read as zeros (dgrad's dy columns past N
 // are zeroed in LDS).
 //
@@ -55,7 +56,6 @@ typedef __attribute__((address_space(3))) v4bf16 lds_v4bf16;
 
 constexpr int kBN = 256;            // output columns per tile
 constexpr int kGroupM = 8;          // row tiles per tile-order patch
-constexpr int kStages = 2;
 constexpr int kSubSteps = kBK / 16;
 constexpr int kKCRow = kBK * 2;     // 128-byte rows of a KC operand tile
 constexpr int kRMRow = 256 * 2;     // 512-byte rows of an RM operand tile (256 columns)
@@ -98,7 +98,7 @@ __device__ __forceinline__ bf16x8 read_rm_frag(uint32_t addr) {
 #endif
 }
 
-template <bool kWgrad, int kBM, int kWavesM>
+template <bool kWgrad, int kBM, int kWavesM, int kStages>
 __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
   constexpr int kWaves = 4;
   constexpr int kWavesN = kWaves / kWavesM;
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
   constexpr int kReads = (kARM ? 2 * kMI : kMI) + 2 * kNI;  // LDS reads per sub-step
   constexpr int kMfma = kMI * kNI;              // MFMAs per sub-step
   static_assert(kStages * kStageBytes <= 160 * 1024, "LDS budget");
-  static_assert(kStores + kDmaA + kDmaB <= 63, "vmcnt range");
+  static_assert(kStores + (kStages - 1) * (kDmaA + kDmaB) <= 63, "vmcnt range");
   static_assert(!kARM || kBM == 256, "a reduction-major A tile is 256 columns wide");
   __shared__ __attribute__((aligned(1024))) char smem[kStages * kStageBytes];
   lds_char *const sbase = (lds_char *)smem;
@@ -297,12 +297,13 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
   Tile cur;
   if (!find_tile(0, cur)) return;
   setup_dma(cur);
-  issue_a(0, 0);
-  issue_b(0, 0);
-  // Stage 1 (a re-read of stage 0 into the unused slot when there is one
-  // step, so the count of outstanding loads is the same for every tile).
-  issue_a(min(1, cur.ktiles - 1), 1);
-  issue_b(min(1, cur.ktiles - 1), 1);
+  // Every stage slot is filled (stages past the last re-read the last one), so
+  // the count of outstanding loads is the same for every tile.
+#pragma unroll
+  for (int st = 0; st < kStages; ++st) {
+    issue_a(min(st, cur.ktiles - 1), st);
+    issue_b(min(st, cur.ktiles - 1), st);
+  }
 
   for (int64_t round = 0;; ++round) {
 #pragma unroll
@@ -310,12 +311,12 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
 #pragma unroll
       for (int j = 0; j < kNI; ++j) acc[i][j] = f32x16{};
 
-    // Stage 0 has landed. Younger: stage 1 and, after the first tile, the
-    // previous tile's output stores issued between the two stages.
+    // Stage 0 has landed. Younger: the other prefetched stages and, after the
+    // first tile, the previous tile's output stores (issued after them).
     if (round == 0) {
-      wait_vm_n<kDmaA + kDmaB>();
+      wait_vm_n<(kStages - 1) * (kDmaA + kDmaB)>();
     } else {
-      wait_vm_n<kStores + kDmaA + kDmaB>();
+      wait_vm_n<kStores + (kStages - 1) * (kDmaA + kDmaB)>();
     }
     barrier();
     const int ktiles = cur.ktiles;
@@ -333,7 +334,22 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
       __builtin_amdgcn_sched_barrier(0);
       // This thread's DMA of stage kt + 1 has landed and its reads of stage kt
       // are done; after the barrier, everyone's.
-      wait_dma();
+      // Stage kt + 1 has landed. Younger and allowed to be in flight: stage
+      // kt + 2 (three stages) and, in the first steps after a tile change, the
+      // previous tile's output stores, issued after this tile's first stages.
+      if constexpr (kStages == 2) {
+        if (kt == 0 && round > 0) {
+          wait_vm_n<kStores>();
+        } else {
+          wait_dma();
+        }
+      } else {
+        if (kt <= kStages - 2 && round > 0) {
+          wait_vm_n<(kStages - 2) * (kDmaA + kDmaB) + kStores>();
+        } else {
+          wait_vm_n<(kStages - 2) * (kDmaA + kDmaB)>();
+        }
+      }
       wait_lds();
       barrier();
       if (a_ktail && kt + 1 == ktiles - 1) {
@@ -343,15 +359,15 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
       }
       // Stage kt + 2 into the slot of stage kt (the last step re-reads the
       // final stage into that free slot, so the region below has no branch).
-      const int kdma = min(kt + 2, ktiles - 1);
+      const int kdma = min(kt + kStages, ktiles - 1);
       set_read_slot(kt + 1);
       read_frags(0);
       mfma_ks(1);
-      issue_a(kdma, kt + 2);
+      issue_a(kdma, kt + kStages);
       sched_mix<kMfma, kReads, kDmaA>();
       mfma_ks(2);
       read_frags(1);
-      issue_b(kdma, kt + 2);
+      issue_b(kdma, kt + kStages);
       sched_mix<kMfma, kReads, kDmaB>();
       mfma_ks(3);
       read_frags(2);
@@ -364,8 +380,9 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
     mfma_ks(2);
     mfma_ks(3);
 
-    // No DMA in flight and every wave done reading the ring: the next tile's
-    // stage 0 loads during this tile's epilogue, its stage 1 after the stores.
+    // No DMA in flight and every wave done reading the ring: all prefetched
+    // stages of the next tile are issued before this tile's output stores, so
+    // the next tile's first waits do not wait for the stores.
     wait_dma();
     wait_lds();
     barrier();
@@ -373,8 +390,11 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
     const bool more = find_tile(round + 1, nxt);
     if (more) {
       setup_dma(nxt);
-      issue_a(0, 0);
-      issue_b(0, 0);
+#pragma unroll
+      for (int st = 0; st < kStages; ++st) {
+        issue_a(min(st, nxt.ktiles - 1), st);
+        issue_b(min(st, nxt.ktiles - 1), st);
+      }
     }
 
     // Epilogue straight from registers. Register r of lane l in block (i, j)
@@ -432,17 +452,15 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
       }
     }
     if (!more) break;
-    issue_a(min(1, nxt.ktiles - 1), 1);
-    issue_b(min(1, nxt.ktiles - 1), 1);
     cur = nxt;
   }
 }
 
-template <bool kWgrad, int kBM, int kWavesM>
+template <bool kWgrad, int kBM, int kWavesM, int kStages>
 void launch(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
   int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
   grid = std::max<int64_t>(8, (grid + 7) / 8 * 8);
-  grouped_gemm_bwd_kernel<kWgrad, kBM, kWavesM><<<dim3(grid), dim3(256), 0, s>>>(p);
+  grouped_gemm_bwd_kernel<kWgrad, kBM, kWavesM, kStages><<<dim3(grid), dim3(256), 0, s>>>(p);
 }
 
 }  // namespace
@@ -502,9 +520,9 @@ int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, con
   // 128-row tiles when the groups average at most 160 rows (less padding in
   // every group's last row tile), 256-row tiles otherwise.
   if (M_total <= 160 * G) {
-    launch<false, 128, 1>(p, (ceil_div(M_total, 128) + G) * p.ntiles, s);
+    launch<false, 128, 1, 3>(p, (ceil_div(M_total, 128) + G) * p.ntiles, s);
   } else {
-    launch<false, 256, 2>(p, (ceil_div(M_total, 256) + G) * p.ntiles, s);
+    launch<false, 256, 2, 2>(p, (ceil_div(M_total, 256) + G) * p.ntiles, s);
   }
   return check_launch(fn);
 }
@@ -540,7 +558,7 @@ int moe_grouped_gemm_wgrad(const moe_bf16_t *dy, const moe_bf16_t *x, int64_t M_
   p.K = K;
   p.G = G;
   p.ntiles = ceil_div(K, kBN);
-  launch<true, 256, 2>(p, G * ceil_div(N, 256) * p.ntiles, static_cast<hipStream_t>(stream));
+  launch<true, 256, 2, 2>(p, G * ceil_div(N, 256) * p.ntiles, static_cast<hipStream_t>(stream));
   return check_launch(fn);
 }
 

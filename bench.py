@@ -12,7 +12,10 @@ kernels of this repository on torch's current stream:
   fc1 + SwiGLU (grouped GEMM gathering its A rows from x, i.e. the permute
   fused into fc1) -> fc2 (grouped GEMM) -> merge unpermute.
 The stand-alone permute kernel (x -> permuted rows) is timed separately on the
-same map, after the timed steps, and reported under "standalone".
+same map, after the timed steps, and reported under "standalone"; the four
+grouped GEMMs of the layer's backward (dgrad and wgrad of fc1 and fc2, on the
+same routing) and the reference backward cases at their own shapes are timed
+after that and reported under "backward" (neither is part of `value`).
 
 Prints ONE JSON line: tokens/s of the whole step, per-stage device times
 (HIP events on the launch stream, averaged over the timed steps) with their
@@ -116,6 +119,73 @@ def library_reference(m, kdim, n, groups, dev, reps=5):
             "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2)}
 
 
+def _time_ms(fn, reps=5, warm=2):
+    for _ in range(warm):
+        fn()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record()
+    for _ in range(reps):
+        fn()
+    ev[1].record()
+    torch.cuda.synchronize()
+    return ev[0].elapsed_time(ev[1]) / reps
+
+
+def backward_gemms(pkg, x, row_map, offs, h, w1, w2, dev, library=False):
+    """The grouped GEMMs of the layer's backward on this batch's routing (not part of the timed step).
+
+    dz [R, H] and dy1 [R, 2F] are synthetic N(0,1) gradients; xp = the permuted x.  fc2 dgrad
+    dh = dz @ W2[e]; fc2 wgrad dW2[e] = dz^T h; fc1 dgrad dxp = dy1 @ W1[e]; fc1 wgrad dW1[e] = dy1^T xp.
+    Also the reference backward cases at their own shapes (uniform groups, T=4096).
+    """
+    ops, inp = pkg.ops, pkg.inputs
+    R, H = h.shape[0], x.shape[1]
+    F2 = w1.shape[1]
+    dz = inp.randn_bf16((R, H), seed=SEED + 30, device=dev)
+    dy1 = inp.randn_bf16((R, F2), seed=SEED + 40, device=dev)
+    xp, _ = ops.permute(x, row_map, num_out=R, layout=ops.TOKEN_MAJOR, zero_tail=False)
+    E = w1.shape[0]
+    runs = {
+        "fc2_dgrad": (lambda: ops.grouped_gemm_dgrad(dz, w2, offs), 2 * R * H * w2.shape[2]),
+        "fc2_wgrad": (lambda: ops.grouped_gemm_wgrad(dz, h, offs), 2 * R * H * h.shape[1]),
+        "fc1_dgrad": (lambda: ops.grouped_gemm_dgrad(dy1, w1, offs), 2 * R * F2 * H),
+        "fc1_wgrad": (lambda: ops.grouped_gemm_wgrad(dy1, xp, offs), 2 * R * F2 * H),
+    }
+    out = {}
+    for name, (fn, flops) in runs.items():
+        ms = _time_ms(fn)
+        out[name] = {"ms": round(ms, 4), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2),
+                     "frac_of_peak": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4), "flops": flops}
+    if library:
+        m = R // E
+        a = torch.randn(E, m, H, device=dev, dtype=torch.bfloat16)
+        b = torch.randn(E, H, w2.shape[2], device=dev, dtype=torch.bfloat16)
+        out["library_fc2_dgrad_bmm_ms"] = round(_time_ms(lambda: torch.bmm(a, b)), 4)
+        del a, b
+    del dz, dy1, xp
+    cases = {}
+    for name, kind in [("case07_moe_grouped_gemm_fc1_dgrad", "dgrad"), ("case08_moe_grouped_gemm_fc2_dgrad", "dgrad"),
+                       ("case13_grouped_gemm_single_group_fc1_dgrad", "dgrad"),
+                       ("case19_grouped_gemm_single_group_fc2_dgrad", "dgrad"),
+                       ("case05_moe_grouped_gemm_fc2_wgrad", "wgrad"), ("case09_moe_grouped_gemm_fc1_wgrad", "wgrad")]:
+        case = getattr(pkg.cases, name)
+        a, b = case.get_inputs(dev)
+        model = case.Model()
+        ms = _time_ms(lambda: model(a, b))
+        T, N, K, G = case.TOKENS, case.N, case.K, case.NUM_GROUPS
+        flops = 2 * T * N * K
+        hbm = 2 * (T * N + (G * N * K if kind == "dgrad" else T * K) + (T * K if kind == "dgrad" else G * N * K))
+        cases[name.split("_")[0]] = {"ms": round(ms, 4), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2),
+                                     "GB/s": round(hbm / (ms * 1e-3) / 1e9, 2), "bytes": hbm}
+        del a, b
+    case = pkg.cases.case37_ref_musa_asm_bf16_gemm_nn_256x384
+    g, w = case.make_inputs(seed=0, device=dev)
+    ms = _time_ms(lambda: case.kernel_function(g, w))
+    cases["case37"] = {"ms": round(ms, 4), "TFLOP/s": round(2 * case.M * case.K * case.N / (ms * 1e-3) / 1e12, 2)}
+    out["reference_cases"] = cases
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -128,6 +198,8 @@ def main():
     ap.add_argument("--library-reference", action="store_true",
                     help="also time torch.bmm (hipBLASLt) on the fc1 shape with equal groups "
                          "(E x [R/E, H] @ [H, 2F]): a library GEMM of the same size, reported beside the stages")
+    ap.add_argument("--no-backward", action="store_true",
+                    help="skip the backward grouped GEMMs (reported beside the forward, not in value)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the MoE dispatch path here has no multi-GPU (expert-parallel) "
@@ -229,6 +301,14 @@ def main():
         torch.cuda.synchronize()
         del src
 
+    backward = None
+    if not args.no_backward:
+        b = layer._buffers(T, dev)
+        _, _, mask, _ = ops.topk(logits, k, with_mask=True, with_probs=True)
+        maps = ops.row_id_map(mask, expert_major=False, token_major=True, expert_offsets=True, workspace=b["ws"])
+        backward = backward_gemms(pkg, x, maps["token_major"], maps["expert_offsets"], b["h"], w1, w2, dev,
+                                  library=args.library_reference)
+
     library = None
     if args.library_reference:
         library = library_reference(T * k // E, H, 2 * F, E, dev)
@@ -250,6 +330,8 @@ def main():
         "cpu_baseline": cpu,
         "device": torch.cuda.get_device_name(0),
     }
+    if backward is not None:
+        line["backward"] = backward
     if library is not None:
         line["library_reference"] = library
     print(json.dumps(line))
