@@ -35,7 +35,7 @@ MOE_MAP_EXPERT_MAJOR = 1
 MOE_EPILOGUE_NONE = 0
 MOE_EPILOGUE_SWIGLU = 1
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -60,6 +60,8 @@ SIGNATURES = {
     "moe_grouped_gemm_gather": (_int, [_p, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _int, _p, _p, _sz, _p]),
     "moe_grouped_gemm_dgrad": (_int, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _sz, _p]),
     "moe_grouped_gemm_wgrad": (_int, [_p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _sz, _p]),
+    "moe_router_logits": (_int, [_p, _i64, _i64, _p, _i64, _p, _p]),
+    "moe_router_topk": (_int, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _p]),
 }
 
 _LIB = None

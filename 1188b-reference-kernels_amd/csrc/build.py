@@ -30,6 +30,7 @@ SOURCES = [
     "index_select.hip",
     "grouped_gemm.hip",
     "grouped_gemm_bwd.hip",
+    "router.hip",
 ]
 
 ARCH = os.environ.get("MOE_OFFLOAD_ARCH", "gfx950")

@@ -1,0 +1,295 @@
+// Router gate GEMM (logits in fp32 from bf16 inputs), optionally fused with
+// the router top-k, routing mask and merge probs.
+//
+// Math: kernel_cases/case38_ref_musa_asm_bf16_ssgemm_nt_320x256.py:46-53
+// (reference_fp32): logits[M, N] = inp[M, K] @ weight[N, K]^T, bf16 in, fp32
+// accumulate, fp32 out (moe_router_dtype=fp32, :8-13).  The fused top-k is the
+// routine of topk_device.h (case23_ref_aten_topk.py:47-62; mask and probs as
+// moe_topk) applied to each logits row.
+//
+// Kernel shape (gfx950): one workgroup of 4 wavefronts per 64-row tile that
+// holds all N (<= 512) columns, so one workgroup owns whole logits rows; each
+// wavefront computes 64 rows x 16 kNB columns as 4 x kNB blocks of
+// v_mfma_f32_16x16x32_bf16 (the weight fragment is the first operand, so a
+// lane holds 4 consecutive columns of one row).  A and weight tiles stream
+// through a 3-stage LDS ring (2 stages when N > 320) filled by
+// buffer_load ... lds two steps ahead; rows are 128 bytes with 16-byte chunks
+// XOR-swizzled by (row / 2) % 8.  The epilogue stages the fp32 tile in LDS
+// (row stride 16 bytes past a multiple of 256: conflict-free 16-byte writes),
+// stores the logits rows coalesced and, fused, runs the per-row top-k with one
+// wavefront per row reading its row from LDS.
+#include <algorithm>
+
+#include "gemm_device.h"
+#include "topk_device.h"
+
+namespace moe {
+namespace {
+
+using namespace gemm;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+typedef __attribute__((address_space(3))) float lds_f32;
+
+constexpr int kBM = 64;
+constexpr int kRow = kBK * 2;  // 128-byte LDS rows
+
+struct RouterArgs {
+  const uint16_t *inp;  // [M, K]
+  const uint16_t *w;    // [N, K]
+  float *logits;        // [M, N] or nullptr
+  int64_t M, K;
+  int N, k;
+  float *values;         // top-k: [M, k]
+  int64_t *indices;      // top-k: [M, k]
+  uint8_t *routing_map;  // top-k: [M, N] or nullptr
+  float *probs;          // top-k: [M, N] or nullptr
+  int vec_logits;        // logits rows are 16-byte aligned (N % 4 == 0, aligned base)
+};
+
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+
+template <int kNB, bool kTopk>
+__global__ __launch_bounds__(256) void router_kernel(RouterArgs p) {
+  constexpr int kWaves = 4;
+  constexpr int kNT = 64 * kNB;                 // weight rows (logits columns) per tile
+  constexpr int kABytes = kBM * kRow;           // 8 KiB
+  constexpr int kBBytes = kNT * kRow;
+  constexpr int kStageBytes = kABytes + kBBytes;
+  constexpr int kStages = 3 * kStageBytes <= 150 * 1024 ? 3 : 2;
+  constexpr int kDmaA = kABytes / 1024 / kWaves;  // 2
+  constexpr int kDmaB = kBBytes / 1024 / kWaves;  // 2 kNB
+  constexpr int kDma = kDmaA + kDmaB;
+  constexpr int kEpiStride = kNT * 4 + 16;      // fp32 logits row in LDS
+  constexpr int kRingBytes = kStages * kStageBytes;
+  constexpr int kLdsBytes = kRingBytes > kBM * kEpiStride ? kRingBytes : kBM * kEpiStride;
+  static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+  static_assert((kStages - 1) * kDma <= 63, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
+  lds_char *const sbase = (lds_char *)smem;
+  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sbase));
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t K = p.K;
+  const int N = p.N;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kBM;
+  const int rows_valid = static_cast<int>(min(p.M - row0, int64_t(kBM)));
+  const int ktiles = static_cast<int>(ceil_div(K, kBK));
+  const bool ktail = (K % kBK) != 0;
+
+  // DMA: 1 KiB blocks of 8 rows; lane -> (row, logical chunk) of its 16 bytes.
+  const __amdgpu_buffer_rsrc_t ra =
+      make_rsrc(p.inp + row0 * K, static_cast<uint32_t>(rows_valid) * static_cast<uint32_t>(K) * 2u);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.w, static_cast<uint32_t>(N) * static_cast<uint32_t>(K) * 2u);
+  const uint32_t row_bytes = static_cast<uint32_t>(K) * 2u;
+  int a_off[kDmaA], b_off[kDmaB];
+#pragma unroll
+  for (int j = 0; j < kDmaA; ++j) {
+    const int r = (j * kWaves + wave) * 8 + (lane >> 3);
+    a_off[j] = static_cast<int>(static_cast<uint32_t>(min(r, rows_valid - 1)) * row_bytes + (((lane & 7) ^ swz(r)) << 4));
+  }
+#pragma unroll
+  for (int j = 0; j < kDmaB; ++j) {
+    const int r = (j * kWaves + wave) * 8 + (lane >> 3);
+    b_off[j] = static_cast<int>(static_cast<uint32_t>(min(r, N - 1)) * row_bytes + (((lane & 7) ^ swz(r)) << 4));
+  }
+  auto issue = [&](int kt, int slot) {
+    const uint32_t st = lds_base + (slot % kStages) * kStageBytes;
+    const int soff = kt * kBK * 2;
+#pragma unroll
+    for (int j = 0; j < kDmaA; ++j)
+      dma16b(ra, (lds_void *)(uintptr_t)(st + (j * kWaves + wave) * 1024), a_off[j], soff);
+#pragma unroll
+    for (int j = 0; j < kDmaB; ++j)
+      dma16b(rb, (lds_void *)(uintptr_t)(st + kABytes + (j * kWaves + wave) * 1024), b_off[j], soff);
+  };
+  // Chunks past K in the last stage read the next row (or zeros): zero them.
+  auto zero_ktail = [&](int kt) {
+    lds_char *st = sbase + (kt % kStages) * kStageBytes;
+    const int kvalid = static_cast<int>(K - static_cast<int64_t>(kt) * kBK);
+    for (int idx = tid; idx < (kBM + kNT) * 8; idx += kWaves * 64) {
+      const int r = idx >> 3, c = idx & 7;
+      if (c * 8 >= kvalid) *reinterpret_cast<lds_u32x4 *>(st + r * kRow + ((c ^ swz(r)) << 4)) = u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+
+  // Fragments of v_mfma_f32_16x16x32_bf16: lane l reads row (block + l % 16),
+  // the 8 values k = 8 (l / 16) .. + 7 of the sub-step (logical chunk 4 ks + l / 16).
+  const int frow = lane & 15, fq = lane >> 4;
+  int fa_base[4], fb_base[kNB];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = i * 16 + frow;
+    fa_base[i] = r * kRow;
+  }
+#pragma unroll
+  for (int j = 0; j < kNB; ++j) {
+    const int r = wave * 16 * kNB + j * 16 + frow;
+    fb_base[j] = kABytes + r * kRow;
+  }
+  auto frag_addr = [&](uint32_t slot_base, int base, int r, int ks) {
+    return slot_base + base + ((((ks << 2) | fq) ^ swz(r)) << 4);
+  };
+
+  f32x4 acc[4][kNB];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < kNB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Prologue: stages 0 .. kStages - 2 (re-reads past the last stage keep the
+  // count of outstanding loads fixed).
+#pragma unroll
+  for (int s = 0; s < kStages - 1; ++s) issue(min(s, ktiles - 1), s);
+
+  for (int kt = 0; kt < ktiles; ++kt) {
+    // Stage kt has landed (younger: kStages - 2 stages); after the barrier,
+    // every wave's, and every wave is done with stage kt - 1's slot.
+    wait_vm_n<(kStages - 2) * kDma>();
+    wait_lds();
+    barrier();
+    if (ktail && kt == ktiles - 1) {
+      zero_ktail(kt);
+      wait_lds();
+      barrier();
+    }
+    issue(min(kt + kStages - 1, ktiles - 1), kt + kStages - 1);
+    const uint32_t sb = lds_base + (kt % kStages) * kStageBytes;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bf16x8 fa[4], fb[kNB];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        fa[i] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)frag_addr(sb, fa_base[i], i * 16 + frow, ks));
+#pragma unroll
+      for (int j = 0; j < kNB; ++j)
+        fb[j] = *reinterpret_cast<const lds_bf16x8 *>(
+            (uintptr_t)frag_addr(sb, fb_base[j], wave * 16 * kNB + j * 16 + frow, ks));
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < kNB; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
+    }
+  }
+  wait_dma();  // the re-reads of the last steps
+  wait_lds();
+  barrier();
+
+  // Epilogue. acc[i][j] register r of lane l: logits row i * 16 + l % 16,
+  // column wave * 16 kNB + j * 16 + 4 (l / 16) + r.
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = i * 16 + frow;
+#pragma unroll
+    for (int j = 0; j < kNB; ++j) {
+      const int c = wave * 16 * kNB + j * 16 + fq * 4;
+      *reinterpret_cast<lds_f32x4 *>(sbase + r * kEpiStride + c * 4) = acc[i][j];
+    }
+  }
+  wait_lds();
+  barrier();
+  if (p.logits != nullptr) {
+    float *out = p.logits + row0 * N;
+    if (p.vec_logits) {
+      const int cpr = N / 4;  // 16-byte chunks per row
+      for (int idx = tid; idx < rows_valid * cpr; idx += kWaves * 64) {
+        const int r = idx / cpr, c = idx - r * cpr;
+        *reinterpret_cast<f32x4 *>(out + static_cast<int64_t>(r) * N + c * 4) =
+            *reinterpret_cast<const lds_f32x4 *>(sbase + r * kEpiStride + c * 16);
+      }
+    } else {
+      for (int idx = tid; idx < rows_valid * N; idx += kWaves * 64) {
+        const int r = idx / N, c = idx - r * N;
+        out[static_cast<int64_t>(r) * N + c] = *reinterpret_cast<const lds_f32 *>(sbase + r * kEpiStride + c * 4);
+      }
+    }
+  }
+  if constexpr (kTopk) {
+    constexpr int kEPL = kNB;  // ceil(N / 64) elements per lane
+    for (int r = wave; r < rows_valid; r += kWaves) {
+      const lds_char *rowp = sbase + r * kEpiStride;
+      topk_row<kEPL>([&](int e) { return *reinterpret_cast<const lds_f32 *>(rowp + e * 4); }, row0 + r, N, p.k,
+                     p.values, p.indices, p.routing_map, p.probs);
+    }
+  }
+}
+
+template <bool kTopk>
+void launch_router(const RouterArgs &p, int64_t grid, hipStream_t s) {
+  const int nb = static_cast<int>(ceil_div(p.N, 64));
+  switch (nb) {
+    case 1: router_kernel<1, kTopk><<<dim3(grid), dim3(256), 0, s>>>(p); break;
+    case 2: router_kernel<2, kTopk><<<dim3(grid), dim3(256), 0, s>>>(p); break;
+    case 3: router_kernel<3, kTopk><<<dim3(grid), dim3(256), 0, s>>>(p); break;
+    case 4: router_kernel<4, kTopk><<<dim3(grid), dim3(256), 0, s>>>(p); break;
+    case 5: router_kernel<5, kTopk><<<dim3(grid), dim3(256), 0, s>>>(p); break;
+    case 6: router_kernel<6, kTopk><<<dim3(grid), dim3(256), 0, s>>>(p); break;
+    case 7: router_kernel<7, kTopk><<<dim3(grid), dim3(256), 0, s>>>(p); break;
+    default: router_kernel<8, kTopk><<<dim3(grid), dim3(256), 0, s>>>(p); break;
+  }
+}
+
+int launch(const char *fn, const moe_bf16_t *inp, int64_t M, int64_t K, const moe_bf16_t *weight, int64_t N,
+           int64_t k, float *logits, float *values, int64_t *indices, uint8_t *routing_map, float *probs,
+           bool topk, void *stream) {
+  if (M < 0 || K < 0 || N < 0) {
+    return fail(MOE_ERR_SHAPE, "%s: negative size (M=%lld K=%lld N=%lld)", fn, (long long)M, (long long)K,
+                (long long)N);
+  }
+  if (N < 1 || N > 512) return fail(MOE_ERR_CAPACITY, "%s: N=%lld outside [1, 512]", fn, (long long)N);
+  if (K % 8 != 0 || K == 0) return fail(MOE_ERR_SHAPE, "%s: K=%lld must be a positive multiple of 8", fn, (long long)K);
+  if (K > (int64_t(1) << 22) - 8 || N * K > (int64_t(1) << 30) - 1) {
+    return fail(MOE_ERR_CAPACITY, "%s: K=%lld N=%lld exceed the 32-bit offsets (K < 2^22, N*K < 2^30)", fn,
+                (long long)K, (long long)N);
+  }
+  if (topk) {
+    if (k < 1 || k > N) return fail(MOE_ERR_SHAPE, "%s: k=%lld out of range for N=%lld", fn, (long long)k, (long long)N);
+    if (k > 64) return fail(MOE_ERR_CAPACITY, "%s: k=%lld exceeds the 64 supported", fn, (long long)k);
+  }
+  if (M == 0) return MOE_OK;
+  if (inp == nullptr || weight == nullptr) return fail(MOE_ERR_INVALID_ARG, "%s: null inp or weight", fn);
+  if (!topk && logits == nullptr) return fail(MOE_ERR_INVALID_ARG, "%s: null logits", fn);
+  if (topk && (values == nullptr || indices == nullptr)) return fail(MOE_ERR_INVALID_ARG, "%s: null values or indices", fn);
+  if (!is_aligned(inp, 16) || !is_aligned(weight, 16)) return fail(MOE_ERR_ALIGN, "%s: inp and weight must be 16-byte aligned", fn);
+  if (ceil_div(M, kBM) > 0x7fffffff) return fail(MOE_ERR_CAPACITY, "%s: M=%lld too large", fn, (long long)M);
+  RouterArgs p;
+  p.inp = inp;
+  p.w = weight;
+  p.logits = logits;
+  p.M = M;
+  p.K = K;
+  p.N = static_cast<int>(N);
+  p.k = static_cast<int>(k);
+  p.values = values;
+  p.indices = indices;
+  p.routing_map = routing_map;
+  p.probs = probs;
+  p.vec_logits = (N % 4 == 0) && is_aligned(logits, 16);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (topk) launch_router<true>(p, ceil_div(M, kBM), s);
+  else launch_router<false>(p, ceil_div(M, kBM), s);
+  return check_launch(fn);
+}
+
+}  // namespace
+}  // namespace moe
+
+extern "C" {
+
+int moe_router_logits(const moe_bf16_t *inp, int64_t M, int64_t K, const moe_bf16_t *weight, int64_t N,
+                      float *logits, void *stream) {
+  return moe::launch("moe_router_logits", inp, M, K, weight, N, 0, logits, nullptr, nullptr, nullptr, nullptr,
+                     false, stream);
+}
+
+int moe_router_topk(const moe_bf16_t *inp, int64_t M, int64_t K, const moe_bf16_t *weight, int64_t N, int64_t k,
+                    float *logits, float *values, int64_t *indices, uint8_t *routing_map, float *probs,
+                    void *stream) {
+  return moe::launch("moe_router_topk", inp, M, K, weight, N, k, logits, values, indices, routing_map, probs, true,
+                     stream);
+}
+
+}  // extern "C"

@@ -74,6 +74,59 @@ def topk(logits: torch.Tensor, k: int, *, with_mask: bool = False, with_probs: b
     return tuple(out)
 
 
+def router_logits(inp: torch.Tensor, weight: torch.Tensor, *, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Router gate GEMM: inp [M, K] bf16 @ weight [N, K]^T bf16 -> fp32 logits [M, N] (fp32 accumulate)."""
+    _on_gpu("inp", inp)
+    _on_gpu("weight", weight)
+    _dtype("inp", inp, torch.bfloat16)
+    _dtype("weight", weight, torch.bfloat16)
+    if inp.ndim != 2 or weight.ndim != 2 or inp.shape[1] != weight.shape[1]:
+        raise ValueError(f"shapes inp {tuple(inp.shape)} weight {tuple(weight.shape)}: need [M,K] and [N,K]")
+    M, K = inp.shape
+    N = weight.shape[0]
+    ic, wc = inp.contiguous(), weight.contiguous()
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.float32, device=inp.device)
+    call("moe_router_logits", ptr(ic), M, K, ptr(wc), N, ptr(out), stream_handle())
+    return out
+
+
+def router_topk(inp: torch.Tensor, weight: torch.Tensor, k: int, *, with_logits: bool = False,
+                with_mask: bool = False, with_probs: bool = False):
+    """router_logits followed by topk on its rows, fused in one kernel.
+
+    Returns (values, indices) and, on request and in this order, the fp32 logits [M, N],
+    the routing mask bool [M, N] and the merge probs fp32 [M, N] -- the outputs of topk.
+    """
+    _on_gpu("inp", inp)
+    _on_gpu("weight", weight)
+    _dtype("inp", inp, torch.bfloat16)
+    _dtype("weight", weight, torch.bfloat16)
+    if inp.ndim != 2 or weight.ndim != 2 or inp.shape[1] != weight.shape[1]:
+        raise ValueError(f"shapes inp {tuple(inp.shape)} weight {tuple(weight.shape)}: need [M,K] and [N,K]")
+    M, K = inp.shape
+    N = weight.shape[0]
+    if not (1 <= k <= N):
+        raise ValueError(f"k={k} out of range for N={N}")
+    ic, wc = inp.contiguous(), weight.contiguous()
+    dev = inp.device
+    values = torch.empty(M, k, dtype=torch.float32, device=dev)
+    indices = torch.empty(M, k, dtype=torch.int64, device=dev)
+    logits = torch.empty(M, N, dtype=torch.float32, device=dev) if with_logits else None
+    mask = torch.empty(M, N, dtype=torch.bool, device=dev) if with_mask else None
+    probs = torch.empty(M, N, dtype=torch.float32, device=dev) if with_probs else None
+    call("moe_router_topk", ptr(ic), M, K, ptr(wc), N, k, ptr(logits), ptr(values), ptr(indices),
+         ptr(mask.view(torch.uint8)) if mask is not None else None, ptr(probs), stream_handle())
+    out = [values, indices]
+    if with_logits:
+        out.append(logits)
+    if with_mask:
+        out.append(mask)
+    if with_probs:
+        out.append(probs)
+    return tuple(out)
+
+
 # ---------------------------------------------------------------- row-id map
 def row_id_map(routing_map: torch.Tensor, *, expert_major: bool = True, token_major: bool = True,
                expert_major_i32: bool = False, expert_offsets: bool = False,

@@ -35,6 +35,7 @@
  *   case07/08/13/19 (and case37) kernel_cases/case07_moe_grouped_gemm_fc1_dgrad.py:57-64
  *                 (dgrad, no bundle)
  *   case05/case09 kernel_cases/case09_moe_grouped_gemm_fc1_wgrad.py:57-64 (wgrad, no bundle)
+ *   case38        kernel_cases/case38_ref_musa_asm_bf16_ssgemm_nt_320x256.py:46-53 (router logits)
  */
 #ifndef MOE_DISPATCH_H_
 #define MOE_DISPATCH_H_
@@ -46,7 +47,7 @@
 extern "C" {
 #endif
 
-#define MOE_DISPATCH_ABI_VERSION 3
+#define MOE_DISPATCH_ABI_VERSION 4
 
 typedef uint16_t moe_bf16_t;
 
@@ -251,6 +252,27 @@ int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, con
 int moe_grouped_gemm_wgrad(const moe_bf16_t *dy, const moe_bf16_t *x, int64_t M_total, int64_t N,
                            int64_t K, int64_t G, const int32_t *group_offsets, moe_bf16_t *dw,
                            void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---- router gate GEMM (logits) -------------------------------------------
+ * Replaces case38's router GEMM te_general_gemm(weight, inp, out_dtype=fp32,
+ * layout="TN") (kernel_cases/case38_ref_musa_asm_bf16_ssgemm_nt_320x256.py:1-35;
+ * golden reference_fp32 :46-53): logits = inp @ weight^T, bf16 in, fp32
+ * accumulate, fp32 out.
+ *   inp    bf16 [M, K];  weight bf16 [N, K] (num_experts x hidden)
+ *   logits fp32 [M, N]
+ * Limits: 1 <= N <= 512, K % 8 == 0, K < 2^22, N * K < 2^30; inp and weight
+ *   16-byte aligned.  Workspace: none. */
+int moe_router_logits(const moe_bf16_t *inp, int64_t M, int64_t K, const moe_bf16_t *weight, int64_t N,
+                      float *logits, void *stream);
+
+/* ---- router gate GEMM fused with top-k, routing mask and merge probs -----
+ * moe_router_logits followed by moe_topk on its rows, in one kernel: the
+ * logits never leave the chip unless `logits` is non-NULL.  Outputs and the
+ * top-k semantics are moe_topk's (case23 ordering, mask and softmax probs).
+ * Limits: as moe_router_logits, and 1 <= k <= min(N, 64). */
+int moe_router_topk(const moe_bf16_t *inp, int64_t M, int64_t K, const moe_bf16_t *weight, int64_t N,
+                    int64_t k, float *logits, float *values, int64_t *indices, uint8_t *routing_map,
+                    float *probs, void *stream);
 
 #ifdef __cplusplus
 }

@@ -318,6 +318,14 @@ def grouped_gemm_wgrad_fp32(dy: torch.Tensor, x: torch.Tensor, sizes: Sequence[i
     return torch.stack(outs, dim=0)
 
 
+def router_logits_fp32(inp: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """fp32-accumulated router logits: inp.float() @ weight.float().T.
+
+    kernel_cases/case38_ref_musa_asm_bf16_ssgemm_nt_320x256.py:46-53 (reference_fp32).
+    """
+    return inp.float().matmul(weight.float().t())
+
+
 def swiglu(y: torch.Tensor) -> torch.Tensor:
     """silu(y[:, :F]) * y[:, F:] in fp32, F = N/2 (gate first).  No reference function."""
     f = y.shape[1] // 2

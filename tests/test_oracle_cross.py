@@ -343,6 +343,19 @@ def test_grouped_gemm_wgrad_closed_forms():
     torch.testing.assert_close(whole[0], got.sum(0), rtol=1e-6, atol=1e-6)
 
 
+def test_router_logits_fp32_against_explicit_sum():
+    # The case's own check (explicit broadcast sum, case38...:64-79) and float64, on small shapes.
+    g = torch.Generator().manual_seed(56)
+    inp = torch.randn(5, 40, generator=g).to(torch.bfloat16)
+    w = torch.randn(7, 40, generator=g).to(torch.bfloat16)
+    got = ref_torch.router_logits_fp32(inp, w)
+    manual = (inp.float().unsqueeze(-1) * w.float().t().unsqueeze(0)).sum(dim=1)
+    assert (got - manual).abs().max().item() <= 1e-4
+    ref = inp.double().numpy() @ w.double().numpy().T
+    assert np.allclose(got.numpy(), ref, rtol=1e-6, atol=1e-5)
+    assert got.shape == (5, 7) and got.dtype == torch.float32
+
+
 def test_swiglu_closed_form():
     y = torch.tensor([[0.0, 1.0, 2.0, -3.0], [-1.0, 4.0, 0.5, 0.25]])
     h = ref_torch.swiglu(y).double().numpy()
