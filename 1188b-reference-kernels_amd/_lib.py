@@ -60,8 +60,9 @@ SIGNATURES = {
     "moe_grouped_gemm_gather": (_int, [_p, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _int, _p, _p, _sz, _p]),
     "moe_grouped_gemm_dgrad": (_int, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _sz, _p]),
     "moe_grouped_gemm_wgrad": (_int, [_p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _sz, _p]),
-    "moe_router_logits": (_int, [_p, _i64, _i64, _p, _i64, _p, _p]),
-    "moe_router_topk": (_int, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _p]),
+    "moe_router_workspace_size": (_sz, [_i64, _i64, _i64]),
+    "moe_router_logits": (_int, [_p, _i64, _i64, _p, _i64, _p, _p, _sz, _p]),
+    "moe_router_topk": (_int, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _sz, _p]),
 }
 
 _LIB = None

@@ -1,23 +1,23 @@
-// Router gate GEMM (logits in fp32 from bf16 inputs), optionally fused with
+// Router gate GEMM (logits in fp32 from bf16 inputs), optionally followed by
 // the router top-k, routing mask and merge probs.
 //
 // Math: kernel_cases/case38_ref_musa_asm_bf16_ssgemm_nt_320x256.py:46-53
 // (reference_fp32): logits[M, N] = inp[M, K] @ weight[N, K]^T, bf16 in, fp32
-// accumulate, fp32 out (moe_router_dtype=fp32, :8-13).  The fused top-k is the
+// accumulate, fp32 out (moe_router_dtype=fp32, :8-13).  The top-k is the
 // routine of topk_device.h (case23_ref_aten_topk.py:47-62; mask and probs as
 // moe_topk) applied to each logits row.
 //
-// Kernel shape (gfx950): one workgroup of 4 wavefronts per 64-row tile that
-// holds all N (<= 512) columns, so one workgroup owns whole logits rows; each
-// wavefront computes 64 rows x 16 kNB columns as 4 x kNB blocks of
-// v_mfma_f32_16x16x32_bf16 (the weight fragment is the first operand, so a
-// lane holds 4 consecutive columns of one row).  A and weight tiles stream
-// through a 3-stage LDS ring (2 stages when N > 320) filled by
-// buffer_load ... lds two steps ahead; rows are 128 bytes with 16-byte chunks
-// XOR-swizzled by (row / 2) % 8.  The epilogue stages the fp32 tile in LDS
-// (row stride 16 bytes past a multiple of 256: conflict-free 16-byte writes),
-// stores the logits rows coalesced and, fused, runs the per-row top-k with one
-// wavefront per row reading its row from LDS.
+// Kernel shape (gfx950): one workgroup of 4 wavefronts per 64-row tile
+// holding all N (<= 512) columns; each wavefront computes 64 rows x 16 kNB
+// columns as 4 x kNB blocks of v_mfma_f32_16x16x32_bf16 (the weight fragment
+// is the first operand, so a lane holds 4 consecutive columns of one row).  A
+// and weight tiles stream through a 3-stage LDS ring (2 stages when N > 320)
+// filled by buffer_load ... lds two steps ahead; rows are 128 bytes with
+// 16-byte chunks XOR-swizzled by (row / 2) % 8; the fp32 tile is staged in LDS
+// (row stride 16 bytes past a multiple of 256) and stored as rows.  The top-k
+// runs as a second pass over the logits rows, one wavefront per row, so it
+// keeps the whole chip busy (run in the GEMM's epilogue it serialised 16 rows
+// per wavefront and was slower than the GEMM plus the pass).
 #include <algorithm>
 
 #include "gemm_device.h"
@@ -38,20 +38,16 @@ constexpr int kRow = kBK * 2;  // 128-byte LDS rows
 struct RouterArgs {
   const uint16_t *inp;  // [M, K]
   const uint16_t *w;    // [N, K]
-  float *logits;        // [M, N] or nullptr
+  float *out;           // [M, N] fp32 logits (the output, or workspace for the top-k pass)
   int64_t M, K;
-  int N, k;
-  float *values;         // top-k: [M, k]
-  int64_t *indices;      // top-k: [M, k]
-  uint8_t *routing_map;  // top-k: [M, N] or nullptr
-  float *probs;          // top-k: [M, N] or nullptr
-  int vec_logits;        // logits rows are 16-byte aligned (N % 4 == 0, aligned base)
+  int N;
+  int vec_out;          // rows of out are 16-byte aligned (N % 4 == 0, aligned base)
 };
 
 __device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
 
-template <int kNB, bool kTopk>
-__global__ __launch_bounds__(256) void router_kernel(RouterArgs p) {
+template <int kNB>
+__global__ __launch_bounds__(256) void router_gemm_kernel(RouterArgs p) {
   constexpr int kWaves = 4;
   constexpr int kNT = 64 * kNB;                 // weight rows (logits columns) per tile
   constexpr int kABytes = kBM * kRow;           // 8 KiB
@@ -119,19 +115,8 @@ __global__ __launch_bounds__(256) void router_kernel(RouterArgs p) {
   // Fragments of v_mfma_f32_16x16x32_bf16: lane l reads row (block + l % 16),
   // the 8 values k = 8 (l / 16) .. + 7 of the sub-step (logical chunk 4 ks + l / 16).
   const int frow = lane & 15, fq = lane >> 4;
-  int fa_base[4], fb_base[kNB];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = i * 16 + frow;
-    fa_base[i] = r * kRow;
-  }
-#pragma unroll
-  for (int j = 0; j < kNB; ++j) {
-    const int r = wave * 16 * kNB + j * 16 + frow;
-    fb_base[j] = kABytes + r * kRow;
-  }
-  auto frag_addr = [&](uint32_t slot_base, int base, int r, int ks) {
-    return slot_base + base + ((((ks << 2) | fq) ^ swz(r)) << 4);
+  auto frag_addr = [&](uint32_t slot_base, int r, int ks) {
+    return slot_base + r * kRow + ((((ks << 2) | fq) ^ swz(r)) << 4);
   };
 
   f32x4 acc[4][kNB];
@@ -163,11 +148,11 @@ __global__ __launch_bounds__(256) void router_kernel(RouterArgs p) {
       bf16x8 fa[4], fb[kNB];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        fa[i] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)frag_addr(sb, fa_base[i], i * 16 + frow, ks));
+        fa[i] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)frag_addr(sb, i * 16 + frow, ks));
 #pragma unroll
       for (int j = 0; j < kNB; ++j)
         fb[j] = *reinterpret_cast<const lds_bf16x8 *>(
-            (uintptr_t)frag_addr(sb, fb_base[j], wave * 16 * kNB + j * 16 + frow, ks));
+            (uintptr_t)frag_addr(sb + kABytes, wave * 16 * kNB + j * 16 + frow, ks));
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -178,8 +163,8 @@ __global__ __launch_bounds__(256) void router_kernel(RouterArgs p) {
   wait_lds();
   barrier();
 
-  // Epilogue. acc[i][j] register r of lane l: logits row i * 16 + l % 16,
-  // column wave * 16 kNB + j * 16 + 4 (l / 16) + r.
+  // Epilogue. acc[i][j] register r of lane l: row i * 16 + l % 16, column
+  // wave * 16 kNB + j * 16 + 4 (l / 16) + r; staged in LDS, stored as rows.
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = i * 16 + frow;
@@ -191,50 +176,44 @@ __global__ __launch_bounds__(256) void router_kernel(RouterArgs p) {
   }
   wait_lds();
   barrier();
-  if (p.logits != nullptr) {
-    float *out = p.logits + row0 * N;
-    if (p.vec_logits) {
-      const int cpr = N / 4;  // 16-byte chunks per row
-      for (int idx = tid; idx < rows_valid * cpr; idx += kWaves * 64) {
-        const int r = idx / cpr, c = idx - r * cpr;
-        *reinterpret_cast<f32x4 *>(out + static_cast<int64_t>(r) * N + c * 4) =
-            *reinterpret_cast<const lds_f32x4 *>(sbase + r * kEpiStride + c * 16);
-      }
-    } else {
-      for (int idx = tid; idx < rows_valid * N; idx += kWaves * 64) {
-        const int r = idx / N, c = idx - r * N;
-        out[static_cast<int64_t>(r) * N + c] = *reinterpret_cast<const lds_f32 *>(sbase + r * kEpiStride + c * 4);
-      }
+  float *out = p.out + row0 * N;
+  if (p.vec_out) {
+    const int cpr = N / 4;  // 16-byte chunks per row
+    for (int idx = tid; idx < rows_valid * cpr; idx += kWaves * 64) {
+      const int r = idx / cpr, c = idx - r * cpr;
+      *reinterpret_cast<f32x4 *>(out + static_cast<int64_t>(r) * N + c * 4) =
+          *reinterpret_cast<const lds_f32x4 *>(sbase + r * kEpiStride + c * 16);
     }
-  }
-  if constexpr (kTopk) {
-    constexpr int kEPL = kNB;  // ceil(N / 64) elements per lane
-    for (int r = wave; r < rows_valid; r += kWaves) {
-      const lds_char *rowp = sbase + r * kEpiStride;
-      topk_row<kEPL>([&](int e) { return *reinterpret_cast<const lds_f32 *>(rowp + e * 4); }, row0 + r, N, p.k,
-                     p.values, p.indices, p.routing_map, p.probs);
+  } else {
+    for (int idx = tid; idx < rows_valid * N; idx += kWaves * 64) {
+      const int r = idx / N, c = idx - r * N;
+      out[static_cast<int64_t>(r) * N + c] = *reinterpret_cast<const lds_f32 *>(sbase + r * kEpiStride + c * 4);
     }
   }
 }
 
-template <bool kTopk>
-void launch_router(const RouterArgs &p, int64_t grid, hipStream_t s) {
-  const int nb = static_cast<int>(ceil_div(p.N, 64));
-  switch (nb) {
-    case 1: router_kernel<1, kTopk><<<dim3(grid), dim3(256), 0, s>>>(p); break;
-    case 2: router_kernel<2, kTopk><<<dim3(grid), dim3(256), 0, s>>>(p); break;
-    case 3: router_kernel<3, kTopk><<<dim3(grid), dim3(256), 0, s>>>(p); break;
-    case 4: router_kernel<4, kTopk><<<dim3(grid), dim3(256), 0, s>>>(p); break;
-    case 5: router_kernel<5, kTopk><<<dim3(grid), dim3(256), 0, s>>>(p); break;
-    case 6: router_kernel<6, kTopk><<<dim3(grid), dim3(256), 0, s>>>(p); break;
-    case 7: router_kernel<7, kTopk><<<dim3(grid), dim3(256), 0, s>>>(p); break;
-    default: router_kernel<8, kTopk><<<dim3(grid), dim3(256), 0, s>>>(p); break;
-  }
+// Top-k pass, one wavefront per row of the logits (topk_device.h).
+struct TopkArgs {
+  const float *logits;
+  int64_t M;
+  int N, k;
+  float *values;
+  int64_t *indices;
+  uint8_t *routing_map;
+  float *probs;
+};
+
+template <int kEPL>
+__global__ __launch_bounds__(256) void router_topk_kernel(TopkArgs p) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+  if (t >= p.M) return;
+  const float *row = p.logits + t * p.N;
+  topk_row<kEPL>([&](int e) { return row[e]; }, t, p.N, p.k, p.values, p.indices, p.routing_map, p.probs);
 }
 
 int launch(const char *fn, const moe_bf16_t *inp, int64_t M, int64_t K, const moe_bf16_t *weight, int64_t N,
            int64_t k, float *logits, float *values, int64_t *indices, uint8_t *routing_map, float *probs,
-           bool topk, void *stream) {
+           bool topk, void *workspace, size_t workspace_bytes, void *stream) {
   if (M < 0 || K < 0 || N < 0) {
     return fail(MOE_ERR_SHAPE, "%s: negative size (M=%lld K=%lld N=%lld)", fn, (long long)M, (long long)K,
                 (long long)N);
@@ -255,22 +234,57 @@ int launch(const char *fn, const moe_bf16_t *inp, int64_t M, int64_t K, const mo
   if (topk && (values == nullptr || indices == nullptr)) return fail(MOE_ERR_INVALID_ARG, "%s: null values or indices", fn);
   if (!is_aligned(inp, 16) || !is_aligned(weight, 16)) return fail(MOE_ERR_ALIGN, "%s: inp and weight must be 16-byte aligned", fn);
   if (ceil_div(M, kBM) > 0x7fffffff) return fail(MOE_ERR_CAPACITY, "%s: M=%lld too large", fn, (long long)M);
+  // Without a logits output the top-k pass reads them from the workspace.
+  const size_t plane = static_cast<size_t>(M) * static_cast<size_t>(N) * sizeof(float);
+  const size_t need = logits == nullptr ? plane : 0;
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
+    return fail(MOE_ERR_WORKSPACE, "%s: workspace of %zu bytes needed (got %zu)", fn, need,
+                workspace == nullptr ? size_t(0) : workspace_bytes);
+  }
+  if (need > 0 && !is_aligned(workspace, 16)) return fail(MOE_ERR_ALIGN, "%s: workspace must be 16-byte aligned", fn);
   RouterArgs p;
   p.inp = inp;
   p.w = weight;
-  p.logits = logits;
+  p.out = logits != nullptr ? logits : static_cast<float *>(workspace);
   p.M = M;
   p.K = K;
   p.N = static_cast<int>(N);
-  p.k = static_cast<int>(k);
-  p.values = values;
-  p.indices = indices;
-  p.routing_map = routing_map;
-  p.probs = probs;
-  p.vec_logits = (N % 4 == 0) && is_aligned(logits, 16);
+  p.vec_out = (N % 4 == 0) && is_aligned(p.out, 16);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (topk) launch_router<true>(p, ceil_div(M, kBM), s);
-  else launch_router<false>(p, ceil_div(M, kBM), s);
+  const int64_t grid = ceil_div(M, kBM);
+  const int nb = static_cast<int>(ceil_div(N, 64));
+  switch (nb) {
+    case 1: router_gemm_kernel<1><<<dim3(grid), dim3(256), 0, s>>>(p); break;
+    case 2: router_gemm_kernel<2><<<dim3(grid), dim3(256), 0, s>>>(p); break;
+    case 3: router_gemm_kernel<3><<<dim3(grid), dim3(256), 0, s>>>(p); break;
+    case 4: router_gemm_kernel<4><<<dim3(grid), dim3(256), 0, s>>>(p); break;
+    case 5: router_gemm_kernel<5><<<dim3(grid), dim3(256), 0, s>>>(p); break;
+    case 6: router_gemm_kernel<6><<<dim3(grid), dim3(256), 0, s>>>(p); break;
+    case 7: router_gemm_kernel<7><<<dim3(grid), dim3(256), 0, s>>>(p); break;
+    default: router_gemm_kernel<8><<<dim3(grid), dim3(256), 0, s>>>(p); break;
+  }
+  if (int rc = check_launch(fn)) return rc;
+  if (!topk) return MOE_OK;
+  TopkArgs t;
+  t.logits = p.out;
+  t.M = M;
+  t.N = p.N;
+  t.k = static_cast<int>(k);
+  t.values = values;
+  t.indices = indices;
+  t.routing_map = routing_map;
+  t.probs = probs;
+  const int64_t tgrid = ceil_div(M, 4);
+  switch (nb) {
+    case 1: router_topk_kernel<1><<<dim3(tgrid), dim3(256), 0, s>>>(t); break;
+    case 2: router_topk_kernel<2><<<dim3(tgrid), dim3(256), 0, s>>>(t); break;
+    case 3: router_topk_kernel<3><<<dim3(tgrid), dim3(256), 0, s>>>(t); break;
+    case 4: router_topk_kernel<4><<<dim3(tgrid), dim3(256), 0, s>>>(t); break;
+    case 5: router_topk_kernel<5><<<dim3(tgrid), dim3(256), 0, s>>>(t); break;
+    case 6: router_topk_kernel<6><<<dim3(tgrid), dim3(256), 0, s>>>(t); break;
+    case 7: router_topk_kernel<7><<<dim3(tgrid), dim3(256), 0, s>>>(t); break;
+    default: router_topk_kernel<8><<<dim3(tgrid), dim3(256), 0, s>>>(t); break;
+  }
   return check_launch(fn);
 }
 
@@ -279,17 +293,23 @@ int launch(const char *fn, const moe_bf16_t *inp, int64_t M, int64_t K, const mo
 
 extern "C" {
 
+size_t moe_router_workspace_size(int64_t M, int64_t K, int64_t N) {
+  (void)K;
+  if (M <= 0 || N <= 0) return 0;
+  return static_cast<size_t>(M) * static_cast<size_t>(N) * sizeof(float);
+}
+
 int moe_router_logits(const moe_bf16_t *inp, int64_t M, int64_t K, const moe_bf16_t *weight, int64_t N,
-                      float *logits, void *stream) {
+                      float *logits, void *workspace, size_t workspace_bytes, void *stream) {
   return moe::launch("moe_router_logits", inp, M, K, weight, N, 0, logits, nullptr, nullptr, nullptr, nullptr,
-                     false, stream);
+                     false, workspace, workspace_bytes, stream);
 }
 
 int moe_router_topk(const moe_bf16_t *inp, int64_t M, int64_t K, const moe_bf16_t *weight, int64_t N, int64_t k,
                     float *logits, float *values, int64_t *indices, uint8_t *routing_map, float *probs,
-                    void *stream) {
+                    void *workspace, size_t workspace_bytes, void *stream) {
   return moe::launch("moe_router_topk", inp, M, K, weight, N, k, logits, values, indices, routing_map, probs, true,
-                     stream);
+                     workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -87,13 +87,13 @@ def router_logits(inp: torch.Tensor, weight: torch.Tensor, *, out: Optional[torc
     ic, wc = inp.contiguous(), weight.contiguous()
     if out is None:
         out = torch.empty(M, N, dtype=torch.float32, device=inp.device)
-    call("moe_router_logits", ptr(ic), M, K, ptr(wc), N, ptr(out), stream_handle())
+    call("moe_router_logits", ptr(ic), M, K, ptr(wc), N, ptr(out), None, 0, stream_handle())
     return out
 
 
 def router_topk(inp: torch.Tensor, weight: torch.Tensor, k: int, *, with_logits: bool = False,
                 with_mask: bool = False, with_probs: bool = False):
-    """router_logits followed by topk on its rows, fused in one kernel.
+    """router_logits followed by topk on its rows (two kernels, one call).
 
     Returns (values, indices) and, on request and in this order, the fp32 logits [M, N],
     the routing mask bool [M, N] and the merge probs fp32 [M, N] -- the outputs of topk.
@@ -115,8 +115,10 @@ def router_topk(inp: torch.Tensor, weight: torch.Tensor, k: int, *, with_logits:
     logits = torch.empty(M, N, dtype=torch.float32, device=dev) if with_logits else None
     mask = torch.empty(M, N, dtype=torch.bool, device=dev) if with_mask else None
     probs = torch.empty(M, N, dtype=torch.float32, device=dev) if with_probs else None
+    ws_bytes = 0 if with_logits else _lib.lib().moe_router_workspace_size(M, K, N)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     call("moe_router_topk", ptr(ic), M, K, ptr(wc), N, k, ptr(logits), ptr(values), ptr(indices),
-         ptr(mask.view(torch.uint8)) if mask is not None else None, ptr(probs), stream_handle())
+         ptr(mask.view(torch.uint8)) if mask is not None else None, ptr(probs), ptr(ws), ws_bytes, stream_handle())
     out = [values, indices]
     if with_logits:
         out.append(logits)

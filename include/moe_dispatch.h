@@ -261,18 +261,22 @@ int moe_grouped_gemm_wgrad(const moe_bf16_t *dy, const moe_bf16_t *x, int64_t M_
  *   inp    bf16 [M, K];  weight bf16 [N, K] (num_experts x hidden)
  *   logits fp32 [M, N]
  * Limits: 1 <= N <= 512, K % 8 == 0, K < 2^22, N * K < 2^30; inp and weight
- *   16-byte aligned.  Workspace: none. */
+ *   16-byte aligned.
+ * Workspace: none (pass NULL, 0). */
+size_t moe_router_workspace_size(int64_t M, int64_t K, int64_t N);
 int moe_router_logits(const moe_bf16_t *inp, int64_t M, int64_t K, const moe_bf16_t *weight, int64_t N,
-                      float *logits, void *stream);
+                      float *logits, void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---- router gate GEMM fused with top-k, routing mask and merge probs -----
- * moe_router_logits followed by moe_topk on its rows, in one kernel: the
- * logits never leave the chip unless `logits` is non-NULL.  Outputs and the
- * top-k semantics are moe_topk's (case23 ordering, mask and softmax probs).
- * Limits: as moe_router_logits, and 1 <= k <= min(N, 64). */
+ * moe_router_logits followed by moe_topk on its rows (case23 ordering, mask
+ * and softmax probs as moe_topk), enqueued together; `logits` may be NULL,
+ * then the fp32 logits are kept in the workspace only.
+ * Limits: as moe_router_logits, and 1 <= k <= min(N, 64).
+ * Workspace: moe_router_workspace_size(M, K, N) bytes when logits is NULL,
+ *   none otherwise. */
 int moe_router_topk(const moe_bf16_t *inp, int64_t M, int64_t K, const moe_bf16_t *weight, int64_t N,
                     int64_t k, float *logits, float *values, int64_t *indices, uint8_t *routing_map,
-                    float *probs, void *stream);
+                    float *probs, void *workspace, size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -17,7 +17,7 @@ L = pkg._lib
 def test_library_loads_and_exports_header_symbols():
     lib = L.lib()
     declared = L.header_functions()
-    assert len(declared) == len(L.SIGNATURES) == 18
+    assert len(declared) == len(L.SIGNATURES) == 19
     assert set(declared) == set(L.SIGNATURES)
     for name in declared:
         assert hasattr(lib, name), name
@@ -88,17 +88,18 @@ FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
     ("moe_grouped_gemm_dgrad", (ctypes.c_void_p(0x1008), 4, 16, FAKE, 1, 16, FAKE, FAKE, None, 0, None), L.MOE_ERR_ALIGN, "aligned"),
     ("moe_grouped_gemm_dgrad", (FAKE, 4, 1 << 22, FAKE, 1, 16, FAKE, FAKE, None, 0, None), L.MOE_ERR_CAPACITY, "32-bit"),
     ("moe_grouped_gemm_dgrad", (FAKE, 4, 1 << 16, FAKE, 1, 1 << 16, FAKE, FAKE, None, 0, None), L.MOE_ERR_CAPACITY, "32-bit"),
-    # router (inp, M, K, weight, N, [k,] logits, ...)
-    ("moe_router_logits", (FAKE, 64, 16, FAKE, 0, FAKE, None), L.MOE_ERR_CAPACITY, "N=0"),
-    ("moe_router_logits", (FAKE, 64, 16, FAKE, 513, FAKE, None), L.MOE_ERR_CAPACITY, "512"),
-    ("moe_router_logits", (FAKE, 64, 12, FAKE, 8, FAKE, None), L.MOE_ERR_SHAPE, "multiple of 8"),
-    ("moe_router_logits", (FAKE, -1, 16, FAKE, 8, FAKE, None), L.MOE_ERR_SHAPE, "negative"),
-    ("moe_router_logits", (FAKE, 64, 16, FAKE, 8, None, None), L.MOE_ERR_INVALID_ARG, "null logits"),
-    ("moe_router_logits", (ctypes.c_void_p(0x1002), 64, 16, FAKE, 8, FAKE, None), L.MOE_ERR_ALIGN, "aligned"),
-    ("moe_router_logits", (FAKE, 64, 1 << 22, FAKE, 8, FAKE, None), L.MOE_ERR_CAPACITY, "32-bit"),
-    ("moe_router_topk", (FAKE, 64, 16, FAKE, 8, 9, None, FAKE, FAKE, None, None, None), L.MOE_ERR_SHAPE, "out of range"),
-    ("moe_router_topk", (FAKE, 64, 16, FAKE, 128, 65, None, FAKE, FAKE, None, None, None), L.MOE_ERR_CAPACITY, "64"),
-    ("moe_router_topk", (FAKE, 64, 16, FAKE, 8, 2, None, None, FAKE, None, None, None), L.MOE_ERR_INVALID_ARG, "values"),
+    # router (inp, M, K, weight, N, [k,] logits, [values, indices, map, probs,] ws, ws_bytes, stream)
+    ("moe_router_logits", (FAKE, 64, 16, FAKE, 0, FAKE, None, 0, None), L.MOE_ERR_CAPACITY, "N=0"),
+    ("moe_router_logits", (FAKE, 64, 16, FAKE, 513, FAKE, None, 0, None), L.MOE_ERR_CAPACITY, "512"),
+    ("moe_router_logits", (FAKE, 64, 12, FAKE, 8, FAKE, None, 0, None), L.MOE_ERR_SHAPE, "multiple of 8"),
+    ("moe_router_logits", (FAKE, -1, 16, FAKE, 8, FAKE, None, 0, None), L.MOE_ERR_SHAPE, "negative"),
+    ("moe_router_logits", (FAKE, 64, 16, FAKE, 8, None, None, 0, None), L.MOE_ERR_INVALID_ARG, "null logits"),
+    ("moe_router_logits", (ctypes.c_void_p(0x1002), 64, 16, FAKE, 8, FAKE, None, 0, None), L.MOE_ERR_ALIGN, "aligned"),
+    ("moe_router_logits", (FAKE, 64, 1 << 22, FAKE, 8, FAKE, None, 0, None), L.MOE_ERR_CAPACITY, "32-bit"),
+    ("moe_router_topk", (FAKE, 64, 16, FAKE, 8, 9, None, FAKE, FAKE, None, None, FAKE, 1 << 20, None), L.MOE_ERR_SHAPE, "out of range"),
+    ("moe_router_topk", (FAKE, 64, 16, FAKE, 128, 65, None, FAKE, FAKE, None, None, FAKE, 1 << 20, None), L.MOE_ERR_CAPACITY, "64"),
+    ("moe_router_topk", (FAKE, 64, 16, FAKE, 8, 2, None, None, FAKE, None, None, FAKE, 1 << 20, None), L.MOE_ERR_INVALID_ARG, "values"),
+    ("moe_router_topk", (FAKE, 64, 16, FAKE, 8, 2, None, FAKE, FAKE, None, None, None, 0, None), L.MOE_ERR_WORKSPACE, "workspace"),
     # wgrad (dy, x, M, N, K, G, offsets, dw, ws, ws_bytes, stream)
     ("moe_grouped_gemm_wgrad", (FAKE, FAKE, 4, 16, 16, 5000, FAKE, FAKE, None, 0, None), L.MOE_ERR_CAPACITY, "4096"),
     ("moe_grouped_gemm_wgrad", (FAKE, FAKE, 4, 16, 10, 1, FAKE, FAKE, None, 0, None), L.MOE_ERR_SHAPE, "multiples of 8"),
@@ -126,8 +127,8 @@ def test_empty_problems_are_no_ops():
     assert _status("moe_grouped_gemm_dgrad", None, 0, 16, None, 1, 16, FAKE, None, None, 0, None)[0] == 0
     assert _status("moe_grouped_gemm_dgrad", None, 4, 16, None, 1, 0, FAKE, None, None, 0, None)[0] == 0
     assert _status("moe_grouped_gemm_wgrad", None, None, 4, 0, 16, 1, FAKE, None, None, 0, None)[0] == 0
-    assert _status("moe_router_logits", None, 0, 16, None, 8, None, None)[0] == 0
-    assert _status("moe_router_topk", None, 0, 16, None, 8, 2, None, None, None, None, None, None)[0] == 0
+    assert _status("moe_router_logits", None, 0, 16, None, 8, None, None, 0, None)[0] == 0
+    assert _status("moe_router_topk", None, 0, 16, None, 8, 2, None, None, None, None, None, None, 0, None)[0] == 0
 
 
 def test_workspace_sizes():
@@ -135,6 +136,9 @@ def test_workspace_sizes():
     assert lib.moe_row_id_map_workspace_size(16384, 64) >= 256 * 64 * 4
     assert lib.moe_permute_workspace_size(16384) >= 4096 * 4
     assert lib.moe_row_id_map_workspace_size(-1, 4) == 0
+    # router: one fp32 logits plane (used when the top-k call gets no logits output)
+    assert lib.moe_router_workspace_size(16384, 8192, 320) == 16384 * 320 * 4
+    assert lib.moe_router_workspace_size(0, 8192, 320) == 0
 
 
 def test_status_strings():
