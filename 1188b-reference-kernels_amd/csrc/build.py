@@ -31,6 +31,7 @@ SOURCES = [
     "grouped_gemm.hip",
     "grouped_gemm_bwd.hip",
     "router.hip",
+    "cast.hip",
 ]
 
 ARCH = os.environ.get("MOE_OFFLOAD_ARCH", "gfx950")

@@ -129,6 +129,22 @@ def router_topk(inp: torch.Tensor, weight: torch.Tensor, k: int, *, with_logits:
     return tuple(out)
 
 
+def cast(x: torch.Tensor, dtype: torch.dtype, *, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """x.to(dtype) for bf16 -> fp32 (exact) and fp32 -> bf16 (round to nearest even, any NaN -> 0x7FC0)."""
+    _on_gpu("x", x)
+    pairs = {(torch.bfloat16, torch.float32): "moe_cast_bf16_to_f32", (torch.float32, torch.bfloat16): "moe_cast_f32_to_bf16"}
+    fn = pairs.get((x.dtype, dtype))
+    if fn is None:
+        raise TypeError(f"cast supports bfloat16 -> float32 and float32 -> bfloat16, got {x.dtype} -> {dtype}")
+    xc = x.contiguous()
+    if out is None:
+        out = torch.empty(x.shape, dtype=dtype, device=x.device)
+    elif out.dtype != dtype or out.shape != x.shape or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor of the input's shape and the target dtype")
+    call(fn, ptr(xc), xc.numel(), ptr(out), stream_handle())
+    return out
+
+
 # ---------------------------------------------------------------- row-id map
 def row_id_map(routing_map: torch.Tensor, *, expert_major: bool = True, token_major: bool = True,
                expert_major_i32: bool = False, expert_offsets: bool = False,

@@ -36,6 +36,8 @@
  *                 (dgrad, no bundle)
  *   case05/case09 kernel_cases/case09_moe_grouped_gemm_fc1_wgrad.py:57-64 (wgrad, no bundle)
  *   case38        kernel_cases/case38_ref_musa_asm_bf16_ssgemm_nt_320x256.py:46-53 (router logits)
+ *   case11/case25 kernel_cases/case11_router_bwd_cast_bf16_to_fp32.py:43-44,
+ *                 kernel_cases/case25_ref_unary_cast_fp32_to_bf16.py:56-72 (casts)
  */
 #ifndef MOE_DISPATCH_H_
 #define MOE_DISPATCH_H_
@@ -47,7 +49,7 @@
 extern "C" {
 #endif
 
-#define MOE_DISPATCH_ABI_VERSION 4
+#define MOE_DISPATCH_ABI_VERSION 5
 
 typedef uint16_t moe_bf16_t;
 
@@ -277,6 +279,16 @@ int moe_router_logits(const moe_bf16_t *inp, int64_t M, int64_t K, const moe_bf1
 int moe_router_topk(const moe_bf16_t *inp, int64_t M, int64_t K, const moe_bf16_t *weight, int64_t N,
                     int64_t k, float *logits, float *values, int64_t *indices, uint8_t *routing_map,
                     float *probs, void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---- element casts (router backward) ------------------------------------
+ * Replace case11 Model.forward(x) = x.to(torch.float32)
+ * (kernel_cases/case11_router_bwd_cast_bf16_to_fp32.py:43-44) and case25's
+ * timed inp.to(torch.bfloat16) (kernel_cases/case25_ref_unary_cast_fp32_to_bf16.py:107,
+ * golden round_bf16_rne :56-66: round to nearest even).  Any NaN -> 0x7FC0.
+ * n elements, contiguous; any alignment (16/32-byte aligned pointers take the
+ * vector path).  Workspace: none. */
+int moe_cast_bf16_to_f32(const moe_bf16_t *src, int64_t n, float *dst, void *stream);
+int moe_cast_f32_to_bf16(const float *src, int64_t n, moe_bf16_t *dst, void *stream);
 
 #ifdef __cplusplus
 }

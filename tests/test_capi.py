@@ -17,7 +17,7 @@ L = pkg._lib
 def test_library_loads_and_exports_header_symbols():
     lib = L.lib()
     declared = L.header_functions()
-    assert len(declared) == len(L.SIGNATURES) == 19
+    assert len(declared) == len(L.SIGNATURES) == 21
     assert set(declared) == set(L.SIGNATURES)
     for name in declared:
         assert hasattr(lib, name), name
@@ -100,6 +100,9 @@ FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
     ("moe_router_topk", (FAKE, 64, 16, FAKE, 128, 65, None, FAKE, FAKE, None, None, FAKE, 1 << 20, None), L.MOE_ERR_CAPACITY, "64"),
     ("moe_router_topk", (FAKE, 64, 16, FAKE, 8, 2, None, None, FAKE, None, None, FAKE, 1 << 20, None), L.MOE_ERR_INVALID_ARG, "values"),
     ("moe_router_topk", (FAKE, 64, 16, FAKE, 8, 2, None, FAKE, FAKE, None, None, None, 0, None), L.MOE_ERR_WORKSPACE, "workspace"),
+    ("moe_cast_f32_to_bf16", (FAKE, -1, FAKE, None), L.MOE_ERR_SHAPE, "negative"),
+    ("moe_cast_f32_to_bf16", (None, 8, FAKE, None), L.MOE_ERR_INVALID_ARG, "null"),
+    ("moe_cast_bf16_to_f32", (FAKE, 8, None, None), L.MOE_ERR_INVALID_ARG, "null"),
     # wgrad (dy, x, M, N, K, G, offsets, dw, ws, ws_bytes, stream)
     ("moe_grouped_gemm_wgrad", (FAKE, FAKE, 4, 16, 16, 5000, FAKE, FAKE, None, 0, None), L.MOE_ERR_CAPACITY, "4096"),
     ("moe_grouped_gemm_wgrad", (FAKE, FAKE, 4, 16, 10, 1, FAKE, FAKE, None, 0, None), L.MOE_ERR_SHAPE, "multiples of 8"),
@@ -128,6 +131,8 @@ def test_empty_problems_are_no_ops():
     assert _status("moe_grouped_gemm_dgrad", None, 4, 16, None, 1, 0, FAKE, None, None, 0, None)[0] == 0
     assert _status("moe_grouped_gemm_wgrad", None, None, 4, 0, 16, 1, FAKE, None, None, 0, None)[0] == 0
     assert _status("moe_router_logits", None, 0, 16, None, 8, None, None, 0, None)[0] == 0
+    assert _status("moe_cast_f32_to_bf16", None, 0, None, None)[0] == 0
+    assert _status("moe_cast_bf16_to_f32", None, 0, None, None)[0] == 0
     assert _status("moe_router_topk", None, 0, 16, None, 8, 2, None, None, None, None, None, None, 0, None)[0] == 0
 
 
