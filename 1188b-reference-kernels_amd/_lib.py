@@ -35,7 +35,7 @@ MOE_MAP_EXPERT_MAJOR = 1
 MOE_EPILOGUE_NONE = 0
 MOE_EPILOGUE_SWIGLU = 1
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -65,6 +65,10 @@ SIGNATURES = {
     "moe_router_topk": (_int, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _sz, _p]),
     "moe_cast_bf16_to_f32": (_int, [_p, _i64, _p, _p]),
     "moe_cast_f32_to_bf16": (_int, [_p, _i64, _p, _p]),
+    "moe_router_dgrad_tf32_workspace_size": (_sz, [_i64, _i64, _i64]),
+    "moe_router_dgrad_tf32": (_int, [_p, _i64, _i64, _p, _i64, _p, _p, _sz, _p]),
+    "moe_router_wgrad_tf32_workspace_size": (_sz, [_i64, _i64, _i64]),
+    "moe_router_wgrad_tf32": (_int, [_p, _i64, _i64, _p, _i64, _p, _p, _sz, _p]),
 }
 
 _LIB = None

@@ -63,10 +63,11 @@ constexpr int kRMRow = 256 * 2;     // 512-byte rows of an RM operand tile (256 
 struct BwdArgs {
   const uint16_t *a;        // dy [M, N]
   const uint16_t *b;        // dgrad: w [G, N, K]; wgrad: x [M, K]
-  const int32_t *offsets;   // [G + 1]
-  uint16_t *out;            // dgrad: dx [M, K]; wgrad: dw [G, N, K]
+  const int32_t *offsets;   // [G + 1], or nullptr: group g is rows [g chunk, (g + 1) chunk) of M
+  void *out;                // dgrad: dx [M, K]; wgrad: dw [G, N, K] (bf16, or fp32 for kOut != 0)
   int64_t M, N, K, G;
   int64_t ntiles;           // column tiles, ceil(K / 256)
+  int64_t chunk;            // rows per group when offsets is nullptr
 };
 
 __device__ __forceinline__ int kc_swz(int row) { return (row >> 1) & 7; }
@@ -98,7 +99,9 @@ __device__ __forceinline__ bf16x8 read_rm_frag(uint32_t addr) {
 #endif
 }
 
-template <bool kWgrad, int kBM, int kWavesM, int kStages>
+// kOut: 0 = bf16 output, 1 = fp32 output, 2 = fp32 output added to what out
+// holds.  The fp32 outputs issue the next tile's stages after the stores.
+template <bool kWgrad, int kBM, int kWavesM, int kStages, int kOut>
 __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
   constexpr int kWaves = 4;
   constexpr int kWavesN = kWaves / kWavesM;
@@ -110,7 +113,8 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
   constexpr int kBBytes = kBN * kBK * 2;
   constexpr int kStageBytes = kABytes + kBBytes;
   constexpr int kDmaA = kABytes / 1024 / kWaves, kDmaB = kBBytes / 1024 / kWaves;
-  constexpr int kStores = kMI * kNI * 2;        // 16-byte stores per lane per tile
+  constexpr bool kLate = kOut != 0;             // next tile's stages issued after the stores
+  constexpr int kStores = kLate ? 0 : kMI * kNI * 2;  // stores younger than the next stages
   constexpr int kReads = (kARM ? 2 * kMI : kMI) + 2 * kNI;  // LDS reads per sub-step
   constexpr int kMfma = kMI * kNI;              // MFMAs per sub-step
   static_assert(kStages * kStageBytes <= 160 * 1024, "LDS budget");
@@ -132,6 +136,11 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
 
   // ---- tile walker
   auto group_range = [&](int64_t g, int64_t &lo, int64_t &hi) {
+    if (p.offsets == nullptr) {
+      lo = min(g * p.chunk, p.M);
+      hi = min(lo + p.chunk, p.M);
+      return;
+    }
     lo = min(max(static_cast<int64_t>(p.offsets[g]), int64_t(0)), p.M);
     hi = min(max(static_cast<int64_t>(p.offsets[g + 1]), lo), p.M);
   };
@@ -388,7 +397,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
     barrier();
     Tile nxt;
     const bool more = find_tile(round + 1, nxt);
-    if (more) {
+    if (more && !kLate) {
       setup_dma(nxt);
 #pragma unroll
       for (int st = 0; st < kStages; ++st) {
@@ -404,11 +413,51 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
     // half-wave's words of group g with the lower half-wave's of group g + 1, so
     // a lower lane holds columns 8g .. 8g + 7 of its row and its upper partner
     // 8g + 8 .. 8g + 15: one 16-byte store each.
-    {
+    if constexpr (kOut != 0) {
+      // fp32: register group g of block (i, j) is 4 consecutive columns of
+      // one row, stored (or added to the stored values) as 16 bytes.
       const int64_t wrow0 = cur.i0 + wm * kWaveRows;
       const int64_t row_end = kWgrad ? N : cur.hi;
       const int rows_out = static_cast<int>(min(max(row_end - wrow0, int64_t(0)), int64_t(kWaveRows)));
-      const uint16_t *obase = kWgrad ? p.out + cur.g * N * K : p.out;
+      float *const obase = static_cast<float *>(p.out) + (kWgrad ? cur.g * N * K : 0);
+      const uint32_t ld = static_cast<uint32_t>(K) * 4u;
+      const __amdgpu_buffer_rsrc_t ro =
+          make_rsrc(obase + (rows_out > 0 ? wrow0 * K : 0), static_cast<uint32_t>(rows_out) * ld);
+      const int64_t tcol0 = static_cast<int64_t>(cur.nt) * kBN + wn * kWaveCols;
+      const int half = lane >> 5;
+#pragma unroll
+      for (int i = 0; i < kMI; ++i) {
+        const int orow = i * 32 + (lane & 31);
+#pragma unroll
+        for (int j = 0; j < kNI; ++j) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int64_t gcol = tcol0 + j * 32 + g * 8 + half * 4;
+            const uint32_t off = gcol < K ? static_cast<uint32_t>(orow) * ld + static_cast<uint32_t>(gcol) * 4u : kNoAccess;
+            u32x4 v = {__float_as_uint(acc[i][j][4 * g]), __float_as_uint(acc[i][j][4 * g + 1]),
+                       __float_as_uint(acc[i][j][4 * g + 2]), __float_as_uint(acc[i][j][4 * g + 3])};
+#if defined(__HIP_DEVICE_COMPILE__)
+            if constexpr (kOut == 2) {
+              const u32x4 old = __builtin_amdgcn_raw_buffer_load_b128(ro, static_cast<int>(off), 0, 0);
+              v = u32x4{__float_as_uint(__uint_as_float(old.x) + __uint_as_float(v.x)),
+                        __float_as_uint(__uint_as_float(old.y) + __uint_as_float(v.y)),
+                        __float_as_uint(__uint_as_float(old.z) + __uint_as_float(v.z)),
+                        __float_as_uint(__uint_as_float(old.w) + __uint_as_float(v.w))};
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(v, ro, static_cast<int>(off), 0, 0);
+#else
+            (void)off;
+            (void)v;
+            (void)ro;
+#endif
+          }
+        }
+      }
+    } else {
+      const int64_t wrow0 = cur.i0 + wm * kWaveRows;
+      const int64_t row_end = kWgrad ? N : cur.hi;
+      const int rows_out = static_cast<int>(min(max(row_end - wrow0, int64_t(0)), int64_t(kWaveRows)));
+      const uint16_t *obase = static_cast<const uint16_t *>(p.out) + (kWgrad ? cur.g * N * K : 0);
       const uint32_t ld = static_cast<uint32_t>(K) * 2u;
       const __amdgpu_buffer_rsrc_t ro =
           make_rsrc(obase + (rows_out > 0 ? wrow0 * K : 0), static_cast<uint32_t>(rows_out) * ld);
@@ -452,16 +501,102 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
       }
     }
     if (!more) break;
+    if constexpr (kLate) {
+      setup_dma(nxt);
+#pragma unroll
+      for (int st = 0; st < kStages; ++st) {
+        issue_a(min(st, nxt.ktiles - 1), st);
+        issue_b(min(st, nxt.ktiles - 1), st);
+      }
+    }
     cur = nxt;
   }
 }
 
-template <bool kWgrad, int kBM, int kWavesM, int kStages>
+template <bool kWgrad, int kBM, int kWavesM, int kStages, int kOut = 0>
 void launch(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
   int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
   grid = std::max<int64_t>(8, (grid + 7) / 8 * 8);
-  grouped_gemm_bwd_kernel<kWgrad, kBM, kWavesM, kStages><<<dim3(grid), dim3(256), 0, s>>>(p);
+  grouped_gemm_bwd_kernel<kWgrad, kBM, kWavesM, kStages, kOut><<<dim3(grid), dim3(256), 0, s>>>(p);
 }
+
+// ---- tf32 GEMMs of the router backward on the bf16 matrix cores ---------
+// kernel_cases/case39_ref_musa_asm_tf32_ssgemm_nn_384x256.py:61-68 and
+// case31_ref_musa_asm_tf32_ssgemm_tn_128x256.py:61-68 (reference_tf32): both
+// operands are fp32 rounded to tf32 (round_tf32_rne, :51-58 / :52-58: add 0x1000 unless the 13
+// dropped bits are exactly 0x1000 and the kept LSB is even, then clear them),
+// the products are exact and accumulate in fp32.  gfx950 has no tf32 matrix
+// instruction, so each tf32 value t is split into bf16 hi = RNE(t) and
+// lo = t - hi (at most 4 significant bits: exact in bf16), and
+// a b = hi_a hi_b + hi_a lo_b + lo_a hi_b + lo_a lo_b with the last term,
+// below 2^-16 |a b|, dropped: three bf16 products per tf32 product, each exact
+// in the fp32 accumulator.
+__device__ __forceinline__ uint32_t tf32_rne_bits(uint32_t b) {
+  const uint32_t low = b & 0x1FFFu, lsb = (b >> 13) & 1u;
+  const uint32_t add = (low == 0x1000u && lsb == 0u) ? 0u : 0x1000u;
+  return (b + add) & 0xFFFFE000u;
+}
+
+// src fp32 [rows, cols] (cols % 4 == 0) -> hi (and a second copy hi2) and lo
+// bf16 planes with their own row strides (null planes are skipped).
+struct SplitArgs {
+  const float *src;
+  int64_t rows, cols;
+  uint16_t *hi, *hi2, *lo;
+  int64_t ld_hi, ld_hi2, ld_lo;
+};
+
+__global__ __launch_bounds__(256) void tf32_split_kernel(SplitArgs p) {
+  const int64_t q = p.cols / 4;
+  const int64_t total = p.rows * q;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < total; i += stride) {
+    const int64_t r = i / q, c = (i - r * q) * 4;
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p.src + r * p.cols + c));
+    const uint32_t in[4] = {v.x, v.y, v.z, v.w};
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float t = __uint_as_float(tf32_rne_bits(in[e]));
+      h[e] = f32_to_bf16_rne(t);
+      l[e] = f32_to_bf16_rne(t - bf16_to_f32(h[e]));
+    }
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 hv = {h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+    const u32x2 lv = {l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
+    if (p.hi != nullptr) *reinterpret_cast<u32x2 *>(p.hi + r * p.ld_hi + c) = hv;
+    if (p.hi2 != nullptr) *reinterpret_cast<u32x2 *>(p.hi2 + r * p.ld_hi2 + c) = hv;
+    if (p.lo != nullptr) *reinterpret_cast<u32x2 *>(p.lo + r * p.ld_lo + c) = lv;
+  }
+}
+
+void launch_split(const SplitArgs &a, hipStream_t s) {
+  const int64_t n = a.rows * (a.cols / 4);
+  if (n <= 0) return;
+  const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(ceil_div(n, 256), 8192));
+  tf32_split_kernel<<<dim3(grid), dim3(256), 0, s>>>(a);
+}
+
+// out[i] = sum over s of part[s][i], s ascending (n % 4 == 0, 16-byte aligned).
+__global__ __launch_bounds__(256) void sum_planes_kernel(const float *part, int planes, int64_t n, float *out) {
+  const int64_t q = n / 4;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < q; i += stride) {
+    u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(part) + i);
+    float x = __uint_as_float(a.x), y = __uint_as_float(a.y), z = __uint_as_float(a.z), w = __uint_as_float(a.w);
+    for (int s = 1; s < planes; ++s) {
+      const u32x4 b = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(part + s * n) + i);
+      x += __uint_as_float(b.x);
+      y += __uint_as_float(b.y);
+      z += __uint_as_float(b.z);
+      w += __uint_as_float(b.w);
+    }
+    *(reinterpret_cast<u32x4 *>(out) + i) = u32x4{__float_as_uint(x), __float_as_uint(y), __float_as_uint(z), __float_as_uint(w)};
+  }
+}
+
+constexpr size_t kWsAlign = 256;
+size_t align_up(size_t x) { return (x + kWsAlign - 1) / kWsAlign * kWsAlign; }
 
 }  // namespace
 }  // namespace moe
@@ -516,6 +651,7 @@ int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, con
   p.K = K;
   p.G = G;
   p.ntiles = ceil_div(K, kBN);
+  p.chunk = 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   // 128-row tiles when the groups average at most 160 rows (less padding in
   // every group's last row tile), 256-row tiles otherwise.
@@ -558,7 +694,186 @@ int moe_grouped_gemm_wgrad(const moe_bf16_t *dy, const moe_bf16_t *x, int64_t M_
   p.K = K;
   p.G = G;
   p.ntiles = ceil_div(K, kBN);
+  p.chunk = 0;
   launch<true, 256, 2, 2>(p, G * ceil_div(N, 256) * p.ntiles, static_cast<hipStream_t>(stream));
+  return check_launch(fn);
+}
+
+size_t moe_router_dgrad_tf32_workspace_size(int64_t M, int64_t K, int64_t N) {
+  if (M < 0 || K < 0 || N < 0) return 0;
+  return moe::align_up(static_cast<size_t>(M) * 3 * K * 2) + moe::align_up(static_cast<size_t>(3 * K) * N * 2);
+}
+
+int moe_router_dgrad_tf32(const float *grad_output, int64_t M, int64_t K, const float *weight, int64_t N,
+                          float *grad_input, void *workspace, size_t workspace_bytes, void *stream) {
+  using namespace moe;
+  const char *fn = "moe_router_dgrad_tf32";
+  if (M < 0 || K < 0 || N < 0) {
+    return fail(MOE_ERR_SHAPE, "%s: negative size (M=%lld K=%lld N=%lld)", fn, (long long)M, (long long)K, (long long)N);
+  }
+  if (K % 8 != 0 || N % 8 != 0) return fail(MOE_ERR_SHAPE, "%s: K=%lld and N=%lld must be multiples of 8", fn, (long long)K, (long long)N);
+  if (3 * K > (int64_t(1) << 22) - 8 || N > (int64_t(1) << 22) - 8 || 3 * K * N > (int64_t(1) << 30) - 1) {
+    return fail(MOE_ERR_CAPACITY, "%s: K=%lld N=%lld exceed the 32-bit offsets (3K, N < 2^22, 3K*N < 2^30)", fn,
+                (long long)K, (long long)N);
+  }
+  if (M == 0 || N == 0) return MOE_OK;
+  if (grad_input == nullptr || (K > 0 && (grad_output == nullptr || weight == nullptr))) {
+    return fail(MOE_ERR_INVALID_ARG, "%s: null grad_output, weight or grad_input", fn);
+  }
+  if (!is_aligned(grad_output, 16) || !is_aligned(weight, 16) || !is_aligned(grad_input, 16)) {
+    return fail(MOE_ERR_ALIGN, "%s: grad_output, weight and grad_input must be 16-byte aligned", fn);
+  }
+  const size_t need = moe_router_dgrad_tf32_workspace_size(M, K, N);
+  if (workspace == nullptr || workspace_bytes < need || !is_aligned(workspace, kWsAlign)) {
+    return fail(MOE_ERR_WORKSPACE, "%s: a 256-byte aligned workspace of %zu bytes is needed (got %zu)", fn, need,
+                workspace == nullptr ? size_t(0) : workspace_bytes);
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // A' = [A_hi | A_hi | A_lo] [M, 3K] and B' = [B_hi; B_lo; B_hi] [3K, N]:
+  // A' B' = A_hi B_hi + A_hi B_lo + A_lo B_hi, one GEMM with a 3K reduction.
+  uint16_t *a3 = static_cast<uint16_t *>(workspace);
+  uint16_t *b3 = reinterpret_cast<uint16_t *>(static_cast<char *>(workspace) + align_up(static_cast<size_t>(M) * 3 * K * 2));
+  SplitArgs sa{grad_output, M, K, a3, a3 + K, a3 + 2 * K, 3 * K, 3 * K, 3 * K};
+  SplitArgs sb{weight, K, N, b3, b3 + 2 * K * N, b3 + K * N, N, N, N};
+  launch_split(sa, s);
+  launch_split(sb, s);
+  if (int rc = check_launch(fn)) return rc;
+  BwdArgs p;
+  p.a = a3;
+  p.b = b3;
+  p.offsets = nullptr;
+  p.out = grad_input;
+  p.M = M;
+  p.N = 3 * K;
+  p.K = N;
+  p.G = 1;
+  p.ntiles = ceil_div(N, kBN);
+  p.chunk = M;
+  if (M <= 160) launch<false, 128, 1, 3, 1>(p, (ceil_div(M, 128) + 1) * p.ntiles, s);
+  else launch<false, 256, 2, 2, 1>(p, (ceil_div(M, 256) + 1) * p.ntiles, s);
+  return check_launch(fn);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Reduction split of the tf32 router wgrad: the output has few tiles
+// (case31: 2 x 32 for 256 CUs), so the 2M + M stacked rows are cut into
+// uniform chunks run as groups of one launch each, every chunk writing its own
+// fp32 partial [N, K]; a last pass adds the partials in chunk order.
+struct WgradPlan {
+  int64_t s1, s2;       // chunks of pass 1 (2M rows) and pass 2 (M rows); 1 and 1 = no split
+  int64_t c1, c2;       // rows per chunk
+};
+
+WgradPlan wgrad_plan(int64_t M, int64_t N, int64_t K) {
+  WgradPlan pl{1, 1, 2 * M, M};
+  const int64_t tiles = moe::ceil_div(N, 256) * moe::ceil_div(K, 256);
+  if (M == 0 || tiles >= 256) return pl;
+  auto chunks = [&](int64_t rows) {
+    int64_t s = std::min<int64_t>(moe::ceil_div(512, tiles), std::max<int64_t>(1, rows / 512));
+    return std::max<int64_t>(1, std::min<int64_t>(s, 64));
+  };
+  pl.s1 = chunks(2 * M);
+  pl.s2 = chunks(M);
+  if (pl.s1 == 1 && pl.s2 == 1) return pl;
+  // Chunks are multiples of 64 rows (whole reduction steps).
+  pl.c1 = moe::ceil_div(moe::ceil_div(2 * M, pl.s1), 64) * 64;
+  pl.c2 = moe::ceil_div(moe::ceil_div(M, pl.s2), 64) * 64;
+  pl.s1 = moe::ceil_div(2 * M, pl.c1);
+  pl.s2 = moe::ceil_div(M, pl.c2);
+  return pl;
+}
+
+size_t wgrad_planes_bytes(const WgradPlan &pl, int64_t N, int64_t K) {
+  return (pl.s1 == 1 && pl.s2 == 1) ? 0 : moe::align_up(static_cast<size_t>(pl.s1 + pl.s2) * N * K * 4);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t moe_router_wgrad_tf32_workspace_size(int64_t M, int64_t N, int64_t K) {
+  if (M < 0 || N < 0 || K < 0) return 0;
+  return moe::align_up(static_cast<size_t>(2 * M) * N * 2) + moe::align_up(static_cast<size_t>(M) * N * 2) +
+         moe::align_up(static_cast<size_t>(2 * M) * K * 2) + wgrad_planes_bytes(wgrad_plan(M, N, K), N, K);
+}
+
+int moe_router_wgrad_tf32(const float *grad_output, int64_t M, int64_t N, const float *inp, int64_t K,
+                          float *grad_weight, void *workspace, size_t workspace_bytes, void *stream) {
+  using namespace moe;
+  const char *fn = "moe_router_wgrad_tf32";
+  if (M < 0 || K < 0 || N < 0) {
+    return fail(MOE_ERR_SHAPE, "%s: negative size (M=%lld N=%lld K=%lld)", fn, (long long)M, (long long)N, (long long)K);
+  }
+  if (K % 8 != 0 || N % 8 != 0) return fail(MOE_ERR_SHAPE, "%s: N=%lld and K=%lld must be multiples of 8", fn, (long long)N, (long long)K);
+  if (2 * M * N > (int64_t(1) << 30) - 1 || 2 * M * K > (int64_t(1) << 30) - 1 || N * K > (int64_t(1) << 30) - 1) {
+    return fail(MOE_ERR_CAPACITY, "%s: M=%lld N=%lld K=%lld exceed the 32-bit offsets (2M*N, 2M*K, N*K < 2^30)", fn,
+                (long long)M, (long long)N, (long long)K);
+  }
+  if (N == 0 || K == 0) return MOE_OK;
+  if (grad_weight == nullptr || (M > 0 && (grad_output == nullptr || inp == nullptr))) {
+    return fail(MOE_ERR_INVALID_ARG, "%s: null grad_output, inp or grad_weight", fn);
+  }
+  if (!is_aligned(grad_output, 16) || !is_aligned(inp, 16) || !is_aligned(grad_weight, 16)) {
+    return fail(MOE_ERR_ALIGN, "%s: grad_output, inp and grad_weight must be 16-byte aligned", fn);
+  }
+  const size_t need = moe_router_wgrad_tf32_workspace_size(M, N, K);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need || !is_aligned(workspace, kWsAlign))) {
+    return fail(MOE_ERR_WORKSPACE, "%s: a 256-byte aligned workspace of %zu bytes is needed (got %zu)", fn, need,
+                workspace == nullptr ? size_t(0) : workspace_bytes);
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // Pass 1: [A_hi; A_hi]^T [B_hi; B_lo] over 2M stacked rows; pass 2:
+  // A_lo^T B_hi.  A = grad_output [M, N], B = inp [M, K].
+  char *w = static_cast<char *>(workspace);
+  const size_t sz_a1 = align_up(static_cast<size_t>(2 * M) * N * 2), sz_a2 = align_up(static_cast<size_t>(M) * N * 2);
+  const size_t sz_b1 = align_up(static_cast<size_t>(2 * M) * K * 2);
+  uint16_t *a1 = reinterpret_cast<uint16_t *>(w);
+  uint16_t *a2 = reinterpret_cast<uint16_t *>(w + sz_a1);
+  uint16_t *b1 = reinterpret_cast<uint16_t *>(w + sz_a1 + sz_a2);
+  float *planes = reinterpret_cast<float *>(w + sz_a1 + sz_a2 + sz_b1);
+  if (M > 0) {
+    SplitArgs sa{grad_output, M, N, a1, a1 + M * N, a2, N, N, N};
+    SplitArgs sb{inp, M, K, b1, nullptr, b1 + M * K, K, 0, K};
+    launch_split(sa, s);
+    launch_split(sb, s);
+    if (int rc = check_launch(fn)) return rc;
+  }
+  const WgradPlan pl = wgrad_plan(M, N, K);
+  const bool split = !(pl.s1 == 1 && pl.s2 == 1);
+  BwdArgs p;
+  p.a = a1;
+  p.b = b1;
+  p.offsets = nullptr;
+  p.out = split ? static_cast<void *>(planes) : static_cast<void *>(grad_weight);
+  p.M = 2 * M;
+  p.N = N;
+  p.K = K;
+  p.G = pl.s1;
+  p.ntiles = ceil_div(K, kBN);
+  p.chunk = pl.c1;
+  const int64_t tiles = ceil_div(N, 256) * p.ntiles;
+  launch<true, 256, 2, 2, 1>(p, tiles * p.G, s);
+  if (M > 0) {
+    p.a = a2;
+    p.M = M;
+    p.G = pl.s2;
+    p.chunk = pl.c2;
+    if (split) {
+      p.out = planes + pl.s1 * N * K;
+      launch<true, 256, 2, 2, 1>(p, tiles * p.G, s);
+    } else {
+      launch<true, 256, 2, 2, 2>(p, tiles, s);
+    }
+  }
+  if (split) {
+    const int64_t q = N * K / 4;
+    const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(ceil_div(q, 256), 4096));
+    sum_planes_kernel<<<dim3(grid), dim3(256), 0, s>>>(planes, static_cast<int>(pl.s1 + (M > 0 ? pl.s2 : 0)), N * K,
+                                                       grad_weight);
+  }
   return check_launch(fn);
 }
 

@@ -145,6 +145,44 @@ def cast(x: torch.Tensor, dtype: torch.dtype, *, out: Optional[torch.Tensor] = N
     return out
 
 
+def _ws(nbytes: int, device) -> Optional[torch.Tensor]:
+    return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
+
+
+def router_dgrad_tf32(grad_output: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """grad_input [M, N] = tf32(grad_output [M, K]) @ tf32(weight [K, N]), fp32 in/accumulate/out."""
+    for n, t in (("grad_output", grad_output), ("weight", weight)):
+        _on_gpu(n, t)
+        _dtype(n, t, torch.float32)
+    if grad_output.ndim != 2 or weight.ndim != 2 or grad_output.shape[1] != weight.shape[0]:
+        raise ValueError(f"shapes grad_output {tuple(grad_output.shape)} weight {tuple(weight.shape)}: need [M,K] @ [K,N]")
+    M, K = grad_output.shape
+    N = weight.shape[1]
+    go, wc = grad_output.contiguous(), weight.contiguous()
+    out = torch.empty(M, N, dtype=torch.float32, device=go.device)
+    nbytes = _lib.lib().moe_router_dgrad_tf32_workspace_size(M, K, N)
+    ws = _ws(nbytes, go.device)
+    call("moe_router_dgrad_tf32", ptr(go), M, K, ptr(wc), N, ptr(out), ptr(ws), nbytes, stream_handle())
+    return out
+
+
+def router_wgrad_tf32(grad_output: torch.Tensor, inp: torch.Tensor) -> torch.Tensor:
+    """grad_weight [N, K] = tf32(grad_output [M, N])^T @ tf32(inp [M, K]), fp32 in/accumulate/out."""
+    for n, t in (("grad_output", grad_output), ("inp", inp)):
+        _on_gpu(n, t)
+        _dtype(n, t, torch.float32)
+    if grad_output.ndim != 2 or inp.ndim != 2 or grad_output.shape[0] != inp.shape[0]:
+        raise ValueError(f"shapes grad_output {tuple(grad_output.shape)} inp {tuple(inp.shape)}: need [M,N] and [M,K]")
+    M, N = grad_output.shape
+    K = inp.shape[1]
+    go, ic = grad_output.contiguous(), inp.contiguous()
+    out = torch.empty(N, K, dtype=torch.float32, device=go.device)
+    nbytes = _lib.lib().moe_router_wgrad_tf32_workspace_size(M, N, K)
+    ws = _ws(nbytes, go.device)
+    call("moe_router_wgrad_tf32", ptr(go), M, N, ptr(ic), K, ptr(out), ptr(ws), nbytes, stream_handle())
+    return out
+
+
 # ---------------------------------------------------------------- row-id map
 def row_id_map(routing_map: torch.Tensor, *, expert_major: bool = True, token_major: bool = True,
                expert_major_i32: bool = False, expert_offsets: bool = False,

@@ -36,6 +36,8 @@
  *                 (dgrad, no bundle)
  *   case05/case09 kernel_cases/case09_moe_grouped_gemm_fc1_wgrad.py:57-64 (wgrad, no bundle)
  *   case38        kernel_cases/case38_ref_musa_asm_bf16_ssgemm_nt_320x256.py:46-53 (router logits)
+ *   case39/case31 kernel_cases/case39_ref_musa_asm_tf32_ssgemm_nn_384x256.py:61-68,
+ *                 kernel_cases/case31_ref_musa_asm_tf32_ssgemm_tn_128x256.py:61-68 (tf32 router GEMMs)
  *   case11/case25 kernel_cases/case11_router_bwd_cast_bf16_to_fp32.py:43-44,
  *                 kernel_cases/case25_ref_unary_cast_fp32_to_bf16.py:56-72 (casts)
  */
@@ -49,7 +51,7 @@
 extern "C" {
 #endif
 
-#define MOE_DISPATCH_ABI_VERSION 5
+#define MOE_DISPATCH_ABI_VERSION 6
 
 typedef uint16_t moe_bf16_t;
 
@@ -289,6 +291,30 @@ int moe_router_topk(const moe_bf16_t *inp, int64_t M, int64_t K, const moe_bf16_
  * vector path).  Workspace: none. */
 int moe_cast_bf16_to_f32(const moe_bf16_t *src, int64_t n, float *dst, void *stream);
 int moe_cast_f32_to_bf16(const float *src, int64_t n, moe_bf16_t *dst, void *stream);
+
+/* ---- router backward GEMMs in tf32 -------------------------------------
+ * Replace case39's router dgrad te_general_gemm(weight.to(fp32), grad_output,
+ * layout="NN") and case31's router wgrad te_general_gemm(inp.to(fp32),
+ * grad_output, layout="NT"): golden reference_tf32
+ * (kernel_cases/case39_ref_musa_asm_tf32_ssgemm_nn_384x256.py:61-68,
+ *  kernel_cases/case31_ref_musa_asm_tf32_ssgemm_tn_128x256.py:61-68): both fp32
+ * operands rounded to tf32 (round_tf32_rne, :51-58), products accumulated in
+ * fp32, fp32 out.  Computed on the bf16 matrix cores: each tf32 value t is
+ * split into bf16 hi = RNE(t) and lo = t - hi (exact) and a b is taken as
+ * hi_a hi_b + hi_a lo_b + lo_a hi_b (the dropped lo_a lo_b is below
+ * 2^-16 |a b|); every partial product is exact in the fp32 accumulator.
+ *   dgrad: grad_input [M, N] = tf32(grad_output [M, K]) @ tf32(weight [K, N])
+ *   wgrad: grad_weight [N, K] = tf32(grad_output [M, N])^T @ tf32(inp [M, K])
+ * Limits: the column counts (K and N) % 8 == 0; dgrad 3K, N < 2^22 and
+ *   3K*N < 2^30; wgrad 2M*N, 2M*K, N*K < 2^30; 16-byte aligned tensors.
+ * Workspace: the *_workspace_size bytes, 256-byte aligned (the bf16 hi/lo
+ *   planes; case31: 2 M K + 3 M N bf16 values). */
+size_t moe_router_dgrad_tf32_workspace_size(int64_t M, int64_t K, int64_t N);
+int moe_router_dgrad_tf32(const float *grad_output, int64_t M, int64_t K, const float *weight, int64_t N,
+                          float *grad_input, void *workspace, size_t workspace_bytes, void *stream);
+size_t moe_router_wgrad_tf32_workspace_size(int64_t M, int64_t N, int64_t K);
+int moe_router_wgrad_tf32(const float *grad_output, int64_t M, int64_t N, const float *inp, int64_t K,
+                          float *grad_weight, void *workspace, size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -326,6 +326,31 @@ def router_logits_fp32(inp: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     return inp.float().matmul(weight.float().t())
 
 
+def round_tf32_rne(x: torch.Tensor) -> torch.Tensor:
+    """fp32 -> tf32 (10 mantissa bits), ties to even, as fp32 values.
+
+    kernel_cases/case39_ref_musa_asm_tf32_ssgemm_nn_384x256.py:51-58 (= case31...:52-58):
+    add 0x1000 unless the 13 dropped bits are exactly 0x1000 with an even kept LSB, then clear them.
+    """
+    bits = x.float().contiguous().view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+    low = bits & 0x1FFF
+    lsb = (bits >> 13) & 1
+    add = torch.where((low == 0x1000) & (lsb == 0), torch.zeros_like(bits), torch.full_like(bits, 0x1000))
+    out = ((bits + add) & 0xFFFFE000) & 0xFFFFFFFF
+    out = torch.where(out >= 2 ** 31, out - 2 ** 32, out)
+    return out.to(torch.int32).view(torch.float32).view_as(x)
+
+
+def router_dgrad_tf32(grad_output: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """tf32(grad_output) @ tf32(weight) in fp32: case39...:61-68 (reference_tf32)."""
+    return round_tf32_rne(grad_output).matmul(round_tf32_rne(weight))
+
+
+def router_wgrad_tf32(grad_output: torch.Tensor, inp: torch.Tensor) -> torch.Tensor:
+    """tf32(grad_output)^T @ tf32(inp) in fp32: case31...:61-68 (reference_tf32)."""
+    return round_tf32_rne(grad_output).transpose(0, 1).matmul(round_tf32_rne(inp))
+
+
 def swiglu(y: torch.Tensor) -> torch.Tensor:
     """silu(y[:, :F]) * y[:, F:] in fp32, F = N/2 (gate first).  No reference function."""
     f = y.shape[1] // 2

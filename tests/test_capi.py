@@ -17,7 +17,7 @@ L = pkg._lib
 def test_library_loads_and_exports_header_symbols():
     lib = L.lib()
     declared = L.header_functions()
-    assert len(declared) == len(L.SIGNATURES) == 21
+    assert len(declared) == len(L.SIGNATURES) == 25
     assert set(declared) == set(L.SIGNATURES)
     for name in declared:
         assert hasattr(lib, name), name
@@ -103,6 +103,13 @@ FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
     ("moe_cast_f32_to_bf16", (FAKE, -1, FAKE, None), L.MOE_ERR_SHAPE, "negative"),
     ("moe_cast_f32_to_bf16", (None, 8, FAKE, None), L.MOE_ERR_INVALID_ARG, "null"),
     ("moe_cast_bf16_to_f32", (FAKE, 8, None, None), L.MOE_ERR_INVALID_ARG, "null"),
+    ("moe_router_dgrad_tf32", (FAKE, 64, 12, FAKE, 64, FAKE, FAKE, 1 << 20, None), L.MOE_ERR_SHAPE, "multiples of 8"),
+    ("moe_router_dgrad_tf32", (FAKE, 64, 16, FAKE, 64, FAKE, None, 0, None), L.MOE_ERR_WORKSPACE, "workspace"),
+    ("moe_router_dgrad_tf32", (FAKE, 64, 16, FAKE, 64, None, FAKE, 1 << 20, None), L.MOE_ERR_INVALID_ARG, "null"),
+    ("moe_router_dgrad_tf32", (FAKE, 64, 1 << 21, FAKE, 64, FAKE, FAKE, 1 << 20, None), L.MOE_ERR_CAPACITY, "32-bit"),
+    ("moe_router_wgrad_tf32", (FAKE, 64, 16, FAKE, 20, FAKE, FAKE, 1 << 20, None), L.MOE_ERR_SHAPE, "multiples of 8"),
+    ("moe_router_wgrad_tf32", (FAKE, 64, 16, FAKE, 16, FAKE, None, 0, None), L.MOE_ERR_WORKSPACE, "workspace"),
+    ("moe_router_wgrad_tf32", (FAKE, 1 << 20, 1 << 10, FAKE, 16, FAKE, FAKE, 1 << 20, None), L.MOE_ERR_CAPACITY, "32-bit"),
     # wgrad (dy, x, M, N, K, G, offsets, dw, ws, ws_bytes, stream)
     ("moe_grouped_gemm_wgrad", (FAKE, FAKE, 4, 16, 16, 5000, FAKE, FAKE, None, 0, None), L.MOE_ERR_CAPACITY, "4096"),
     ("moe_grouped_gemm_wgrad", (FAKE, FAKE, 4, 16, 10, 1, FAKE, FAKE, None, 0, None), L.MOE_ERR_SHAPE, "multiples of 8"),

@@ -1,0 +1,73 @@
+"""GPU parity of the tf32 router backward GEMMs (case39 dgrad, case31 wgrad).
+
+The golden (reference_tf32, case39...:61-68 / case31...:61-68) multiplies tf32-rounded operands
+exactly and accumulates in fp32.  Here every tf32 product is three exact bf16 products (the
+dropped lo*lo term is below 2^-16 |a b|) accumulated in fp32 in another order, so the bound is
+|ours - golden| <= 1e-4 * sum_k |a_k b_k| + 1e-5.  The cases' own checks against an explicit sum
+(case39: 1e-3, case31: 1e-2 absolute) are applied as written at full size.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import ref_torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _bound_check(got, ref, absprod, what):
+    err = (got.cpu().double() - ref.double()).abs()
+    bound = 1e-4 * absprod.double() + 1e-5
+    assert bool((err <= bound).all()), f"{what}: worst err/bound {(err / bound).max().item():.3f}"
+
+
+@pytest.mark.parametrize("M,K,N", [(64, 64, 256), (5, 8, 8), (300, 320, 520), (1000, 64, 8192), (130, 1000, 264)])
+def test_router_dgrad_tf32_shapes(pkg, dev, M, K, N):
+    g = torch.Generator().manual_seed(M + K + N)
+    go = torch.randn(M, K, generator=g)
+    w = torch.randn(K, N, generator=g).to(torch.bfloat16).float()
+    got = pkg.ops.router_dgrad_tf32(go.to(dev), w.to(dev))
+    ref = ref_torch.router_dgrad_tf32(go, w)
+    absprod = ref_torch.round_tf32_rne(go).abs() @ ref_torch.round_tf32_rne(w).abs()
+    _bound_check(got, ref, absprod, f"dgrad M={M} K={K} N={N}")
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 64, 256), (5, 8, 8), (1000, 320, 520), (4096, 64, 1000), (0, 16, 24)])
+def test_router_wgrad_tf32_shapes(pkg, dev, M, N, K):
+    g = torch.Generator().manual_seed(3 * M + N + K)
+    go = torch.randn(M, N, generator=g)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).float()
+    got = pkg.ops.router_wgrad_tf32(go.to(dev), x.to(dev))
+    assert got.shape == (N, K)
+    ref = ref_torch.router_wgrad_tf32(go, x)
+    absprod = ref_torch.round_tf32_rne(go).abs().t() @ ref_torch.round_tf32_rne(x).abs()
+    _bound_check(got, ref, absprod, f"wgrad M={M} N={N} K={K}")
+
+
+def test_case39_full_size(pkg, dev):
+    case = pkg.cases.case39_ref_musa_asm_tf32_ssgemm_nn_384x256
+    go, w = case.make_inputs(seed=0, device=dev)
+    got = case.kernel_function(go, w)
+    assert got.shape == (case.M, case.N) and got.dtype == torch.float32
+    a, b = ref_torch.round_tf32_rne(go), ref_torch.round_tf32_rne(w)
+    ref = a @ b
+    bound = 1e-4 * (a.abs() @ b.abs()) + 1e-5
+    assert bool(((got - ref).abs() <= bound).all())
+    rows = torch.tensor([0, case.M // 2, case.M - 1], device=dev)
+    manual = (a[rows].double().unsqueeze(-1) * b.double().unsqueeze(0)).sum(dim=1)
+    assert (got[rows].double() - manual).abs().max().item() <= 1e-3
+
+
+def test_case31_full_size(pkg, dev):
+    case = pkg.cases.case31_ref_musa_asm_tf32_ssgemm_tn_128x256
+    go, x = case.make_inputs(seed=0, device=dev)
+    got = case.kernel_function(go, x)
+    assert got.shape == (case.N, case.K) and got.dtype == torch.float32
+    a, b = ref_torch.round_tf32_rne(go), ref_torch.round_tf32_rne(x)
+    ref = a.t() @ b
+    bound = 1e-4 * (a.abs().t() @ b.abs()) + 1e-5
+    assert bool(((got - ref).abs() <= bound).all())
+    cols = torch.tensor([0, case.N // 2, case.N - 1], device=dev)
+    manual = torch.stack([(a[:, c].double().unsqueeze(1) * b.double()).sum(dim=0) for c in cols.tolist()])
+    assert (got[cols].double() - manual).abs().max().item() <= 1e-2

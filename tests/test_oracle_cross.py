@@ -356,6 +356,36 @@ def test_router_logits_fp32_against_explicit_sum():
     assert got.shape == (5, 7) and got.dtype == torch.float32
 
 
+def test_round_tf32_known_answers_and_bound():
+    # The case's own tie checks (case39...:70-79): 1.0 + half ulp stays, 1.0 + 1.5 ulp rounds up.
+    ties = torch.tensor([0x3F801000, 0x3F803000], dtype=torch.int32).view(torch.float32)
+    got = ref_torch.round_tf32_rne(ties).view(torch.int32).tolist()
+    assert got == [0x3F800000, 0x3F804000]
+    # Independent restatement: nearest multiple of 2^(e-10) (ties to even) via float64.
+    g = torch.Generator().manual_seed(57)
+    x = torch.randn(20000, generator=g) * torch.exp(torch.randn(20000, generator=g) * 5)
+    r = ref_torch.round_tf32_rne(x)
+    assert bool(((r.view(torch.int32) & 0x1FFF) == 0).all())
+    xd = x.double().numpy()
+    e = np.floor(np.log2(np.abs(xd)))
+    q = 2.0 ** (e - 10)
+    ref = np.round(xd / q) * q   # numpy rounds half to even
+    assert np.array_equal(r.double().numpy(), ref)
+
+
+def test_router_tf32_gemms_against_float64():
+    g = torch.Generator().manual_seed(58)
+    a = torch.randn(9, 24, generator=g)
+    b = torch.randn(24, 16, generator=g)
+    got = ref_torch.router_dgrad_tf32(a, b)
+    ref = ref_torch.round_tf32_rne(a).double().numpy() @ ref_torch.round_tf32_rne(b).double().numpy()
+    assert np.allclose(got.numpy(), ref, rtol=1e-6, atol=1e-5)
+    x = torch.randn(9, 16, generator=g)
+    got = ref_torch.router_wgrad_tf32(a, x)
+    ref = ref_torch.round_tf32_rne(a).double().numpy().T @ ref_torch.round_tf32_rne(x).double().numpy()
+    assert got.shape == (24, 16) and np.allclose(got.numpy(), ref, rtol=1e-6, atol=1e-5)
+
+
 def test_swiglu_closed_form():
     y = torch.tensor([[0.0, 1.0, 2.0, -3.0], [-1.0, 4.0, 0.5, 0.25]])
     h = ref_torch.swiglu(y).double().numpy()
