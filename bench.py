@@ -15,7 +15,9 @@ The stand-alone permute kernel (x -> permuted rows) is timed separately on the
 same map, after the timed steps, and reported under "standalone"; the four
 grouped GEMMs of the layer's backward (dgrad and wgrad of fc1 and fc2, on the
 same routing) and the reference backward cases at their own shapes are timed
-after that and reported under "backward" (neither is part of `value`).
+after that and reported under "backward", the router front end and backward
+(router GEMM, its top-k, the reference router cases) under "router" (none of
+them is part of `value`).
 
 Prints ONE JSON line: tokens/s of the whole step, per-stage device times
 (HIP events on the launch stream, averaged over the timed steps) with their
@@ -186,6 +188,50 @@ def backward_gemms(pkg, x, row_map, offs, h, w1, w2, dev, library=False):
     return out
 
 
+def router_section(pkg, x, dev):
+    """The router front end and its backward (not part of the timed step): the c5 router GEMM on this
+    batch's x with a random [E, H] gate, alone and with the top-k, and the reference router cases at
+    their own shapes (case38 logits, case39/case31 tf32 dgrad/wgrad, case11/case25 casts)."""
+    ops, inp = pkg.ops, pkg.inputs
+    T, H = x.shape
+    E, k = CFG["experts"], CFG["topk"]
+    wr = inp.randn_bf16((E, H), std=0.02, seed=SEED + 50, device=dev)
+    out = {}
+    ms = _time_ms(lambda: ops.router_logits(x, wr))
+    out["c5_router_logits"] = {"ms": round(ms, 4), "TFLOP/s": round(2 * T * H * E / (ms * 1e-3) / 1e12, 2),
+                               "GB/s": round(2 * (T * H + E * H) / (ms * 1e-3) / 1e9, 2)}
+    ms = _time_ms(lambda: ops.router_topk(x, wr, k, with_logits=True, with_mask=True, with_probs=True))
+    out["c5_router_topk"] = {"ms": round(ms, 4)}
+    cases = {}
+    c = pkg.cases.case38_ref_musa_asm_bf16_ssgemm_nt_320x256
+    a, b = c.make_inputs(seed=0, device=dev)
+    ms = _time_ms(lambda: c.kernel_function(a, b))
+    cases["case38"] = {"ms": round(ms, 4), "TFLOP/s": round(2 * c.M * c.K * c.N / (ms * 1e-3) / 1e12, 2)}
+    del a, b
+    c = pkg.cases.case39_ref_musa_asm_tf32_ssgemm_nn_384x256
+    a, b = c.make_inputs(seed=0, device=dev)
+    ms = _time_ms(lambda: c.kernel_function(a, b))
+    cases["case39"] = {"ms": round(ms, 4), "tf32 TFLOP/s": round(2 * c.M * c.K * c.N / (ms * 1e-3) / 1e12, 2)}
+    del a, b
+    c = pkg.cases.case31_ref_musa_asm_tf32_ssgemm_tn_128x256
+    a, b = c.make_inputs(seed=0, device=dev)
+    ms = _time_ms(lambda: c.kernel_function(a, b))
+    cases["case31"] = {"ms": round(ms, 4), "tf32 TFLOP/s": round(2 * c.M * c.K * c.N / (ms * 1e-3) / 1e12, 2)}
+    del a, b
+    c = pkg.cases.case11_router_bwd_cast_bf16_to_fp32
+    (a,) = c.get_inputs(dev)
+    ms = _time_ms(lambda: c.kernel_function(a))
+    cases["case11"] = {"ms": round(ms, 4), "GB/s": round(a.numel() * 6 / (ms * 1e-3) / 1e9, 2)}
+    del a
+    c = pkg.cases.case25_ref_unary_cast_fp32_to_bf16
+    a = c.make_inputs(seed=0, device=dev)
+    ms = _time_ms(lambda: c.kernel_function(a))
+    cases["case25"] = {"ms": round(ms, 4), "GB/s": round(a.numel() * 6 / (ms * 1e-3) / 1e9, 2)}
+    del a
+    out["reference_cases"] = cases
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -200,6 +246,8 @@ def main():
                          "(E x [R/E, H] @ [H, 2F]): a library GEMM of the same size, reported beside the stages")
     ap.add_argument("--no-backward", action="store_true",
                     help="skip the backward grouped GEMMs (reported beside the forward, not in value)")
+    ap.add_argument("--no-router", action="store_true",
+                    help="skip the router front end / router backward timings (reported beside the forward)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the MoE dispatch path here has no multi-GPU (expert-parallel) "
@@ -309,6 +357,8 @@ def main():
         backward = backward_gemms(pkg, x, maps["token_major"], maps["expert_offsets"], b["h"], w1, w2, dev,
                                   library=args.library_reference)
 
+    router = None if args.no_router else router_section(pkg, x, dev)
+
     library = None
     if args.library_reference:
         library = library_reference(T * k // E, H, 2 * F, E, dev)
@@ -332,6 +382,8 @@ def main():
     }
     if backward is not None:
         line["backward"] = backward
+    if router is not None:
+        line["router"] = router
     if library is not None:
         line["library_reference"] = library
     print(json.dumps(line))
