@@ -232,6 +232,110 @@ def router_section(pkg, x, dev):
     return out
 
 
+def _median_ms(fn, flush, reps=50, warm=25):
+    """Median device time of fn over `reps` calls after `warm` calls; 1 GiB is overwritten before each
+    timed call so no input is served from the 256 MB Infinity Cache."""
+    for _ in range(warm):
+        fn()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    times = []
+    for _ in range(reps):
+        flush.zero_()
+        ev[0].record()
+        fn()
+        ev[1].record()
+        torch.cuda.synchronize()
+        times.append(ev[0].elapsed_time(ev[1]))
+    return statistics.median(times)
+
+
+def _rate(ms, amount, unit):
+    rate = amount / (ms * 1e-3) / (1e9 if unit == "GB/s" else 1e12)
+    peak = HBM_PEAK_GBS if unit == "GB/s" else BF16_PEAK_TFLOPS
+    return {"ms": round(ms, 4), unit: round(rate, 2), "frac_of_peak": round(rate / peak, 4),
+            ("bytes" if unit == "GB/s" else "flops"): amount}
+
+
+def config_lines(pkg, dev):
+    """Per-kernel figures at the baseline configs C1-C5 and the reference-case shapes: median of 50
+    timed calls after 25 warm-up calls, 1 GiB flushed before each call (one JSON line per config)."""
+    ops, inp = pkg.ops, pkg.inputs
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    lines = []
+    for name, cfg in inp.CONFIGS.items():
+        T, H, E, k = cfg["tokens"], cfg["hidden"], cfg["experts"], cfg["topk"]
+        seed = inp.SEED_CONFIG_BASE + int(name[1:])
+        logits = inp.router_logits(T, E, skew=cfg["skew"], seed=seed, device=dev)
+        x = inp.randn_bf16((T, H), seed=seed + 1, device=dev)
+        _, _, mask, probs = ops.topk(logits, k, with_mask=True, with_probs=True)
+        maps = ops.row_id_map(mask, expert_major=True, token_major=True, expert_major_i32=True, expert_offsets=True)
+        R = int(maps["expert_offsets"][-1].item())
+        tm = maps["token_major"]
+        res = {"topk": _rate(_median_ms(lambda: ops.topk(logits, k, with_mask=True, with_probs=True), flush),
+                             4 * T * E + 12 * T * k + T * E + 4 * T * E, "GB/s")}
+        res["row_id_map_int64_both"] = _rate(_median_ms(lambda: ops.row_id_map(mask), flush), T * E + 16 * T * E, "GB/s")
+        res["row_id_map_int32_em"] = _rate(_median_ms(
+            lambda: ops.row_id_map(mask, expert_major=False, token_major=False, expert_major_i32=True), flush),
+            T * E + 4 * T * E, "GB/s")
+        xp = torch.empty(R, H, dtype=torch.bfloat16, device=dev)
+        pp = torch.empty(R, dtype=torch.float32, device=dev)
+        res["permute_with_probs"] = _rate(_median_ms(
+            lambda: ops.permute(x, tm, probs, num_out=R, layout=ops.TOKEN_MAJOR, zero_tail=False, out=xp,
+                                permuted_probs=pp), flush),
+            2 * T * H + 8 * T * E + 4 * T * E + 2 * R * H + 4 * R, "GB/s")
+        res["unpermute_merge"] = _rate(_median_ms(
+            lambda: ops.unpermute(xp, tm, probs, layout=ops.TOKEN_MAJOR), flush),
+            2 * R * H + 8 * T * E + 4 * T * E + 2 * T * H, "GB/s")
+        if name == "c2":
+            g = inp.randn_bf16((R, H), seed=seed + 2, device=dev)
+            dpp = torch.randn(R, device=dev)
+            em = maps["expert_major"]
+            res["permute_bwd"] = _rate(_median_ms(lambda: ops.permute_bwd(g, dpp, em), flush),
+                                       2 * R * H + 4 * R + 8 * T * E + 2 * T * H + 4 * T * E, "GB/s")
+            del g
+        del xp, pp
+        lines.append({"config": name, "tokens": T, "hidden": H, "experts": E, "topk": k, "routed_rows": R,
+                      "kernels": res})
+    for name, cfg in inp.GEMM_CONFIGS.items():
+        seed = inp.SEED_CONFIG_BASE + int(name[1:])
+        G, K, N = cfg["groups"], cfg["K"], cfg["N"]
+        variants = {"zipf": inp.zipf_group_sizes(cfg["total"], G, seed=seed)}
+        if name == "c4":
+            variants["uniform_8192"] = [8192] * G
+        res = {}
+        for vname, sizes in variants.items():
+            M = sum(sizes)
+            a = inp.randn_bf16((M, K), seed=seed + 1, device=dev)
+            w = inp.randn_bf16((G, N, K), std=0.02, seed=seed + 2, device=dev)
+            offs = ops.group_offsets_from_splits(sizes, dev)
+            out = torch.empty(M, N // 2 if cfg["swiglu"] else N, dtype=torch.bfloat16, device=dev)
+            ms = _median_ms(lambda: ops.grouped_gemm(a, w, offs, swiglu=cfg["swiglu"], out=out), flush, reps=20, warm=5)
+            res[("fc1_swiglu" if cfg["swiglu"] else "fc2") + "_" + vname] = dict(_rate(ms, 2 * M * K * N, "TFLOP/s"),
+                                                                                group_rows=sizes)
+            del a, w, out
+        lines.append({"config": name, "groups": G, "K": K, "N": N, "kernels": res})
+    # Reference-case shapes (T=16384, E=320, H=8192): case12's mask, case17 permute, case15 unpermute.
+    rm, sel = inp.reference_routing_mask()
+    mask = rm.to(dev)
+    T, E, H = mask.shape[0], mask.shape[1], 8192
+    maps = ops.row_id_map(mask, expert_major=True, token_major=True)
+    R = int(mask.sum().item())
+    xr, probs = inp.case17_x_probs(sel)
+    xr, probs = xr.to(dev), probs.to(dev)
+    res = {"row_id_map_int64_both": _rate(_median_ms(lambda: ops.row_id_map(mask), flush), T * E + 16 * T * E, "GB/s")}
+    tm, em = maps["token_major"], maps["expert_major"]
+    xp = torch.empty(R, H, dtype=torch.bfloat16, device=dev)
+    pp = torch.empty(R, dtype=torch.float32, device=dev)
+    res["permute_with_probs (case17)"] = _rate(_median_ms(
+        lambda: ops.permute(xr, tm, probs, num_out=R, layout=ops.TOKEN_MAJOR, zero_tail=False, out=xp,
+                            permuted_probs=pp), flush), 2 * T * H + 8 * T * E + 4 * T * E + 2 * R * H + 4 * R, "GB/s")
+    res["unpermute (case15)"] = _rate(_median_ms(lambda: ops.unpermute(xp, em, layout=ops.EXPERT_MAJOR), flush),
+                                      2 * R * H + 8 * T * E + 2 * T * H, "GB/s")
+    lines.append({"config": "reference_shapes", "tokens": T, "hidden": H, "experts": E, "routed_rows": R,
+                  "kernels": res})
+    return lines
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -248,6 +352,9 @@ def main():
                     help="skip the backward grouped GEMMs (reported beside the forward, not in value)")
     ap.add_argument("--no-router", action="store_true",
                     help="skip the router front end / router backward timings (reported beside the forward)")
+    ap.add_argument("--configs", action="store_true",
+                    help="instead of the step benchmark, print one JSON line per baseline config (C1-C5) and the "
+                         "reference shapes with per-kernel medians (50 calls, 1 GiB flushed before each)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the MoE dispatch path here has no multi-GPU (expert-parallel) "
@@ -256,6 +363,10 @@ def main():
 
     pkg = importlib.import_module("1188b-reference-kernels_amd")
     dev = torch.device("cuda:0")
+    if args.configs:
+        for line in config_lines(pkg, dev):
+            print(json.dumps(line), flush=True)
+        return
     T, H, F, E, k = CFG["tokens"], CFG["hidden"], CFG["ffn"], CFG["experts"], CFG["topk"]
     inp = pkg.inputs
     x = inp.randn_bf16((T, H), seed=SEED, device=dev)
