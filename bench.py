@@ -261,7 +261,6 @@ def config_lines(pkg, dev):
     timed calls after 25 warm-up calls, 1 GiB flushed before each call (one JSON line per config)."""
     ops, inp = pkg.ops, pkg.inputs
     flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-    lines = []
     for name, cfg in inp.CONFIGS.items():
         T, H, E, k = cfg["tokens"], cfg["hidden"], cfg["experts"], cfg["topk"]
         seed = inp.SEED_CONFIG_BASE + int(name[1:])
@@ -294,7 +293,7 @@ def config_lines(pkg, dev):
                                        2 * R * H + 4 * R + 8 * T * E + 2 * T * H + 4 * T * E, "GB/s")
             del g
         del xp, pp
-        lines.append({"config": name, "tokens": T, "hidden": H, "experts": E, "topk": k, "routed_rows": R,
+        yield ({"config": name, "tokens": T, "hidden": H, "experts": E, "topk": k, "routed_rows": R,
                       "kernels": res})
     for name, cfg in inp.GEMM_CONFIGS.items():
         seed = inp.SEED_CONFIG_BASE + int(name[1:])
@@ -313,7 +312,7 @@ def config_lines(pkg, dev):
             res[("fc1_swiglu" if cfg["swiglu"] else "fc2") + "_" + vname] = dict(_rate(ms, 2 * M * K * N, "TFLOP/s"),
                                                                                 group_rows=sizes)
             del a, w, out
-        lines.append({"config": name, "groups": G, "K": K, "N": N, "kernels": res})
+        yield ({"config": name, "groups": G, "K": K, "N": N, "kernels": res})
     # Reference-case shapes (T=16384, E=320, H=8192): case12's mask, case17 permute, case15 unpermute.
     rm, sel = inp.reference_routing_mask()
     mask = rm.to(dev)
@@ -331,9 +330,99 @@ def config_lines(pkg, dev):
                             permuted_probs=pp), flush), 2 * T * H + 8 * T * E + 4 * T * E + 2 * R * H + 4 * R, "GB/s")
     res["unpermute (case15)"] = _rate(_median_ms(lambda: ops.unpermute(xp, em, layout=ops.EXPERT_MAJOR), flush),
                                       2 * R * H + 8 * T * E + 2 * T * H, "GB/s")
-    lines.append({"config": "reference_shapes", "tokens": T, "hidden": H, "experts": E, "routed_rows": R,
+    yield ({"config": "reference_shapes", "tokens": T, "hidden": H, "experts": E, "routed_rows": R,
                   "kernels": res})
-    return lines
+    del xr, probs, xp, pp, maps, mask
+    yield (reference_case_line(pkg, dev, flush))
+
+
+# The reference's published times for the dispatch cases, all on MTT S5000 (Moore Threads):
+# "optimized" = its own kernel (kernel_results/README.md:14-17), "trace" = the production kernel's
+# median/range in a profiler trace (the kernel_cases file cited).  None is on MI355X.
+PUBLISHED_MTT_S5000_MS = {
+    "case06": (2.0448, "optimized, kernel_results/README.md:14"),
+    "case12": (0.4580, "optimized, kernel_results/README.md:15"),
+    "case15": (1.3131, "optimized, kernel_results/README.md:16"),
+    "case17": (2.5681, "optimized, kernel_results/README.md:17"),
+    "case21": (3.313, "trace median, kernel_cases/case21_ref_permute_with_mask_map_trans.py:34-37"),
+    "case22": (1.565, "trace 1.565-1.632, kernel_cases/case22_ref_moe_permute_mask_kernel_true.py:28-33"),
+    "case23": (1.565, "trace median, kernel_cases/case23_ref_aten_topk.py:31-34"),
+    "case24": (1.158, "trace 1.158-1.237, kernel_cases/case24_ref_moe_unpermute_mask_kernel_false.py:28-31"),
+    "case30": (1.509, "trace 1.509-1.558, kernel_cases/case30_ref_moe_permute_mask_kernel.py:24-30"),
+    "case32": (1.200, "trace 1.200-1.251, kernel_cases/case32_ref_moe_unpermute_mask_kernel.py:29-32"),
+}
+
+
+def reference_case_line(pkg, dev, flush):
+    """Each dispatch case's drop-in `kernel_function` at the case's own default shape and inputs (the
+    host-side checks and the max(row_id_map) read-back included where the reference does them), with
+    algorithmic bytes and the reference's published MTT S5000 time beside it."""
+    cases, inp = pkg.cases, pkg.inputs
+    res = {}
+
+    def add(name, fn, nbytes):
+        r = _rate(_median_ms(fn, flush), nbytes, "GB/s")
+        if name in PUBLISHED_MTT_S5000_MS:
+            pub, src = PUBLISHED_MTT_S5000_MS[name]
+            r.update(published_mtt_s5000_ms=pub, published_source=src, speedup_vs_published=round(pub / r["ms"], 2))
+        res[name] = r
+
+    c = cases.case06_cp_seq_chunk_index_select
+    k_ag, v_ag, index = c.get_inputs(dev)
+    add("case06", lambda: c.kernel_function(k_ag, v_ag, index), 2 * (k_ag.numel() + v_ag.numel()) * 2)
+    del k_ag, v_ag, index
+
+    c = cases.case12_moe_row_id_map_pass2
+    (rmap,) = c.get_inputs(dev)
+    T, E = rmap.shape
+    add("case12", lambda: c.kernel_function(rmap), T * E + 16 * T * E)
+    del rmap
+
+    c = cases.case15_moe_unpermute_mask_fwd
+    pin, em = c.get_inputs(dev)
+    R, H = pin.shape
+    E, T = em.shape
+    add("case15", lambda: c.kernel_function(pin, em), 2 * R * H + 8 * T * E + 2 * T * H)
+    del pin, em
+
+    c = cases.case17_moe_permute_with_mask_map
+    x, tm, probs = c.get_inputs(dev)
+    T, H = x.shape
+    E = probs.shape[1]
+    R = c.get_init_inputs()[1]
+    add("case17", lambda: c.kernel_function(x, tm, probs, num_out=R),
+        2 * T * H + 8 * T * E + 4 * T * E + 2 * R * H + 4 * R)
+    del x, tm, probs
+
+    c = cases.case23_aten_topk
+    logits = c.make_inputs(device=dev)
+    T, E = logits.shape
+    add("case23", lambda: c.kernel_function(logits, 8), 4 * T * E + 12 * T * 8)
+    del logits
+
+    # The deep_ep / TE scatter-gather cases share one (t + k) mod E routing of T=16384 tokens, top-8.
+    c21, c22, c24, c30, c32 = (cases.case21_permute_with_mask_map_trans, cases.case22_moe_permute_mask_kernel_true,
+                               cases.case24_moe_unpermute_mask_kernel_false, cases.case30_moe_permute_mask_kernel,
+                               cases.case32_moe_unpermute_mask_kernel)
+    T, H = c21.M, c21.HIDDEN
+    em64 = c21.make_row_id_map(device=dev)
+    em32 = c24.make_row_id_map(device=dev)
+    E = em64.shape[0]
+    R = T * c21.TOPK
+    x = inp.randn_bf16((T, H), seed=21, device=dev)
+    add("case21", lambda: c21.kernel_function(x, em64), 8 * E * T + 2 * T * H + 2 * R * H)
+    add("case30", lambda: c30.kernel_function(x, em64), 8 * E * T + 2 * T * H + 2 * R * H)
+    probs = c22.make_probs(em64, device=dev)
+    add("case22", lambda: c22.kernel_function(x, em64, probs), 8 * E * T + 2 * T * H + 4 * T * E + 2 * R * H + 4 * R)
+    del x, probs
+    g = inp.randn_bf16((R, H), seed=24, device=dev)
+    add("case24", lambda: c24.kernel_function(g, em32), 2 * R * H + 4 * E * T + 4 * T * H + 2 * T * H)
+    pg = torch.randn(R, device=dev)
+    add("case32", lambda: c32.kernel_function(g, em32, pg),
+        2 * R * H + 4 * E * T + 4 * R + 4 * T * H + 2 * T * H + 4 * T * E)
+    del g, pg, em64, em32
+    return {"config": "reference_cases", "note": "each case's kernel_function at its own default shape",
+            "kernels": res}
 
 
 def main():
