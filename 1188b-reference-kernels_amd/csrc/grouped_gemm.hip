@@ -389,6 +389,383 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
     }
   }
 }
+
+// Pipelined form of the kernel above for K > 128 and 16-byte output rows: the
+// same K step (4 waves of 128 x 128, fragments of a whole step in VGPRs, DMA
+// into a two-slot LDS ring), but consecutive tiles of a workgroup follow each
+// other without draining the pipeline:
+//   * the last K step of a tile DMAs the next tile's stage 0 and the step
+//     after it (whose MFMAs finish the tile) reads that stage's fragments and
+//     DMAs stage 1, exactly like an inner step -- the LDS ring never idles;
+//   * the epilogue works on registers only (bf16 RNE in hardware, then
+//     v_permlane32_swap so a lane holds 8 consecutive columns, one 16-byte
+//     buffer store; rows past the group end lie past the store resource and
+//     are dropped), issued after the next tile's stage DMAs so the next waits
+//     leave the stores in flight (vector-memory operations complete in issue
+//     order);
+//   * the first MFMAs of a tile take a zero accumulator operand (no clearing);
+//   * the tile after next is found during the epilogue from group offsets
+//     staged in LDS, and (gather) its source rows are loaded during the next
+//     tile's first step, long before its DMA offsets are formed.
+template <bool kSwiglu, bool kGather>
+__global__ __launch_bounds__(256) void grouped_gemm_pipe_kernel(GemmArgs p) {
+  constexpr int kWaves = 4;
+  constexpr int kThreads = 256;
+  constexpr int kMI = 4, kNI = 4;
+  constexpr int kDma = kOperandBytes / 1024 / kWaves;  // 8 DMA instructions per operand per stage
+  constexpr int kEpiCols = kSwiglu ? kBN / 2 : kBN;    // output columns of a tile
+  constexpr int kOutNI = kSwiglu ? kNI / 2 : kNI;      // output blocks of 32 columns per wave
+  constexpr int kStores = kMI * kOutNI * 2;            // 16-byte stores per lane per tile
+  constexpr int kMaxG = 4096;
+  static_assert(kStores <= 63, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) char smem[kStages * kStageBytes];
+  __shared__ int32_t s_offs[kMaxG + 1];
+  lds_char *const sbase = (lds_char *)smem;
+  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sbase));
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+  const int64_t P = gridDim.x;
+  const int64_t b = blockIdx.x;
+  const int64_t K = p.K;
+  const int ktiles = static_cast<int>(ceil_div(K, kBK));  // >= 3 (host)
+  const bool ktail = (K % kBK) != 0;
+
+  for (int64_t i = tid; i <= p.G; i += kThreads) s_offs[i] = p.offsets[i];
+  __syncthreads();
+
+  // ---- tile walker (group offsets from LDS)
+  auto group_rows = [&](int64_t g, int64_t &lo, int64_t &hi) {
+    lo = min(max(static_cast<int64_t>(s_offs[g]), int64_t(0)), p.M);
+    hi = min(max(static_cast<int64_t>(s_offs[g + 1]), lo), p.M);
+  };
+  int64_t g_cur = 0, tiles_before = 0, m_lo, m_hi;
+  group_rows(0, m_lo, m_hi);
+  int64_t mt_g = ceil_div(m_hi - m_lo, kBM);
+  struct Tile {
+    int64_t g, row0;
+    uint32_t nt;
+    int rows_valid;
+  };
+  auto find_tile = [&](int64_t round, Tile &t) -> bool {
+    const int64_t L = round * P + (b % 8) * (P / 8) + b / 8;
+    while (g_cur < p.G && L >= tiles_before + mt_g * p.ntiles) {
+      tiles_before += mt_g * p.ntiles;
+      ++g_cur;
+      if (g_cur < p.G) {
+        group_rows(g_cur, m_lo, m_hi);
+        mt_g = ceil_div(m_hi - m_lo, kBM);
+      }
+    }
+    if (g_cur >= p.G) return false;
+    const uint32_t q = static_cast<uint32_t>(L - tiles_before);
+    const uint32_t ntl = static_cast<uint32_t>(p.ntiles);
+    const uint32_t per_grp = kGroupM * ntl;
+    const uint32_t full = static_cast<uint32_t>(mt_g) / kGroupM;
+    uint32_t mt, nt;
+    if (q < full * per_grp) {
+      const uint32_t grp = q / per_grp, r = q - grp * per_grp;
+      nt = r / kGroupM;
+      mt = grp * kGroupM + r % kGroupM;
+    } else {
+      const uint32_t r = q - full * per_grp, gm = static_cast<uint32_t>(mt_g) - full * kGroupM;
+      nt = r / gm;
+      mt = full * kGroupM + (r - nt * gm);
+    }
+    t.g = g_cur;
+    t.row0 = m_lo + static_cast<int64_t>(mt) * kBM;
+    t.nt = nt;
+    t.rows_valid = static_cast<int>(min(m_hi - t.row0, int64_t(kBM)));
+    return true;
+  };
+
+  // ---- DMA sources of the tile being loaded
+  const int dma_row = lane / kChunks;
+  const int dma_pchunk = lane % kChunks;
+  // Gather: source row (in x) of each of this lane's DMA rows of a tile.
+  // Without a valid tile the loads still issue (a fixed count of vector-memory
+  // operations) over an empty resource and return zeros.
+  int32_t src_rows[kDma];
+  auto load_rows = [&](const Tile &t, bool valid) {
+    if constexpr (kGather) {
+      const __amdgpu_buffer_rsrc_t r_rows = make_rsrc(p.a_rows, valid ? static_cast<uint32_t>(p.M * 4) : 0u);
+#pragma unroll
+      for (int j = 0; j < kDma; ++j) {
+        const int r = (j * kWaves + wave) * kRowsPerKiB + dma_row;
+        const uint32_t off = static_cast<uint32_t>(t.row0 + min(r, t.rows_valid - 1)) * 4u;
+#if defined(__HIP_DEVICE_COMPILE__)
+        src_rows[j] = __builtin_amdgcn_raw_buffer_load_b32(r_rows, static_cast<int>(off), 0, 0);
+#else
+        (void)off;
+        (void)r_rows;
+        src_rows[j] = 0;
+#endif
+      }
+    } else {
+      (void)t;
+      (void)valid;
+    }
+  };
+  __amdgpu_buffer_rsrc_t ra, rb;
+  int a_off[kDma], b_off[kDma];
+  auto setup_dma = [&](const Tile &t) {
+    const uint32_t row_bytes = static_cast<uint32_t>(K) * 2u;
+    ra = kGather ? make_rsrc(p.a, static_cast<uint32_t>(p.a_src_rows * K * 2))
+                 : make_rsrc(p.a + t.row0 * K, static_cast<uint32_t>(t.rows_valid) * row_bytes);
+    rb = make_rsrc(p.w + t.g * p.N * K, static_cast<uint32_t>(p.N * K * 2));
+#pragma unroll
+    for (int j = 0; j < kDma; ++j) {
+      const int r = (j * kWaves + wave) * kRowsPerKiB + dma_row;
+      const int lchunk = dma_pchunk ^ swz(r);
+      if constexpr (kGather) {
+        // An index outside x points past the resource (zeros).
+        const int32_t src = src_rows[j];
+        a_off[j] = (src >= 0 && src < p.a_src_rows) ? static_cast<int>(static_cast<uint32_t>(src) * row_bytes + lchunk * 16)
+                                                   : static_cast<int>(kNoAccess);
+      } else {
+        a_off[j] = static_cast<int>(static_cast<uint32_t>(min(r, t.rows_valid - 1)) * row_bytes + lchunk * 16);
+      }
+      b_off[j] = static_cast<int>(static_cast<uint32_t>(b_row_clamped<kSwiglu>(t.nt, r, p.ncols, p.N)) * row_bytes +
+                                  lchunk * 16);
+    }
+  };
+  // Operand `op` (0 = A, 1 = B) of K step `kt` of the tile set up last into ring slot `slot`.
+  auto issue_half = [&](int kt, int slot, int op) {
+    const uint32_t st = lds_base + (slot % kStages) * kStageBytes + op * kOperandBytes;
+    const int soff = kt * kBK * 2;
+#pragma unroll
+    for (int j = 0; j < kDma; ++j) {
+      const uint32_t blk = j * kWaves + wave;
+      dma16b(op ? rb : ra, (lds_void *)(uintptr_t)(st + blk * 1024), op ? b_off[j] : a_off[j], soff);
+    }
+  };
+  auto zero_ktail = [&](int slot) {
+    lds_char *st = sbase + (slot % kStages) * kStageBytes;
+    const int kvalid = static_cast<int>(K - static_cast<int64_t>(ktiles - 1) * kBK);
+    for (int idx = tid; idx < 2 * kBM * kChunks; idx += kThreads) {
+      const int op = idx / (kBM * kChunks), rem = idx % (kBM * kChunks);
+      const int r = rem / kChunks, c = rem % kChunks;
+      if (c * 8 >= kvalid) {
+        *reinterpret_cast<lds_u32x4 *>(st + op * kOperandBytes + r * kRowBytes + ((c ^ swz(r)) * 16)) =
+            u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  };
+
+  // ---- fragments
+  int fa_base[kMI], fb_base[kNI];
+#pragma unroll
+  for (int i = 0; i < kMI; ++i) {
+    const int r = wm * 128 + i * 32 + (lane & 31);
+    fa_base[i] = r * kRowBytes | (swz(r) << 4);
+  }
+#pragma unroll
+  for (int j = 0; j < kNI; ++j) {
+    int r;
+    if constexpr (kSwiglu) {
+      const int jj = j % (kNI / 2);
+      r = (j < kNI / 2 ? 0 : 128) + wn * 64 + jj * 32 + (lane & 31);
+    } else {
+      r = wn * 128 + j * 32 + (lane & 31);
+    }
+    fb_base[j] = r * kRowBytes | (swz(r) << 4);
+  }
+  const int khalf = lane >> 5;
+  f32x16 acc[kMI][kNI];
+  uint32_t rd_a[kMI], rd_b[kNI];
+  auto set_read_slot = [&](int slot) {
+    const uint32_t so = lds_base + (slot % kStages) * kStageBytes;
+#pragma unroll
+    for (int i = 0; i < kMI; ++i) rd_a[i] = so + (fa_base[i] ^ (khalf << 4));
+#pragma unroll
+    for (int j = 0; j < kNI; ++j) rd_b[j] = so + kOperandBytes + (fb_base[j] ^ (khalf << 4));
+  };
+  bf16x8 fa[kSubSteps][kMI], fb[kSubSteps][kNI];
+  auto read_frags = [&](int ks) {
+#pragma unroll
+    for (int i = 0; i < kMI; ++i)
+      fa[ks][i] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)(rd_a[i] ^ (ks << 5)));
+#pragma unroll
+    for (int j = 0; j < kNI; ++j)
+      fb[ks][j] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)(rd_b[j] ^ (ks << 5)));
+  };
+  auto mfma_ks = [&](int ks) {
+#pragma unroll
+    for (int i = 0; i < kMI; ++i)
+#pragma unroll
+      for (int j = 0; j < kNI; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks][j], fa[ks][i], acc[i][j], 0, 0, 0);
+  };
+  auto mfma_first = [&]() {
+#pragma unroll
+    for (int i = 0; i < kMI; ++i)
+#pragma unroll
+      for (int j = 0; j < kNI; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[0][j], fa[0][i], f32x16{}, 0, 0, 0);
+  };
+
+  // Epilogue of tile t from the accumulators. With w as the MFMA's first
+  // operand, register r of lane l in block (i, j) holds output row i * 32 +
+  // l % 32 and column j * 32 + (r / 4) * 8 + (l / 32) * 4 + r % 4 of this
+  // wave's part. After rounding, each 4-register group is two packed words;
+  // v_permlane32_swap trades the upper half-wave's words of group g with the
+  // lower half-wave's of group g + 1, so a lower lane holds columns 8 g ..
+  // 8 g + 7 of its row and its upper partner 8 g + 8 .. 8 g + 15.
+  auto epilogue = [&](const Tile &t) {
+    const uint32_t ld = static_cast<uint32_t>(p.ncols) * 2u;
+    const __amdgpu_buffer_rsrc_t ro =
+        make_rsrc(p.out + t.row0 * p.ncols, static_cast<uint32_t>(t.rows_valid) * ld);
+    const int64_t wcol0 = static_cast<int64_t>(t.nt) * kEpiCols + wn * (kEpiCols / 2);
+    const int half = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < kMI; ++i) {
+      const uint32_t orow = static_cast<uint32_t>(wm * 128 + i * 32 + (lane & 31));
+#pragma unroll
+      for (int jo = 0; jo < kOutNI; ++jo) {
+        uint32_t w[4][2];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float h[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if constexpr (kSwiglu) {
+              const float gt = acc[i][jo][4 * g + q];
+              h[q] = gt * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gt * -1.4426950408889634f)) *
+                     acc[i][jo + kNI / 2][4 * g + q];
+            } else {
+              h[q] = acc[i][jo][4 * g + q];
+            }
+          }
+          const bf16x2 lo = {(__bf16)h[0], (__bf16)h[1]};
+          const bf16x2 hi = {(__bf16)h[2], (__bf16)h[3]};
+          w[g][0] = __builtin_bit_cast(uint32_t, lo);
+          w[g][1] = __builtin_bit_cast(uint32_t, hi);
+        }
+#pragma unroll
+        for (int gp = 0; gp < 4; gp += 2) {
+          u32x4 o;
+#if defined(__HIP_DEVICE_COMPILE__)
+          const auto s0 = __builtin_amdgcn_permlane32_swap(w[gp][0], w[gp + 1][0], false, false);
+          const auto s1 = __builtin_amdgcn_permlane32_swap(w[gp][1], w[gp + 1][1], false, false);
+          o = u32x4{s0[0], s1[0], s0[1], s1[1]};
+#else
+          o = u32x4{0u, 0u, 0u, 0u};
+#endif
+          const int64_t gcol = wcol0 + jo * 32 + (gp + half) * 8;
+          // Columns past the output get an offset past the resource: the store is dropped.
+          const uint32_t off = gcol < p.ncols ? orow * ld + static_cast<uint32_t>(gcol) * 2u : kNoAccess;
+#if defined(__HIP_DEVICE_COMPILE__)
+          __builtin_amdgcn_raw_buffer_store_b128(o, ro, static_cast<int>(off), 0, 0);
+#else
+          (void)off;
+          (void)ro;
+          (void)o;
+#endif
+        }
+      }
+    }
+  };
+
+  // ---- first tile: stages 0 and 1 in flight, stage 0 read into VGPRs
+  Tile cur, nxt;
+  if (!find_tile(0, cur)) return;
+  load_rows(cur, true);
+  setup_dma(cur);
+  issue_half(0, 0, 0);
+  issue_half(0, 0, 1);
+  issue_half(1, 1, 0);
+  issue_half(1, 1, 1);
+  bool more = find_tile(1, nxt);
+  wait_vm_n<2 * kDma>();
+  barrier();
+  set_read_slot(0);
+#pragma unroll
+  for (int ks = 0; ks < kSubSteps; ++ks) read_frags(ks);
+
+  int sb = 0;  // ring slot of the current tile's stage 0
+  for (int64_t round = 0;; ++round) {
+    // One K step: MFMAs of stage kt (fragments in VGPRs), fragments of stage
+    // kt + 1 read from LDS, DMA of the stage two ahead (this tile's kt + 2 or,
+    // past its end, the next tile's kt + 2 - ktiles) into the slot of stage kt.
+    auto step = [&](int kt, bool first, bool last) {
+      if (first) {
+        mfma_first();
+      } else {
+        mfma_ks(0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // Stage kt + 1 has landed. In a tile's first step the previous tile's
+      // output stores were issued after it and may still be in flight.
+      if (first && round > 0) {
+        wait_vm_n<kStores>();
+      } else {
+        wait_dma();
+      }
+      wait_lds();
+      barrier();
+      if (first) load_rows(nxt, more);  // read in this tile's last step
+      if (ktail && kt + 1 == ktiles - 1) {
+        zero_ktail(sb + kt + 1);
+        wait_lds();
+        barrier();
+      }
+      // The last step DMAs the next tile's stage 0 (without a next tile it
+      // re-reads this tile's last stage into the free slot: no branch below).
+      if (last && more) setup_dma(nxt);
+      const int kdma = !last ? kt + 2 : (more ? 0 : ktiles - 1);
+      set_read_slot(sb + kt + 1);
+      read_frags(0);
+      mfma_ks(1);
+      issue_half(kdma, sb + kt + 2, 0);
+      sched_pattern<0x100, 0x020>();
+      mfma_ks(2);
+      read_frags(1);
+      issue_half(kdma, sb + kt + 2, 1);
+      sched_pattern<0x100, 0x020>();
+      mfma_ks(3);
+      read_frags(2);
+      sched_pattern<0x100, 0>();
+      read_frags(3);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    step(0, true, false);
+    for (int kt = 1; kt + 2 < ktiles; ++kt) step(kt, false, false);
+    step(ktiles - 2, false, true);
+
+    // Last step of the tile: it reads the next tile's stage 0 (DMA'd in the
+    // step above) and DMAs its stage 1 (without a next tile: reads and DMA of
+    // data nobody uses, so the code has no branch).
+    mfma_ks(0);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_dma();
+    wait_lds();
+    barrier();
+    set_read_slot(sb + ktiles);
+    read_frags(0);
+    mfma_ks(1);
+    issue_half(more ? 1 : ktiles - 1, sb + ktiles + 1, 0);
+    sched_pattern<0x100, 0x020>();
+    mfma_ks(2);
+    read_frags(1);
+    issue_half(more ? 1 : ktiles - 1, sb + ktiles + 1, 1);
+    sched_pattern<0x100, 0x020>();
+    mfma_ks(3);
+    read_frags(2);
+    sched_pattern<0x100, 0>();
+    read_frags(3);
+    __builtin_amdgcn_sched_barrier(0);
+    epilogue(cur);
+    __builtin_amdgcn_sched_barrier(0);
+    if (!more) break;
+    cur = nxt;
+    sb += ktiles;
+    more = find_tile(round + 2, nxt);
+  }
+  wait_dma();  // no LDS DMA outlives the workgroup
+}
 }  // namespace
 }  // namespace moe
 
@@ -443,7 +820,18 @@ int launch_grouped_gemm(const char *fn, const moe_bf16_t *a, int64_t a_src_rows,
   int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
   grid = std::max<int64_t>(8, (grid + 7) / 8 * 8);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (swiglu) {
+  // The pipelined kernel needs three K steps per tile, 16-byte output rows, a
+  // 256-row output panel below 2 GiB and (gather) 32-bit offsets into a_rows.
+  const bool pipe = K > 2 * kBK && p.vec_out && ncols < (int64_t(1) << 22) && (!gather || M_total < (int64_t(1) << 29));
+  if (pipe) {
+    if (swiglu) {
+      if (gather) grouped_gemm_pipe_kernel<true, true><<<dim3(grid), dim3(256), 0, s>>>(p);
+      else grouped_gemm_pipe_kernel<true, false><<<dim3(grid), dim3(256), 0, s>>>(p);
+    } else {
+      if (gather) grouped_gemm_pipe_kernel<false, true><<<dim3(grid), dim3(256), 0, s>>>(p);
+      else grouped_gemm_pipe_kernel<false, false><<<dim3(grid), dim3(256), 0, s>>>(p);
+    }
+  } else if (swiglu) {
     if (gather) grouped_gemm_kernel<true, true><<<dim3(grid), dim3(256), 0, s>>>(p);
     else grouped_gemm_kernel<true, false><<<dim3(grid), dim3(256), 0, s>>>(p);
   } else {

@@ -34,6 +34,18 @@ def _dtype(name: str, t: torch.Tensor, *dtypes: torch.dtype) -> None:
         raise TypeError(f"{name} must have dtype {' or '.join(map(str, dtypes))}, got {t.dtype}")
 
 
+def _out(out: Optional[torch.Tensor], shape: tuple, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
+    """A caller-provided output (checked: GPU, dtype, shape, contiguous) or a new one."""
+    if out is None:
+        return torch.empty(shape, dtype=dtype, device=device)
+    _on_gpu("out", out)
+    _dtype("out", out, dtype)
+    if tuple(out.shape) != tuple(shape) or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous {tuple(shape)} tensor, got {tuple(out.shape)}"
+                         f"{'' if out.is_contiguous() else ' (non-contiguous)'}")
+    return out
+
+
 def _map_dims(row_id_map: torch.Tensor, layout: str) -> tuple[int, int]:
     """(tokens, experts) of a 2-D map in the given layout."""
     if row_id_map.ndim != 2:
@@ -85,8 +97,7 @@ def router_logits(inp: torch.Tensor, weight: torch.Tensor, *, out: Optional[torc
     M, K = inp.shape
     N = weight.shape[0]
     ic, wc = inp.contiguous(), weight.contiguous()
-    if out is None:
-        out = torch.empty(M, N, dtype=torch.float32, device=inp.device)
+    out = _out(out, (M, N), torch.float32, inp.device)
     call("moe_router_logits", ptr(ic), M, K, ptr(wc), N, ptr(out), None, 0, stream_handle())
     return out
 
@@ -246,8 +257,7 @@ def permute(x: torch.Tensor, row_id_map: torch.Tensor, probs: Optional[torch.Ten
         if tuple(probs.shape) != (T, E):
             raise ValueError(f"probs {tuple(probs.shape)} expected {(T, E)}")
         pc = probs.contiguous().to(torch.float32)
-    if out is None:
-        out = torch.empty(num_out, H, dtype=x.dtype, device=x.device)
+    out = _out(out, (num_out, H), x.dtype, x.device)
     if pc is not None and permuted_probs is None:
         permuted_probs = torch.empty(num_out, dtype=torch.float32, device=x.device)
     ws = None
@@ -283,8 +293,7 @@ def unpermute(pin: torch.Tensor, row_id_map: torch.Tensor, merge_probs: Optional
         if tuple(merge_probs.shape) != (T, E):
             raise ValueError(f"merge_probs {tuple(merge_probs.shape)} expected {(T, E)}")
         wc = merge_probs.contiguous().to(torch.float32)
-    if out is None:
-        out = torch.empty(T, H, dtype=pin.dtype, device=pin.device)
+    out = _out(out, (T, H), pin.dtype, pin.device)
     acc = torch.empty(T, H, dtype=torch.float32, device=pin.device) if with_acc else None
     call("moe_unpermute", ptr(pc), R, H, ptr(mc), _IDX[mc.dtype], _LAYOUTS[layout], E, T, ptr(wc), ptr(out),
          ptr(acc), stream_handle())
@@ -371,8 +380,7 @@ def grouped_gemm(a: torch.Tensor, w: torch.Tensor, group_offsets: torch.Tensor, 
     M = a.shape[0]
     ac, wc, oc = a.contiguous(), w.contiguous(), group_offsets.contiguous()
     ncols = N // 2 if swiglu else N
-    if out is None:
-        out = torch.empty(M, ncols, dtype=torch.bfloat16, device=a.device)
+    out = _out(out, (M, ncols), torch.bfloat16, a.device)
     call("moe_grouped_gemm", ptr(ac), M, K, ptr(wc), G, N, ptr(oc),
          MOE_EPILOGUE_SWIGLU if swiglu else MOE_EPILOGUE_NONE, ptr(out), None, 0, stream_handle())
     return out
@@ -422,8 +430,7 @@ def grouped_gemm_gather(x: torch.Tensor, a_rows: torch.Tensor, w: torch.Tensor, 
     M = a_rows.shape[0]
     xc, rc, wc, oc = x.contiguous(), a_rows.contiguous(), w.contiguous(), group_offsets.contiguous()
     ncols = N // 2 if swiglu else N
-    if out is None:
-        out = torch.empty(M, ncols, dtype=torch.bfloat16, device=x.device)
+    out = _out(out, (M, ncols), torch.bfloat16, x.device)
     call("moe_grouped_gemm_gather", ptr(xc), x.shape[0], ptr(rc), M, K, ptr(wc), G, N, ptr(oc),
          MOE_EPILOGUE_SWIGLU if swiglu else MOE_EPILOGUE_NONE, ptr(out), None, 0, stream_handle())
     return out
@@ -448,8 +455,7 @@ def grouped_gemm_dgrad(dy: torch.Tensor, w: torch.Tensor, group_offsets: torch.T
         raise ValueError(f"group_offsets {tuple(group_offsets.shape)} expected ({G + 1},)")
     M = dy.shape[0]
     dyc, wc, oc = dy.contiguous(), w.contiguous(), group_offsets.contiguous()
-    if out is None:
-        out = torch.empty(M, K, dtype=torch.bfloat16, device=dy.device)
+    out = _out(out, (M, K), torch.bfloat16, dy.device)
     call("moe_grouped_gemm_dgrad", ptr(dyc), M, N, ptr(wc), G, K, ptr(oc), ptr(out), None, 0, stream_handle())
     return out
 
@@ -472,7 +478,6 @@ def grouped_gemm_wgrad(dy: torch.Tensor, x: torch.Tensor, group_offsets: torch.T
     M, N = dy.shape
     K = x.shape[1]
     dyc, xc, oc = dy.contiguous(), x.contiguous(), group_offsets.contiguous()
-    if out is None:
-        out = torch.empty(G, N, K, dtype=torch.bfloat16, device=dy.device)
+    out = _out(out, (G, N, K), torch.bfloat16, dy.device)
     call("moe_grouped_gemm_wgrad", ptr(dyc), ptr(xc), M, N, K, G, ptr(oc), ptr(out), None, 0, stream_handle())
     return out

@@ -109,3 +109,40 @@ def test_grouped_gemm_errors(pkg, dev):
         pkg.ops.grouped_gemm(x, w, offs)
     with pytest.raises(ValueError):
         pkg.ops.grouped_gemm(x, w[:, :, :8], offs)
+
+
+@pytest.mark.parametrize("sizes,K,N,swiglu,gather", [
+    ([300, 0, 17, 513], 200, 264, False, False),      # ragged, empty group, K and N tails
+    ([40] * 600, 200, 512, False, False),             # 600 groups: many tile changes per workgroup
+    ([2000, 3, 1500], 2048, 7168, False, False),      # fc2 class, several tiles per workgroup
+    ([64, 700, 0, 1500], 7168, 4096, True, False),    # fc1 class
+    ([40] * 300, 136, 272, True, True),               # K tail, three K steps, gather
+    ([900, 0, 2100], 7168, 4096, True, True),         # fc1 gather class
+])
+def test_pipelined_kernel_matches_drained_kernel(pkg, dev, sizes, K, N, swiglu, gather):
+    """K > 128 with 16-byte output rows runs the pipelined kernel (tiles back to back,
+    register epilogue); an output 2 bytes off 16-byte alignment runs the drained
+    kernel (LDS-staged epilogue). Same K order, same rounding: equal bit for bit."""
+    g = torch.Generator().manual_seed(sum(sizes) + K + N)
+    M = sum(sizes)
+    w = (torch.randn(len(sizes), N, K, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    offs = pkg.ops.group_offsets_from_splits(sizes, dev)
+    ncols = N // 2 if swiglu else N
+    buf = torch.full((M * ncols + 16,), float("nan"), dtype=torch.bfloat16, device=dev)
+    drained = buf[1:1 + M * ncols].view(M, ncols)
+    assert drained.data_ptr() % 16 != 0
+    if gather:
+        X = 777
+        x = torch.randn(X, K, generator=g).to(torch.bfloat16).to(dev)
+        rows = torch.randint(0, X, (M,), generator=g, dtype=torch.int32).to(dev)
+        piped = pkg.ops.grouped_gemm_gather(x, rows, w, offs, swiglu=swiglu)
+        pkg.ops.grouped_gemm_gather(x, rows, w, offs, swiglu=swiglu, out=drained)
+    else:
+        x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+        piped = pkg.ops.grouped_gemm(x, w, offs, swiglu=swiglu)
+        pkg.ops.grouped_gemm(x, w, offs, swiglu=swiglu, out=drained)
+    torch.cuda.synchronize()
+    assert torch.equal(piped.view(torch.int16), drained.view(torch.int16)), f"sizes={sizes[:4]} K={K} N={N}"
+    # and both against the fp32 golden on sampled rows of every group
+    a = x[rows.long()] if gather else x
+    _sampled_check(a, w, offs.cpu(), piped, swiglu, rows_per_group=8)
