@@ -8,7 +8,10 @@
 // SwiGLU (fused, no reference function): h = silu(y[:, :F]) * y[:, F:] on the
 // fp32 accumulators, F = N / 2, rounded once to bf16.
 //
-// Kernel shape (gfx950):
+// Two kernels: grouped_gemm_pipe_kernel (further down; K > 128 and 16-byte
+// output rows, i.e. every MoE shape) and grouped_gemm_kernel, the drained
+// form for the rest (K <= 128, unaligned outputs). Both are bit-identical on
+// the shapes both take. Shared shape (gfx950), as the drained kernel has it:
 //   * one persistent workgroup of 4 wavefronts (one per SIMD) per CU; output
 //     tile 256 x 256, K step 64; each wavefront owns 128 x 128 of the tile as
 //     4 x 4 blocks of v_mfma_f32_32x32x16_bf16 (256 accumulator registers);
@@ -390,32 +393,37 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
   }
 }
 
-// Pipelined form of the kernel above for K > 128 and 16-byte output rows: the
-// same K step (4 waves of 128 x 128, fragments of a whole step in VGPRs, DMA
-// into a two-slot LDS ring), but consecutive tiles of a workgroup follow each
-// other without draining the pipeline:
-//   * the last K step of a tile DMAs the next tile's stage 0 and the step
-//     after it (whose MFMAs finish the tile) reads that stage's fragments and
-//     DMAs stage 1, exactly like an inner step -- the LDS ring never idles;
-//   * the epilogue works on registers only (bf16 RNE in hardware, then
-//     v_permlane32_swap so a lane holds 8 consecutive columns, one 16-byte
-//     buffer store; rows past the group end lie past the store resource and
-//     are dropped), issued after the next tile's stage DMAs so the next waits
-//     leave the stores in flight (vector-memory operations complete in issue
-//     order);
-//   * the first MFMAs of a tile take a zero accumulator operand (no clearing);
-//   * the tile after next is found during the epilogue from group offsets
-//     staged in LDS, and (gather) its source rows are loaded during the next
-//     tile's first step, long before its DMA offsets are formed.
+// Pipelined kernel (K > 128, 16-byte output rows): the one the host runs for
+// the MoE shapes. Same tile and ring as the kernel above, two differences:
+//   * v_mfma_f32_16x16x32_bf16 blocks (8 x 8 of 16 x 16 per wave): half the
+//     accumulator traffic per FLOP of the 32 x 32 x 16 form; the board holds
+//     a higher shader clock under it (about 1.9 GHz against 1.6 GHz for the
+//     32 x 32 form of the same loop at c5), which is what bounds a dense bf16
+//     GEMM of this size;
+//   * consecutive tiles of a workgroup follow each other without draining the
+//     pipeline: the last K step of a tile DMAs the next tile's stage 0 and the
+//     step after it (whose MFMAs finish the tile) reads that stage's
+//     fragments and DMAs stage 1, like an inner step; the epilogue works on
+//     registers only (bf16 RNE in hardware, v_permlane16_swap so a lane holds
+//     8 consecutive columns, one 16-byte buffer store; rows past the group end
+//     lie past the store resource and are dropped), issued after the next
+//     tile's stage DMAs so the next waits leave the stores in flight
+//     (vector-memory operations complete in issue order); the first MFMAs of
+//     a tile take a zero accumulator operand; the tile after next is found
+//     during the epilogue from group offsets staged in LDS, and (gather) its
+//     source rows are loaded during the next tile's first step, long before
+//     its DMA offsets are formed.
+// One K step per wave: 4 units of 32 MFMAs (K half x row-block half); the
+// fragments of the next stage are read into the registers each unit frees
+// (4, 12, 4 and 12 ds_read_b128), the 16 DMA instructions of the stage two
+// ahead are spread over the first two units.
 template <bool kSwiglu, bool kGather>
 __global__ __launch_bounds__(256) void grouped_gemm_pipe_kernel(GemmArgs p) {
   constexpr int kWaves = 4;
   constexpr int kThreads = 256;
-  constexpr int kMI = 4, kNI = 4;
   constexpr int kDma = kOperandBytes / 1024 / kWaves;  // 8 DMA instructions per operand per stage
   constexpr int kEpiCols = kSwiglu ? kBN / 2 : kBN;    // output columns of a tile
-  constexpr int kOutNI = kSwiglu ? kNI / 2 : kNI;      // output blocks of 32 columns per wave
-  constexpr int kStores = kMI * kOutNI * 2;            // 16-byte stores per lane per tile
+  constexpr int kStores = kSwiglu ? 16 : 32;           // 16-byte stores per lane per tile
   constexpr int kMaxG = 4096;
   static_assert(kStores <= 63, "vmcnt range");
   __shared__ __attribute__((aligned(1024))) char smem[kStages * kStageBytes];
@@ -483,8 +491,6 @@ __global__ __launch_bounds__(256) void grouped_gemm_pipe_kernel(GemmArgs p) {
   };
 
   // ---- DMA sources of the tile being loaded
-  const int dma_row = lane / kChunks;
-  const int dma_pchunk = lane % kChunks;
   // Gather: source row (in x) of each of this lane's DMA rows of a tile.
   // Without a valid tile the loads still issue (a fixed count of vector-memory
   // operations) over an empty resource and return zeros.
@@ -492,10 +498,13 @@ __global__ __launch_bounds__(256) void grouped_gemm_pipe_kernel(GemmArgs p) {
   auto load_rows = [&](const Tile &t, bool valid) {
     if constexpr (kGather) {
       const __amdgpu_buffer_rsrc_t r_rows = make_rsrc(p.a_rows, valid ? static_cast<uint32_t>(p.M * 4) : 0u);
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const uint32_t row0 = static_cast<uint32_t>(t.row0);
 #pragma unroll
       for (int j = 0; j < kDma; ++j) {
-        const int r = (j * kWaves + wave) * kRowsPerKiB + dma_row;
-        const uint32_t off = static_cast<uint32_t>(t.row0 + min(r, t.rows_valid - 1)) * 4u;
+        const int r = (j * kWaves + wave) * kRowsPerKiB + ln / kChunks;
+        const uint32_t off = (row0 + static_cast<uint32_t>(min(r, t.rows_valid - 1))) * 4u;
 #if defined(__HIP_DEVICE_COMPILE__)
         src_rows[j] = __builtin_amdgcn_raw_buffer_load_b32(r_rows, static_cast<int>(off), 0, 0);
 #else
@@ -511,25 +520,41 @@ __global__ __launch_bounds__(256) void grouped_gemm_pipe_kernel(GemmArgs p) {
   };
   __amdgpu_buffer_rsrc_t ra, rb;
   int a_off[kDma], b_off[kDma];
+  // DMA offsets in 32-bit arithmetic (the host bounds every panel below 2 GiB).
+  const int ncols32 = static_cast<int>(p.ncols), n32 = static_cast<int>(p.N);
+  const int src_rows32 = static_cast<int>(min(p.a_src_rows, int64_t(0x7fffffff)));
   auto setup_dma = [&](const Tile &t) {
     const uint32_t row_bytes = static_cast<uint32_t>(K) * 2u;
     ra = kGather ? make_rsrc(p.a, static_cast<uint32_t>(p.a_src_rows * K * 2))
                  : make_rsrc(p.a + t.row0 * K, static_cast<uint32_t>(t.rows_valid) * row_bytes);
     rb = make_rsrc(p.w + t.g * p.N * K, static_cast<uint32_t>(p.N * K * 2));
+    const int nt = static_cast<int>(t.nt);
+    // Recomputed per call (not kept live across the tile loop): the lane's
+    // DMA row and chunk from an opaque copy of the lane index.
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int drow = ln / kChunks, dchunk = ln % kChunks;
 #pragma unroll
     for (int j = 0; j < kDma; ++j) {
-      const int r = (j * kWaves + wave) * kRowsPerKiB + dma_row;
-      const int lchunk = dma_pchunk ^ swz(r);
+      const int r = (j * kWaves + wave) * kRowsPerKiB + drow;
+      const uint32_t lbytes = static_cast<uint32_t>(dchunk ^ swz(r)) * 16u;
       if constexpr (kGather) {
         // An index outside x points past the resource (zeros).
         const int32_t src = src_rows[j];
-        a_off[j] = (src >= 0 && src < p.a_src_rows) ? static_cast<int>(static_cast<uint32_t>(src) * row_bytes + lchunk * 16)
-                                                   : static_cast<int>(kNoAccess);
+        a_off[j] = (src >= 0 && src < src_rows32) ? static_cast<int>(static_cast<uint32_t>(src) * row_bytes + lbytes)
+                                                 : static_cast<int>(kNoAccess);
       } else {
-        a_off[j] = static_cast<int>(static_cast<uint32_t>(min(r, t.rows_valid - 1)) * row_bytes + lchunk * 16);
+        a_off[j] = static_cast<int>(static_cast<uint32_t>(min(r, t.rows_valid - 1)) * row_bytes + lbytes);
       }
-      b_off[j] = static_cast<int>(static_cast<uint32_t>(b_row_clamped<kSwiglu>(t.nt, r, p.ncols, p.N)) * row_bytes +
-                                  lchunk * 16);
+      int brow;
+      if constexpr (kSwiglu) {
+        // rows 0..127: gate columns j0 .. j0+127; rows 128..255: up columns F + j0 ..
+        const int c = min(nt * (kBN / 2) + (r & 127), ncols32 - 1);
+        brow = r < 128 ? c : ncols32 + c;
+      } else {
+        brow = min(nt * kBN + r, n32 - 1);
+      }
+      b_off[j] = static_cast<int>(static_cast<uint32_t>(brow) * row_bytes + lbytes);
     }
   };
   // Operand `op` (0 = A, 1 = B) of K step `kt` of the tile set up last into ring slot `slot`.
@@ -555,117 +580,119 @@ __global__ __launch_bounds__(256) void grouped_gemm_pipe_kernel(GemmArgs p) {
     }
   };
 
-  // ---- fragments
-  int fa_base[kMI], fb_base[kNI];
-#pragma unroll
-  for (int i = 0; i < kMI; ++i) {
-    const int r = wm * 128 + i * 32 + (lane & 31);
-    fa_base[i] = r * kRowBytes | (swz(r) << 4);
-  }
-#pragma unroll
-  for (int j = 0; j < kNI; ++j) {
-    int r;
-    if constexpr (kSwiglu) {
-      const int jj = j % (kNI / 2);
-      r = (j < kNI / 2 ? 0 : 128) + wn * 64 + jj * 32 + (lane & 31);
-    } else {
-      r = wn * 128 + j * 32 + (lane & 31);
-    }
-    fb_base[j] = r * kRowBytes | (swz(r) << 4);
-  }
-  const int khalf = lane >> 5;
-  f32x16 acc[kMI][kNI];
-  uint32_t rd_a[kMI], rd_b[kNI];
-  auto set_read_slot = [&](int slot) {
-    const uint32_t so = lds_base + (slot % kStages) * kStageBytes;
-#pragma unroll
-    for (int i = 0; i < kMI; ++i) rd_a[i] = so + (fa_base[i] ^ (khalf << 4));
-#pragma unroll
-    for (int j = 0; j < kNI; ++j) rd_b[j] = so + kOperandBytes + (fb_base[j] ^ (khalf << 4));
+  // ---- fragments of v_mfma_f32_16x16x32_bf16: lane l reads row (block +
+  // l % 16), the 8 values k = 8 (l / 16) .. + 7 of K half ks (logical chunk
+  // 4 ks + l / 16, i.e. address ^ (ks << 6)).
+  constexpr int kMI16 = 8, kNI16 = 8;
+  const int fq = lane >> 4;
+  // Row blocks 16 apart share the swizzle ((row / 2) % 8 changes by 8), so a
+  // block's fragment address is the wave's first block's plus a constant
+  // (an immediate ds_read offset): one address register per operand.
+  const int ra0 = wm * 128 + (lane & 15);
+  const int rb0 = (kSwiglu ? wn * 64 : wn * 128) + (lane & 15);
+  const uint32_t fa0 = ra0 * kRowBytes + ((fq ^ swz(ra0)) << 4);
+  const uint32_t fb0 = kOperandBytes + rb0 * kRowBytes + ((fq ^ swz(rb0)) << 4);
+  auto b_blk_off = [](int j) {
+    return kSwiglu ? (j / (kNI16 / 2)) * 128 * kRowBytes + (j % (kNI16 / 2)) * 16 * kRowBytes : j * 16 * kRowBytes;
   };
-  bf16x8 fa[kSubSteps][kMI], fb[kSubSteps][kNI];
-  auto read_frags = [&](int ks) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  f32x4 acc[kMI16][kNI16];
+  uint32_t rd_so = 0;
+  auto set_read_slot = [&](int slot) { rd_so = lds_base + (slot % kStages) * kStageBytes; };
+  bf16x8 fa[2][kMI16], fb[2][kNI16];
+  // A fragments of row blocks 4 ih .. 4 ih + 3 / all B fragments of K half ks.
+  auto read_a = [&](int ks, int ih) {
+    const uint32_t base = (rd_so + fa0) ^ (ks << 6);
 #pragma unroll
-    for (int i = 0; i < kMI; ++i)
-      fa[ks][i] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)(rd_a[i] ^ (ks << 5)));
-#pragma unroll
-    for (int j = 0; j < kNI; ++j)
-      fb[ks][j] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)(rd_b[j] ^ (ks << 5)));
+    for (int i = 4 * ih; i < 4 * ih + 4; ++i)
+      fa[ks][i] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)(base + i * 16 * kRowBytes));
   };
-  auto mfma_ks = [&](int ks) {
+  auto read_b = [&](int ks) {
+    const uint32_t base = (rd_so + fb0) ^ (ks << 6);
 #pragma unroll
-    for (int i = 0; i < kMI; ++i)
-#pragma unroll
-      for (int j = 0; j < kNI; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks][j], fa[ks][i], acc[i][j], 0, 0, 0);
+    for (int j = 0; j < kNI16; ++j)
+      fb[ks][j] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)(base + b_blk_off(j)));
   };
-  auto mfma_first = [&]() {
+  auto read_all = [&]() {
+    read_a(0, 0);
+    read_a(0, 1);
+    read_b(0);
+    read_a(1, 0);
+    read_a(1, 1);
+    read_b(1);
+  };
+  // 32 MFMAs: K half ks, row blocks 4 ih .. 4 ih + 3, all column blocks.
+  auto mfma_unit = [&](int ks, int ih, bool zero) {
 #pragma unroll
-    for (int i = 0; i < kMI; ++i)
+    for (int i = 4 * ih; i < 4 * ih + 4; ++i)
 #pragma unroll
-      for (int j = 0; j < kNI; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[0][j], fa[0][i], f32x16{}, 0, 0, 0);
+      for (int j = 0; j < kNI16; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[ks][j], fa[ks][i], zero ? f32x4{} : acc[i][j], 0, 0, 0);
   };
 
   // Epilogue of tile t from the accumulators. With w as the MFMA's first
-  // operand, register r of lane l in block (i, j) holds output row i * 32 +
-  // l % 32 and column j * 32 + (r / 4) * 8 + (l / 32) * 4 + r % 4 of this
-  // wave's part. After rounding, each 4-register group is two packed words;
-  // v_permlane32_swap trades the upper half-wave's words of group g with the
-  // lower half-wave's of group g + 1, so a lower lane holds columns 8 g ..
-  // 8 g + 7 of its row and its upper partner 8 g + 8 .. 8 g + 15.
+  // operand, register r of lane l in block (i, j) holds output row i * 16 +
+  // l % 16 and column j * 16 + 4 (l / 16) + r of this wave's part. After
+  // rounding, a block is two packed words per lane; v_permlane16_swap trades
+  // rows (16 lanes) 1 and 3 of block j's words with rows 0 and 2 of block j + 1's,
+  // so lanes of row q hold the 8 consecutive columns (q / 2) 8 .. + 7 of
+  // block j + q % 2.
   auto epilogue = [&](const Tile &t) {
     const uint32_t ld = static_cast<uint32_t>(p.ncols) * 2u;
     const __amdgpu_buffer_rsrc_t ro =
         make_rsrc(p.out + t.row0 * p.ncols, static_cast<uint32_t>(t.rows_valid) * ld);
-    const int64_t wcol0 = static_cast<int64_t>(t.nt) * kEpiCols + wn * (kEpiCols / 2);
-    const int half = lane >> 5;
+    // 32-bit column and row arithmetic (the host keeps ncols below 2^22) from
+    // an opaque copy of the lane index, so nothing per lane stays live across tiles.
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int eq = ln >> 4;
+    const int wcol0 = static_cast<int>(t.nt) * kEpiCols + wn * (kEpiCols / 2) + (eq & 1) * 16 + (eq >> 1) * 8;
+    constexpr int kOut16 = kSwiglu ? kNI16 / 2 : kNI16;
 #pragma unroll
-    for (int i = 0; i < kMI; ++i) {
-      const uint32_t orow = static_cast<uint32_t>(wm * 128 + i * 32 + (lane & 31));
+    for (int i = 0; i < kMI16; ++i) {
+      const uint32_t orow = static_cast<uint32_t>(wm * 128 + i * 16 + (ln & 15));
 #pragma unroll
-      for (int jo = 0; jo < kOutNI; ++jo) {
-        uint32_t w[4][2];
+      for (int jp = 0; jp < kOut16; jp += 2) {
+        uint32_t w[2][2];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
+        for (int d = 0; d < 2; ++d) {
           float h[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             if constexpr (kSwiglu) {
-              const float gt = acc[i][jo][4 * g + q];
+              const float gt = acc[i][jp + d][q];
               h[q] = gt * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gt * -1.4426950408889634f)) *
-                     acc[i][jo + kNI / 2][4 * g + q];
+                     acc[i][jp + d + kNI16 / 2][q];
             } else {
-              h[q] = acc[i][jo][4 * g + q];
+              h[q] = acc[i][jp + d][q];
             }
           }
           const bf16x2 lo = {(__bf16)h[0], (__bf16)h[1]};
           const bf16x2 hi = {(__bf16)h[2], (__bf16)h[3]};
-          w[g][0] = __builtin_bit_cast(uint32_t, lo);
-          w[g][1] = __builtin_bit_cast(uint32_t, hi);
+          w[d][0] = __builtin_bit_cast(uint32_t, lo);
+          w[d][1] = __builtin_bit_cast(uint32_t, hi);
         }
-#pragma unroll
-        for (int gp = 0; gp < 4; gp += 2) {
-          u32x4 o;
+        u32x4 o;
 #if defined(__HIP_DEVICE_COMPILE__)
-          const auto s0 = __builtin_amdgcn_permlane32_swap(w[gp][0], w[gp + 1][0], false, false);
-          const auto s1 = __builtin_amdgcn_permlane32_swap(w[gp][1], w[gp + 1][1], false, false);
-          o = u32x4{s0[0], s1[0], s0[1], s1[1]};
+        const auto s0 = __builtin_amdgcn_permlane16_swap(w[0][0], w[1][0], false, false);
+        const auto s1 = __builtin_amdgcn_permlane16_swap(w[0][1], w[1][1], false, false);
+        o = u32x4{s0[0], s1[0], s0[1], s1[1]};
 #else
-          o = u32x4{0u, 0u, 0u, 0u};
+        o = u32x4{0u, 0u, 0u, 0u};
 #endif
-          const int64_t gcol = wcol0 + jo * 32 + (gp + half) * 8;
-          // Columns past the output get an offset past the resource: the store is dropped.
-          const uint32_t off = gcol < p.ncols ? orow * ld + static_cast<uint32_t>(gcol) * 2u : kNoAccess;
+        const int gcol = wcol0 + jp * 16;
+        // Columns past the output get an offset past the resource: the store is dropped.
+        const uint32_t off = gcol < ncols32 ? orow * ld + static_cast<uint32_t>(gcol) * 2u : kNoAccess;
 #if defined(__HIP_DEVICE_COMPILE__)
-          __builtin_amdgcn_raw_buffer_store_b128(o, ro, static_cast<int>(off), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(o, ro, static_cast<int>(off), 0, 0);
 #else
-          (void)off;
-          (void)ro;
-          (void)o;
+        (void)off;
+        (void)ro;
+        (void)o;
 #endif
-        }
       }
+      // One row block at a time: bounds the registers the epilogue holds.
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
@@ -682,20 +709,18 @@ __global__ __launch_bounds__(256) void grouped_gemm_pipe_kernel(GemmArgs p) {
   wait_vm_n<2 * kDma>();
   barrier();
   set_read_slot(0);
-#pragma unroll
-  for (int ks = 0; ks < kSubSteps; ++ks) read_frags(ks);
+  read_all();
 
   int sb = 0;  // ring slot of the current tile's stage 0
   for (int64_t round = 0;; ++round) {
     // One K step: MFMAs of stage kt (fragments in VGPRs), fragments of stage
     // kt + 1 read from LDS, DMA of the stage two ahead (this tile's kt + 2 or,
     // past its end, the next tile's kt + 2 - ktiles) into the slot of stage kt.
+    // One K step: MFMAs of stage kt (fragments in VGPRs), fragments of stage
+    // kt + 1 read from LDS, DMA of the stage two ahead (this tile's kt + 2 or,
+    // past its end, the next tile's kt + 2 - ktiles) into the slot of stage kt.
     auto step = [&](int kt, bool first, bool last) {
-      if (first) {
-        mfma_first();
-      } else {
-        mfma_ks(0);
-      }
+      mfma_unit(0, 0, first);
       __builtin_amdgcn_sched_barrier(0);
       // Stage kt + 1 has landed. In a tile's first step the previous tile's
       // output stores were issued after it and may still be in flight.
@@ -717,18 +742,20 @@ __global__ __launch_bounds__(256) void grouped_gemm_pipe_kernel(GemmArgs p) {
       if (last && more) setup_dma(nxt);
       const int kdma = !last ? kt + 2 : (more ? 0 : ktiles - 1);
       set_read_slot(sb + kt + 1);
-      read_frags(0);
-      mfma_ks(1);
+      mfma_unit(0, 1, first);
+      read_a(0, 0);
       issue_half(kdma, sb + kt + 2, 0);
-      sched_pattern<0x100, 0x020>();
-      mfma_ks(2);
-      read_frags(1);
+      sched_mix<32, 4, 8>();
+      mfma_unit(1, 0, false);
+      read_a(0, 1);
+      read_b(0);
       issue_half(kdma, sb + kt + 2, 1);
-      sched_pattern<0x100, 0x020>();
-      mfma_ks(3);
-      read_frags(2);
-      sched_pattern<0x100, 0>();
-      read_frags(3);
+      sched_mix<32, 12, 8>();
+      mfma_unit(1, 1, false);
+      read_a(1, 0);
+      sched_mix<32, 4, 0>();
+      read_a(1, 1);
+      read_b(1);
       __builtin_amdgcn_sched_barrier(0);
     };
     step(0, true, false);
@@ -738,24 +765,26 @@ __global__ __launch_bounds__(256) void grouped_gemm_pipe_kernel(GemmArgs p) {
     // Last step of the tile: it reads the next tile's stage 0 (DMA'd in the
     // step above) and DMAs its stage 1 (without a next tile: reads and DMA of
     // data nobody uses, so the code has no branch).
-    mfma_ks(0);
+    mfma_unit(0, 0, false);
     __builtin_amdgcn_sched_barrier(0);
     wait_dma();
     wait_lds();
     barrier();
     set_read_slot(sb + ktiles);
-    read_frags(0);
-    mfma_ks(1);
+    mfma_unit(0, 1, false);
+    read_a(0, 0);
     issue_half(more ? 1 : ktiles - 1, sb + ktiles + 1, 0);
-    sched_pattern<0x100, 0x020>();
-    mfma_ks(2);
-    read_frags(1);
+    sched_mix<32, 4, 8>();
+    mfma_unit(1, 0, false);
+    read_a(0, 1);
+    read_b(0);
     issue_half(more ? 1 : ktiles - 1, sb + ktiles + 1, 1);
-    sched_pattern<0x100, 0x020>();
-    mfma_ks(3);
-    read_frags(2);
-    sched_pattern<0x100, 0>();
-    read_frags(3);
+    sched_mix<32, 12, 8>();
+    mfma_unit(1, 1, false);
+    read_a(1, 0);
+    sched_mix<32, 4, 0>();
+    read_a(1, 1);
+    read_b(1);
     __builtin_amdgcn_sched_barrier(0);
     epilogue(cur);
     __builtin_amdgcn_sched_barrier(0);

@@ -120,9 +120,10 @@ def test_grouped_gemm_errors(pkg, dev):
     ([900, 0, 2100], 7168, 4096, True, True),         # fc1 gather class
 ])
 def test_pipelined_kernel_matches_drained_kernel(pkg, dev, sizes, K, N, swiglu, gather):
-    """K > 128 with 16-byte output rows runs the pipelined kernel (tiles back to back,
-    register epilogue); an output 2 bytes off 16-byte alignment runs the drained
-    kernel (LDS-staged epilogue). Same K order, same rounding: equal bit for bit."""
+    """K > 128 with 16-byte output rows runs the pipelined kernel (16x16x32 MFMAs,
+    tiles back to back, register epilogue); an output 2 bytes off 16-byte alignment
+    runs the drained kernel (32x32x16 MFMAs, LDS-staged epilogue). Both accumulate
+    K in the same ascending order in fp32 and round once: equal bit for bit."""
     g = torch.Generator().manual_seed(sum(sizes) + K + N)
     M = sum(sizes)
     w = (torch.randn(len(sizes), N, K, generator=g) * 0.05).to(torch.bfloat16).to(dev)
