@@ -716,9 +716,6 @@ __global__ __launch_bounds__(256) void grouped_gemm_pipe_kernel(GemmArgs p) {
     // One K step: MFMAs of stage kt (fragments in VGPRs), fragments of stage
     // kt + 1 read from LDS, DMA of the stage two ahead (this tile's kt + 2 or,
     // past its end, the next tile's kt + 2 - ktiles) into the slot of stage kt.
-    // One K step: MFMAs of stage kt (fragments in VGPRs), fragments of stage
-    // kt + 1 read from LDS, DMA of the stage two ahead (this tile's kt + 2 or,
-    // past its end, the next tile's kt + 2 - ktiles) into the slot of stage kt.
     auto step = [&](int kt, bool first, bool last) {
       mfma_unit(0, 0, first);
       __builtin_amdgcn_sched_barrier(0);
@@ -758,6 +755,8 @@ __global__ __launch_bounds__(256) void grouped_gemm_pipe_kernel(GemmArgs p) {
       read_b(1);
       __builtin_amdgcn_sched_barrier(0);
     };
+    // The first and the last step are peeled (with the last step inside the
+    // loop as a uniform branch the SwiGLU kernel measured 7% slower at c5).
     step(0, true, false);
     for (int kt = 1; kt + 2 < ktiles; ++kt) step(kt, false, false);
     step(ktiles - 2, false, true);
