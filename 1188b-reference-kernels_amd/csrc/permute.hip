@@ -5,11 +5,14 @@
 // case22...:47-69, case30...:44-58:
 //   out[map(t, e)] = x[t];  permuted_probs[map(t, e)] = probs[t, e]   (map >= 0)
 //
-// Layout of the work: one wavefront per token.  The wave reads the token's
+// Layout of the work: one workgroup of 4 wavefronts per token, each wavefront
+// owning every 4th 1 KiB slice of the row (256 x 4 measured best of 256-1024
+// threads x 1-4 wavefronts per row at c5).  A wave reads the token's
 // map entries 64 experts at a time, turns "entry >= 0" into a 64-bit ballot,
 // loads the x row once into VGPRs as 16-byte vectors (non-temporal), then
 // walks the ballot's set bits in ascending expert order and stores the row to
-// each destination.  The row is read from HBM once and written k times, which
+// each destination (plain stores: measured 4-5% faster than non-temporal ones
+// at c5 with a 1 GiB flush between calls).  The row is read from HBM once and written k times, which
 // is the algorithmic minimum (2TH + 2RH bytes plus the map and probs).
 #include <algorithm>
 
@@ -19,10 +22,10 @@ namespace moe {
 namespace {
 
 #ifndef MOE_PERMUTE_THREADS
-#define MOE_PERMUTE_THREADS 512
+#define MOE_PERMUTE_THREADS 256
 #endif
 #ifndef MOE_PERMUTE_SPLIT
-#define MOE_PERMUTE_SPLIT 2
+#define MOE_PERMUTE_SPLIT 4
 #endif
 constexpr int kThreads = MOE_PERMUTE_THREADS;
 constexpr int kSplit = MOE_PERMUTE_SPLIT;            // wavefronts sharing one token row
@@ -82,7 +85,7 @@ __global__ __launch_bounds__(kThreads) void permute_kernel(PermuteArgs a) {
 #pragma unroll
             for (int j = 0; j < kMaxVecPerLane; ++j) {
               const int64_t v = seg + (j * kSplit + part) * kWave + lane;
-              if (v < nvec) __builtin_nontemporal_store(buf[j], o + v);
+              if (v < nvec) o[v] = buf[j];  // plain stores: 4-5% faster than non-temporal ones here
             }
           }
         }
