@@ -5,9 +5,9 @@
 // case22...:47-69, case30...:44-58:
 //   out[map(t, e)] = x[t];  permuted_probs[map(t, e)] = probs[t, e]   (map >= 0)
 //
-// Layout of the work: one workgroup of 4 wavefronts per token, each wavefront
-// owning every 4th 1 KiB slice of the row (256 x 4 measured best of 256-1024
-// threads x 1-4 wavefronts per row at c5).  A wave reads the token's
+// Layout of the work: 4 (token-major map) or 2 (expert-major map) wavefronts per
+// token, each owning every 4th / 2nd 1 KiB slice of the row (PermShape).  A
+// wave reads the token's
 // map entries 64 experts at a time, turns "entry >= 0" into a 64-bit ballot,
 // loads the x row once into VGPRs as 16-byte vectors (non-temporal), then
 // walks the ballot's set bits in ascending expert order and stores the row to
@@ -21,16 +21,21 @@
 namespace moe {
 namespace {
 
-#ifndef MOE_PERMUTE_THREADS
-#define MOE_PERMUTE_THREADS 256
-#endif
-#ifndef MOE_PERMUTE_SPLIT
-#define MOE_PERMUTE_SPLIT 4
-#endif
-constexpr int kThreads = MOE_PERMUTE_THREADS;
-constexpr int kSplit = MOE_PERMUTE_SPLIT;            // wavefronts sharing one token row
-constexpr int kTokensPerBlock = kThreads / kWave / kSplit;
-constexpr int kMaxVecPerLane = 16 / kSplit;         // 16-byte vectors per lane per pass
+// Launch shape per map layout (best of 256-1024 threads x 1-4 wavefronts per
+// token row, measured with a 1 GiB flush between calls): a token-major map row
+// is one contiguous read, so 4 wavefronts share a row, one token per
+// workgroup; an expert-major map is read down a column (stride T entries), so
+// 2 wavefronts share a row and a workgroup takes 4 neighbouring tokens, whose
+// map entries share cache lines.
+template <bool kExpertMajor>
+struct PermShape {
+  static constexpr int kThreads = kExpertMajor ? 512 : 256;
+  static constexpr int kSplit = kExpertMajor ? 2 : 4;  // wavefronts sharing one token row
+  static constexpr int kTokensPerBlock = kThreads / kWave / kSplit;
+  static constexpr int kMaxVecPerLane = 16 / kSplit;   // 16-byte vectors per lane per pass
+};
+constexpr int kMinTokensPerBlock = 1;  // of both shapes (sizes the zero-tail workspace)
+constexpr int kTailThreads = 256;      // zero-tail kernel
 
 struct PermuteArgs {
   const uint16_t *x;
@@ -49,7 +54,11 @@ __device__ __forceinline__ int64_t map_at(const PermuteArgs &a, int64_t t, int64
 }
 
 template <bool kI64, bool kExpertMajor, bool kProbs, bool kVec>
-__global__ __launch_bounds__(kThreads) void permute_kernel(PermuteArgs a) {
+__global__ __launch_bounds__(PermShape<kExpertMajor>::kThreads) void permute_kernel(PermuteArgs a) {
+  constexpr int kThreads = PermShape<kExpertMajor>::kThreads;
+  constexpr int kSplit = PermShape<kExpertMajor>::kSplit;
+  constexpr int kTokensPerBlock = PermShape<kExpertMajor>::kTokensPerBlock;
+  constexpr int kMaxVecPerLane = PermShape<kExpertMajor>::kMaxVecPerLane;
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
   const int part = wave % kSplit;  // which share of the row this wave copies
@@ -129,23 +138,23 @@ __global__ __launch_bounds__(kThreads) void permute_kernel(PermuteArgs a) {
 
 // Zero-fills out rows [R, num_out) and pp[R, num_out), R = sum(block_counts).
 template <bool kVec>
-__global__ __launch_bounds__(kThreads) void permute_zero_tail_kernel(const int32_t *block_counts,
+__global__ __launch_bounds__(kTailThreads) void permute_zero_tail_kernel(const int32_t *block_counts,
                                                                      int64_t nblocks, uint16_t *out,
                                                                      float *pp, int64_t H,
                                                                      int64_t num_out) {
-  __shared__ int64_t partial[kThreads];
+  __shared__ int64_t partial[kTailThreads];
   int64_t s = 0;
-  for (int64_t i = threadIdx.x; i < nblocks; i += kThreads) s += block_counts[i];
+  for (int64_t i = threadIdx.x; i < nblocks; i += kTailThreads) s += block_counts[i];
   partial[threadIdx.x] = s;
   __syncthreads();
-  for (int w = kThreads / 2; w > 0; w >>= 1) {
+  for (int w = kTailThreads / 2; w > 0; w >>= 1) {
     if (threadIdx.x < w) partial[threadIdx.x] += partial[threadIdx.x + w];
     __syncthreads();
   }
   const int64_t R = partial[0];
   if (R >= num_out) return;
-  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  const int64_t gstride = static_cast<int64_t>(gridDim.x) * kThreads;
+  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * kTailThreads + threadIdx.x;
+  const int64_t gstride = static_cast<int64_t>(gridDim.x) * kTailThreads;
   if (pp != nullptr) {
     for (int64_t i = R + gtid; i < num_out; i += gstride) pp[i] = 0.0f;
   }
@@ -163,6 +172,7 @@ __global__ __launch_bounds__(kThreads) void permute_zero_tail_kernel(const int32
 
 template <bool kI64, bool kExpertMajor, bool kProbs>
 void launch_permute_3(const PermuteArgs &a, bool vec, int64_t grid, hipStream_t s) {
+  constexpr int kThreads = PermShape<kExpertMajor>::kThreads;
   if (vec) {
     permute_kernel<kI64, kExpertMajor, kProbs, true><<<dim3(grid), dim3(kThreads), 0, s>>>(a);
   } else {
@@ -207,7 +217,7 @@ extern "C" {
 
 size_t moe_permute_workspace_size(int64_t T) {
   if (T < 0) return 0;
-  return static_cast<size_t>(moe::ceil_div(T, moe::kTokensPerBlock)) * sizeof(int32_t) + 256;
+  return static_cast<size_t>(moe::ceil_div(T, moe::kMinTokensPerBlock)) * sizeof(int32_t) + 256;
 }
 
 int moe_permute(const moe_bf16_t *x, int64_t T, int64_t H, const void *row_id_map, int idx_dtype,
@@ -232,7 +242,8 @@ int moe_permute(const moe_bf16_t *x, int64_t T, int64_t H, const void *row_id_ma
   if (permuted_probs != nullptr && probs == nullptr && T * E > 0) {
     return fail(MOE_ERR_INVALID_ARG, "moe_permute: permuted_probs given without probs");
   }
-  const int64_t nblocks = ceil_div(T, kTokensPerBlock);
+  const bool em = map_layout == MOE_MAP_EXPERT_MAJOR;
+  const int64_t nblocks = ceil_div(T, em ? PermShape<true>::kTokensPerBlock : PermShape<false>::kTokensPerBlock);
   if (nblocks > 0x7fffffff) return fail(MOE_ERR_CAPACITY, "moe_permute: T=%lld too large", (long long)T);
   if (zero_tail && (workspace == nullptr || workspace_bytes < moe_permute_workspace_size(T))) {
     return fail(MOE_ERR_WORKSPACE, "moe_permute: zero_tail needs %zu bytes of workspace, got %zu",
@@ -253,7 +264,6 @@ int moe_permute(const moe_bf16_t *x, int64_t T, int64_t H, const void *row_id_ma
   const bool vec = (H % 8 == 0) && is_aligned(x, 16) && is_aligned(out, 16);
   if (nblocks > 0) {
     const bool i64 = idx_dtype == MOE_IDX_I64;
-    const bool em = map_layout == MOE_MAP_EXPERT_MAJOR;
     if (i64 && em) launch_permute_2<true, true>(a, vec, nblocks, s);
     else if (i64) launch_permute_2<true, false>(a, vec, nblocks, s);
     else if (em) launch_permute_2<false, true>(a, vec, nblocks, s);
@@ -263,12 +273,12 @@ int moe_permute(const moe_bf16_t *x, int64_t T, int64_t H, const void *row_id_ma
   }
   if (zero_tail && num_out > 0) {
     const int64_t tail_elems = num_out * (H > 0 ? H : 1);
-    const int64_t grid = std::min<int64_t>(1024, std::max<int64_t>(1, ceil_div(tail_elems, kThreads * 8)));
+    const int64_t grid = std::min<int64_t>(1024, std::max<int64_t>(1, ceil_div(tail_elems, kTailThreads * 8)));
     if (vec) {
-      permute_zero_tail_kernel<true><<<dim3(grid), dim3(kThreads), 0, s>>>(
+      permute_zero_tail_kernel<true><<<dim3(grid), dim3(kTailThreads), 0, s>>>(
           a.block_counts, nblocks, out, a.pp, H, num_out);
     } else {
-      permute_zero_tail_kernel<false><<<dim3(grid), dim3(kThreads), 0, s>>>(
+      permute_zero_tail_kernel<false><<<dim3(grid), dim3(kTailThreads), 0, s>>>(
           a.block_counts, nblocks, out, a.pp, H, num_out);
     }
     return check_launch("moe_permute(zero tail)");
