@@ -197,6 +197,67 @@ __global__ __launch_bounds__(kScanThreads) void rim_scan_kernel(int32_t *counts,
   }
 }
 
+// The same scan with every count staged in LDS first (one round of
+// independent 16-byte loads), for nc * E <= kLdsScanMax counts and E % 4 == 0:
+// thread (part, expert) column-sums a run of chunks, the runs and the experts
+// are scanned in LDS, and the bases are written back from LDS with 16-byte
+// stores.  One dependent global round trip instead of four.
+constexpr int kLdsScanMax = 24576;  // counts (96 KiB of LDS)
+__global__ __launch_bounds__(kScanThreads) void rim_scan_lds_kernel(int32_t *counts, int64_t nc, int64_t E,
+                                                                    int32_t *expert_offsets) {
+  __shared__ __attribute__((aligned(16))) int32_t cnt[kLdsScanMax];
+  __shared__ int64_t totals[kMaxE];
+  __shared__ int64_t part_sums[kScanThreads];
+  __shared__ int64_t wave_sums[kScanThreads / kWave];
+  __shared__ int64_t grand_total;
+  const int64_t n = nc * E;
+  for (int64_t i = threadIdx.x; i < n / 4; i += kScanThreads)
+    reinterpret_cast<u32x4 *>(cnt)[i] = reinterpret_cast<const u32x4 *>(counts)[i];
+  __syncthreads();
+  // Threads = parts x experts (E <= kScanThreads here); part p sums chunks [p per, (p+1) per).
+  const int64_t parts = kScanThreads / E;
+  const int64_t per = ceil_div(nc, parts);
+  const int64_t e = threadIdx.x % E, p = threadIdx.x / E;
+  const bool active = p < parts;
+  const int64_t c_begin = p * per, c_end = min(c_begin + per, nc);
+  int64_t sum = 0;
+  if (active)
+    for (int64_t c = c_begin; c < c_end; ++c) sum += cnt[c * E + e];
+  part_sums[threadIdx.x] = sum;
+  __syncthreads();
+  if (active && p == 0) {
+    int64_t run = 0;
+    for (int64_t q = 0; q < parts; ++q) {
+      const int64_t v = part_sums[q * E + e];
+      part_sums[q * E + e] = run;
+      run += v;
+    }
+    totals[e] = run;
+  }
+  __syncthreads();
+  // Exclusive scan of the totals over experts -> offsets.
+  const int64_t local = threadIdx.x < E ? totals[threadIdx.x] : 0;
+  const int64_t off = block_exclusive_scan(local, wave_sums, &grand_total);
+  if (threadIdx.x < E) totals[threadIdx.x] = off;
+  __syncthreads();
+  if (expert_offsets != nullptr) {
+    for (int64_t i = threadIdx.x; i < E; i += kScanThreads) expert_offsets[i] = static_cast<int32_t>(totals[i]);
+    if (threadIdx.x == 0) expert_offsets[E] = static_cast<int32_t>(grand_total);
+  }
+  // Bases in place in LDS, then stored as 16-byte vectors.
+  if (active) {
+    int64_t run = totals[e] + part_sums[threadIdx.x];
+    for (int64_t c = c_begin; c < c_end; ++c) {
+      const int32_t v = cnt[c * E + e];
+      cnt[c * E + e] = static_cast<int32_t>(run);
+      run += v;
+    }
+  }
+  __syncthreads();
+  for (int64_t i = threadIdx.x; i < n / 4; i += kScanThreads)
+    reinterpret_cast<u32x4 *>(counts)[i] = reinterpret_cast<const u32x4 *>(cnt)[i];
+}
+
 __global__ __launch_bounds__(kThreads) void rim_fill_kernel(const uint8_t *mask, int64_t T, int64_t E,
                                                             const int32_t *base, int64_t *row_em,
                                                             int64_t *row_tm, int32_t *row_em32, bool vec) {
@@ -207,12 +268,20 @@ __global__ __launch_bounds__(kThreads) void rim_fill_kernel(const uint8_t *mask,
   const int64_t t0 = chunk * kChunk;
   const int lane = lane_id(), wave = threadIdx.x / kWave;
   const int64_t t = t0 + lane;
-  // This chunk's base row per expert, read once (independent loads).
-  for (int64_t e = threadIdx.x; e < E; e += kThreads) s_base[e] = base[chunk * E + e];
+  // This chunk's base row per expert, read once (independent loads). With
+  // E <= kThreads the load is issued before the first mask tile's loads and
+  // stored after them, so the two round trips overlap.
+  int32_t bv = 0;
+  if (E <= kThreads) {
+    if (threadIdx.x < E) bv = base[chunk * E + threadIdx.x];
+  } else {
+    for (int64_t e = threadIdx.x; e < E; e += kThreads) s_base[e] = base[chunk * E + e];
+  }
   for (int64_t eg0 = 0; eg0 < E; eg0 += kEG) {
     const int eg_n = static_cast<int>(E - eg0 < kEG ? E - eg0 : kEG);
-    __syncthreads();
+    if (eg0 > 0) __syncthreads();
     load_mask_tile(tile, mask, T, E, t0, eg0, eg_n, vec);
+    if (eg0 == 0 && E <= kThreads && threadIdx.x < E) s_base[threadIdx.x] = bv;
     __syncthreads();
     for (int c = wave; c < eg_n; c += kWaves) {
       const int64_t e = eg0 + c;
@@ -280,7 +349,11 @@ int moe_row_id_map(const uint8_t *routing_map, int64_t T, int64_t E, int64_t *ro
   rim_count_kernel<<<dim3(nc), dim3(kThreads), 0, s>>>(routing_map, T, E, counts, vec);
   int st = check_launch("moe_row_id_map(count)");
   if (st != MOE_OK) return st;
-  rim_scan_kernel<<<dim3(1), dim3(kScanThreads), 0, s>>>(counts, nc, E, expert_offsets);
+  if (nc * E <= kLdsScanMax && E % 4 == 0 && E <= kScanThreads && is_aligned(counts, 16)) {
+    rim_scan_lds_kernel<<<dim3(1), dim3(kScanThreads), 0, s>>>(counts, nc, E, expert_offsets);
+  } else {
+    rim_scan_kernel<<<dim3(1), dim3(kScanThreads), 0, s>>>(counts, nc, E, expert_offsets);
+  }
   st = check_launch("moe_row_id_map(scan)");
   if (st != MOE_OK) return st;
   rim_fill_kernel<<<dim3(nc), dim3(kThreads), 0, s>>>(routing_map, T, E, counts, row_expert_major,
