@@ -719,7 +719,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_pipe_kernel(GemmArgs p) {
   };
 
   // ---- first tile: stages 0 and 1 in flight, stage 0 read into VGPRs
-  Tile cur, nxt;
+  Tile cur{}, nxt{};  // nxt stays zero when no tile follows (its row loads then read nothing)
   if (!find_tile(0, cur)) return;
   load_rows(cur, true);
   setup_dma(cur);
