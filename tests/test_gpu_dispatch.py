@@ -138,7 +138,13 @@ def _wide(R, H, seed):
 @pytest.mark.parametrize("layout", ["token_major", "expert_major"])
 @pytest.mark.parametrize("idx", [torch.int64, torch.int32])
 @pytest.mark.parametrize("merge", [False, True])
-@pytest.mark.parametrize("T,E,k,H", [(257, 8, 2, 2048), (96, 64, 8, 7168), (40, 320, 6, 72), (21, 9, 4, 11)])
+# Shapes cover both launch forms: one wavefront per 1 KiB slice of the row (up to
+# 16 per token) and 4 tokens per workgroup for short rows (with a partial last
+# workgroup), each with the map read per wavefront (E <= 64) or staged in LDS
+# (E > 64, including a partial last 64-expert chunk and E = 1024), plus the
+# scalar path for rows that are not a multiple of 8 elements.
+@pytest.mark.parametrize("T,E,k,H", [(257, 8, 2, 2048), (96, 64, 8, 7168), (40, 320, 6, 72), (21, 9, 4, 11),
+                                     (43, 130, 3, 24), (29, 200, 5, 13), (33, 1024, 8, 4096)])
 def test_unpermute_matches_oracle(pkg, dev, layout, idx, merge, T, E, k, H):
     rm = _mask(T, E, k, seed=T + 7 * E)
     em, tm = ref_torch.row_id_map(rm)
@@ -193,7 +199,8 @@ def test_unpermute_cases_24_32_modular(pkg, dev):
 
 
 # -------------------------------------------------------------- permute bwd
-@pytest.mark.parametrize("T,E,k,H", [(512, 320, 8, 1024), (200, 64, 8, 7168), (37, 6, 2, 20)])
+@pytest.mark.parametrize("T,E,k,H", [(512, 320, 8, 1024), (200, 64, 8, 7168), (37, 6, 2, 20), (19, 130, 4, 40),
+                                     (23, 100, 3, 9)])
 def test_permute_bwd_matches_oracle(pkg, dev, T, E, k, H):
     rm = _mask(T, E, k, seed=11 * T)
     em, _ = ref_torch.row_id_map(rm)
