@@ -218,8 +218,11 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
       for (int j = 0; j < kDmaA; ++j) {
         const int r = (j * kWaves + wave) * 8 + (lane >> 3);
         const int lchunk = (lane & 7) ^ kc_swz(r);
-        a_off[j] = static_cast<int>(static_cast<uint32_t>(min(r, rows_valid - 1)) * static_cast<uint32_t>(N) * 2u +
-                                    lchunk * 16);
+        // Rows past the group's end read as zeros (results dropped; zero
+        // operands cost the MFMAs less energy than a repeated real row).
+        a_off[j] = r < rows_valid ? static_cast<int>(static_cast<uint32_t>(r) * static_cast<uint32_t>(N) * 2u +
+                                                     lchunk * 16)
+                                  : static_cast<int>(kNoAccess);
       }
     }
     b_step = kBK * static_cast<int>(K) * 2;
