@@ -7,7 +7,9 @@
 // expert 1's, ...  The same construction appears in case15/17/18/21/22/24/30/32.
 //
 // Three launches, all integer work on a mask of T*E bytes:
-//   1. count: block = one 64-token chunk; the chunk's mask tile is loaded into
+//   1. count: block = one 64-token chunk x one group of up to 128 experts
+//      (grid.y; at E = 320 three groups, 3x the workgroups of one block per
+//      chunk walking the groups in turn); the chunk's mask tile is loaded into
 //      LDS with 16-byte vector loads (one per thread at E = 64), then
 //      per-expert popcounts (wave ballots over 64 tokens) -> counts[chunk][e].
 //   2. scan: 16 experts per workgroup; per-expert sums over 16 runs of chunks
@@ -15,7 +17,7 @@
 //      then counts are rewritten in place as the (chunk, expert) base row
 //      relative to the expert's first row, and the expert's total is stored.
 //      (A single workgroup scanning every expert took 35 us at E = 320.)
-//   3. fill: block = one 64-token chunk; the experts' offsets are the
+//   3. fill: block = one 64-token chunk x one group of up to 128 experts; the experts' offsets are the
 //      exclusive scan of the totals (E <= 4096 values, scanned in LDS by every
 //      block; block 0 stores them as expert_offsets[0..E]); mask tile and the
 //      chunk's E bases go through LDS, each wave ranks 64 tokens of one expert with ballot +
@@ -74,15 +76,13 @@ __global__ __launch_bounds__(kThreads) void rim_count_kernel(const uint8_t *mask
   const int64_t chunk = blockIdx.x;
   const int64_t t0 = chunk * kChunk;
   const int lane = lane_id(), wave = threadIdx.x / kWave;
-  for (int64_t eg0 = 0; eg0 < E; eg0 += kEG) {
-    const int eg_n = static_cast<int>(E - eg0 < kEG ? E - eg0 : kEG);
-    __syncthreads();
-    load_mask_tile(tile, mask, T, E, t0, eg0, eg_n, vec);
-    __syncthreads();
-    for (int c = wave; c < eg_n; c += kWaves) {
-      const uint64_t m = __ballot(tile[lane * kTileStride + c] != 0);
-      if (lane == 0) counts[chunk * E + eg0 + c] = __popcll(m);
-    }
+  const int64_t eg0 = static_cast<int64_t>(blockIdx.y) * kEG;  // this block's group of experts
+  const int eg_n = static_cast<int>(E - eg0 < kEG ? E - eg0 : kEG);
+  load_mask_tile(tile, mask, T, E, t0, eg0, eg_n, vec);
+  __syncthreads();
+  for (int c = wave; c < eg_n; c += kWaves) {
+    const uint64_t m = __ballot(tile[lane * kTileStride + c] != 0);
+    if (lane == 0) counts[chunk * E + eg0 + c] = __popcll(m);
   }
 }
 
@@ -196,44 +196,43 @@ __global__ __launch_bounds__(kThreads) void rim_fill_kernel(const uint8_t *mask,
       bv[i] = base[chunk * E + e_first + i];
     }
   }
-  for (int64_t eg0 = 0; eg0 < E; eg0 += kEG) {
-    const int eg_n = static_cast<int>(E - eg0 < kEG ? E - eg0 : kEG);
-    if (eg0 > 0) __syncthreads();
-    load_mask_tile(tile, mask, T, E, t0, eg0, eg_n, vec);
-    if (eg0 == 0) {
-      int32_t local = 0;
+  const int64_t eg0 = static_cast<int64_t>(blockIdx.y) * kEG;  // this block's group of experts
+  const int eg_n = static_cast<int>(E - eg0 < kEG ? E - eg0 : kEG);
+  const bool first_block = chunk == 0 && blockIdx.y == 0;
+  load_mask_tile(tile, mask, T, E, t0, eg0, eg_n, vec);
+  {
+    int32_t local = 0;
 #pragma unroll
-      for (int i = 0; i < kMaxE / kThreads; ++i) local += tv[i];
-      int32_t run = block_exclusive_scan(local, wave_sums, &grand_total);
+    for (int i = 0; i < kMaxE / kThreads; ++i) local += tv[i];
+    int32_t run = block_exclusive_scan(local, wave_sums, &grand_total);
 #pragma unroll
-      for (int i = 0; i < kMaxE / kThreads; ++i) {
-        if (i < per && e_first + i < E) {
-          if (chunk == 0 && expert_offsets != nullptr) expert_offsets[e_first + i] = run;
-          s_base[e_first + i] = run + bv[i];
-          run += tv[i];
-        }
+    for (int i = 0; i < kMaxE / kThreads; ++i) {
+      if (i < per && e_first + i < E) {
+        if (first_block && expert_offsets != nullptr) expert_offsets[e_first + i] = run;
+        s_base[e_first + i] = run + bv[i];
+        run += tv[i];
       }
-      if (chunk == 0 && expert_offsets != nullptr && threadIdx.x == 0) expert_offsets[E] = grand_total;
     }
-    __syncthreads();
-    for (int c = wave; c < eg_n; c += kWaves) {
-      const int64_t e = eg0 + c;
-      const bool sel = tile[lane * kTileStride + c] != 0;
-      const uint64_t m = __ballot(sel);
-      const int32_t b = s_base[e];
-      const int32_t v = sel ? b + lanes_below(m) : -1;
-      if (t < T) {
-        if (row_em != nullptr) row_em[e * T + t] = v;
-        if (row_em32 != nullptr) row_em32[e * T + t] = v;
-      }
-      out_tile[lane * (kEG + 1) + c] = v;
+    if (first_block && expert_offsets != nullptr && threadIdx.x == 0) expert_offsets[E] = grand_total;
+  }
+  __syncthreads();
+  for (int c = wave; c < eg_n; c += kWaves) {
+    const int64_t e = eg0 + c;
+    const bool sel = tile[lane * kTileStride + c] != 0;
+    const uint64_t m = __ballot(sel);
+    const int32_t b = s_base[e];
+    const int32_t v = sel ? b + lanes_below(m) : -1;
+    if (t < T) {
+      if (row_em != nullptr) row_em[e * T + t] = v;
+      if (row_em32 != nullptr) row_em32[e * T + t] = v;
     }
-    __syncthreads();
-    if (row_tm != nullptr) {
-      for (int i = threadIdx.x; i < kChunk * eg_n; i += kThreads) {
-        const int r = i / eg_n, c = i % eg_n;
-        if (t0 + r < T) row_tm[(t0 + r) * E + eg0 + c] = out_tile[r * (kEG + 1) + c];
-      }
+    out_tile[lane * (kEG + 1) + c] = v;
+  }
+  __syncthreads();
+  if (row_tm != nullptr) {
+    for (int i = threadIdx.x; i < kChunk * eg_n; i += kThreads) {
+      const int r = i / eg_n, c = i % eg_n;
+      if (t0 + r < T) row_tm[(t0 + r) * E + eg0 + c] = out_tile[r * (kEG + 1) + c];
     }
   }
 }
@@ -280,7 +279,8 @@ int moe_row_id_map(const uint8_t *routing_map, int64_t T, int64_t E, int64_t *ro
     return MOE_OK;
   }
   const bool vec = (E % 16 == 0) && is_aligned(routing_map, 16);
-  rim_count_kernel<<<dim3(nc), dim3(kThreads), 0, s>>>(routing_map, T, E, counts, vec);
+  const dim3 chunk_grid(static_cast<uint32_t>(nc), static_cast<uint32_t>(ceil_div(E, kEG)));
+  rim_count_kernel<<<chunk_grid, dim3(kThreads), 0, s>>>(routing_map, T, E, counts, vec);
   int st = check_launch("moe_row_id_map(count)");
   if (st != MOE_OK) return st;
   int32_t *totals = counts + nc * E;
@@ -288,7 +288,7 @@ int moe_row_id_map(const uint8_t *routing_map, int64_t T, int64_t E, int64_t *ro
                                                                                                    totals);
   st = check_launch("moe_row_id_map(scan)");
   if (st != MOE_OK) return st;
-  rim_fill_kernel<<<dim3(nc), dim3(kThreads), 0, s>>>(routing_map, T, E, counts, totals, row_expert_major,
+  rim_fill_kernel<<<chunk_grid, dim3(kThreads), 0, s>>>(routing_map, T, E, counts, totals, row_expert_major,
                                                        row_token_major, row_expert_major_i32, expert_offsets, vec);
   return check_launch("moe_row_id_map(fill)");
 }
