@@ -60,7 +60,10 @@ def test_row_id_map_empty(pkg, dev):
 # ------------------------------------------------------------------ permute
 @pytest.mark.parametrize("layout", ["token_major", "expert_major"])
 @pytest.mark.parametrize("idx", [torch.int64, torch.int32])
-@pytest.mark.parametrize("T,E,k,H", [(300, 8, 2, 2048), (129, 64, 8, 7168), (70, 320, 6, 136), (33, 5, 3, 13)])
+# E <= 64: map read per wavefront; 64 < E <= 1024: staged in LDS once per workgroup (vector and scalar rows,
+# partial last workgroup); E > 1024: per-wavefront reads again.
+@pytest.mark.parametrize("T,E,k,H", [(300, 8, 2, 2048), (129, 64, 8, 7168), (70, 320, 6, 136), (33, 5, 3, 13),
+                                     (23, 200, 5, 13), (41, 1100, 4, 64)])
 def test_permute_matches_oracle(pkg, dev, layout, idx, T, E, k, H):
     rm = _mask(T, E, k, seed=3 * T + E)
     em, tm = ref_torch.row_id_map(rm)
