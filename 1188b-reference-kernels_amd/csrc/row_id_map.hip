@@ -7,9 +7,9 @@
 // expert 1's, ...  The same construction appears in case15/17/18/21/22/24/30/32.
 //
 // Three launches, all integer work on a mask of T*E bytes:
-//   1. count: block = one 64-token chunk x one group of up to 128 experts
-//      (grid.y; at E = 320 three groups, 3x the workgroups of one block per
-//      chunk walking the groups in turn); the chunk's mask tile is loaded into
+//   1. count: block = one 64-token chunk x one group of up to 32 experts
+//      (grid.y: 4 groups at E = 64, 10 at E = 320; one block per chunk walking
+//      128-expert groups in turn was 1.4-2.3x slower); the chunk's mask tile is loaded into
 //      LDS with 16-byte vector loads (one per thread at E = 64), then
 //      per-expert popcounts (wave ballots over 64 tokens) -> counts[chunk][e].
 //   2. scan: 16 experts per workgroup; per-expert sums over 16 runs of chunks
@@ -17,7 +17,7 @@
 //      then counts are rewritten in place as the (chunk, expert) base row
 //      relative to the expert's first row, and the expert's total is stored.
 //      (A single workgroup scanning every expert took 35 us at E = 320.)
-//   3. fill: block = one 64-token chunk x one group of up to 128 experts; the experts' offsets are the
+//   3. fill: block = one 64-token chunk x one group of up to 32 experts; the experts' offsets are the
 //      exclusive scan of the totals (E <= 4096 values, scanned in LDS by every
 //      block; block 0 stores them as expert_offsets[0..E]); mask tile and the
 //      chunk's E bases go through LDS, each wave ranks 64 tokens of one expert with ballot +
@@ -33,7 +33,7 @@ namespace {
 constexpr int kChunk = 64;          // tokens per chunk = wave width (one ballot)
 constexpr int kThreads = 256;       // count / fill blocks
 constexpr int kWaves = kThreads / kWave;
-constexpr int kEG = 128;            // experts per LDS group in the fill kernel
+constexpr int kEG = 32;             // experts per block (grid.y) of the count and fill kernels
 constexpr int kMaxE = 4096;
 
 // Byte tile [kChunk][kEG] of the mask, row stride kTileStride bytes (odd word
