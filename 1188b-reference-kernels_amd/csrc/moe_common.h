@@ -59,6 +59,15 @@ __device__ __forceinline__ int64_t readlane64(int64_t v, int lane) {
   return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
+// A wave-uniform 64-bit value as scalar registers.  Each half goes through
+// uint32_t: the builtin returns int, and OR-ing that int into a 64-bit value
+// would sign-extend a low half with bit 31 set across the high half.
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
 __device__ __forceinline__ float readlane_f32(float v, int lane) {
   return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), lane));
 }

@@ -85,12 +85,6 @@ __device__ __forceinline__ int64_t map_at(const UnpermuteArgs &a, int64_t t, int
   return load_idx<kI64>(a.map, kExpertMajor ? e * a.T + t : t * a.E + e);
 }
 
-__device__ __forceinline__ uint64_t uniform_u64(uint64_t v) {
-  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
-  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
-  return (static_cast<uint64_t>(hi) << 32) | lo;
-}
-
 __device__ __forceinline__ void accumulate8(float (&acc)[8], const u32x4 &v, float w, bool weighted) {
   const uint32_t d[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll

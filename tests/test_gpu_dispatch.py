@@ -80,6 +80,35 @@ def test_permute_matches_oracle(pkg, dev, layout, idx, T, E, k, H):
         assert_bits_equal(pp, ref_pp, f"permuted probs num_out={num_out}")
 
 
+@pytest.mark.parametrize("layout", ["token_major", "expert_major"])
+@pytest.mark.parametrize("E", [96, 320])
+def test_permute_stores_stay_inside_out(pkg, dev, layout, E):
+    """Regression: a 64-bit ballot rebuilt from two 32-bit scalar halves must not sign-extend the low half.
+
+    With expert c*64+31 routed (bit 31 of the chunk's ballot), a sign-extended low half set bits 32..63 too,
+    and the kernel stored rows to the map entries of unrouted experts (-1: one row before `out`). Here `out` is
+    a view inside a sentinel-filled buffer whose guard rows must stay untouched.
+    """
+    T, k, H = 64, 4, 64
+    rm = torch.zeros(T, E, dtype=torch.bool)
+    for t in range(T):
+        rm[t, [31, 64 + 31 if E > 95 else 1, (t * 7) % E, (t * 13 + 5) % E]] = True  # lane 31 of chunks 0 and 1
+    em, tm = ref_torch.row_id_map(rm)
+    R = int(rm.sum())
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(E)).to(torch.bfloat16)
+    probs = torch.rand(T, E, generator=torch.Generator().manual_seed(E + 1)) * rm
+    sentinel = torch.full((R + 2, H), 7.0, dtype=torch.bfloat16, device=dev)
+    pp = torch.full((R + 2,), 7.0, dtype=torch.float32, device=dev)
+    m = (tm if layout == "token_major" else em).to(dev)
+    pkg.ops.permute(x.to(dev), m, probs.to(dev), num_out=R, layout=layout, zero_tail=False,
+                    out=sentinel[1:R + 1], permuted_probs=pp[1:R + 1])
+    assert torch.all(sentinel[0] == 7.0) and torch.all(sentinel[R + 1] == 7.0), "row stored outside out"
+    assert pp[0].item() == 7.0 and pp[R + 1].item() == 7.0, "prob stored outside permuted_probs"
+    ref_out, ref_pp = ref_torch.permute_token_major(x, tm, probs, R)
+    assert_bits_equal(sentinel[1:R + 1], ref_out, "permute out")
+    assert_bits_equal(pp[1:R + 1], ref_pp, "permuted probs")
+
+
 def test_permute_case17_reference_inputs(pkg, dev):
     # The case17 generator at the reference shape class (T reduced to 4096 to keep
     # the CPU oracle quick; the routing stream is the reference's own).
