@@ -145,7 +145,9 @@ def test_empty_problems_are_no_ops():
 
 def test_workspace_sizes():
     lib = L.lib()
-    assert lib.moe_row_id_map_workspace_size(16384, 64) >= 256 * 64 * 4
+    # chunk counts [ceil(T/64), E] plus the expert totals [E], int32
+    assert lib.moe_row_id_map_workspace_size(16384, 64) >= (256 * 64 + 64) * 4
+    assert lib.moe_row_id_map_workspace_size(16385, 320) >= (257 * 320 + 320) * 4
     assert lib.moe_permute_workspace_size(16384) >= 4096 * 4
     assert lib.moe_row_id_map_workspace_size(-1, 4) == 0
     # router: one fp32 logits plane (used when the top-k call gets no logits output)
