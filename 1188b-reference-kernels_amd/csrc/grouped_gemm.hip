@@ -724,6 +724,26 @@ __global__ __launch_bounds__(256) void grouped_gemm_pipe_kernel(GemmArgs p) {
     }
   };
 
+  // The part of a K step after its barrier: MFMA units 1-3 of the fragments
+  // in VGPRs, the next stage's fragments read from the LDS slot set by
+  // set_read_slot into the registers each unit frees, and the DMA of stage
+  // `kdma` (of the tile set up last) into ring slot `wr`.
+  auto step_body = [&](bool zero, int kdma, int wr) __attribute__((always_inline)) {
+    mfma_unit(0, 1, zero);
+    read_a(0, 0);
+    issue_half(kdma, wr, 0);
+    sched_mix<32, 4, 8>();
+    mfma_unit(1, 0, false);
+    read_a(0, 1);
+    read_b(0);
+    issue_half(kdma, wr, 1);
+    sched_mix<32, 12, 8>();
+    last_unit_reads();
+    sched_mix<32, 12, 0>();
+    read_a(1, 1);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
   // ---- first tile: stages 0 and 1 in flight, stage 0 read into VGPRs
   Tile cur{}, nxt{};  // nxt stays zero when no tile follows (its row loads then read nothing)
   if (!find_tile(0, cur)) return;
@@ -767,19 +787,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_pipe_kernel(GemmArgs p) {
       if (last && more) setup_dma(nxt);
       const int kdma = !last ? kt + 2 : (more ? 0 : ktiles - 1);
       set_read_slot(sb + kt + 1);
-      mfma_unit(0, 1, first);
-      read_a(0, 0);
-      issue_half(kdma, sb + kt + 2, 0);
-      sched_mix<32, 4, 8>();
-      mfma_unit(1, 0, false);
-      read_a(0, 1);
-      read_b(0);
-      issue_half(kdma, sb + kt + 2, 1);
-      sched_mix<32, 12, 8>();
-      last_unit_reads();
-      sched_mix<32, 12, 0>();
-      read_a(1, 1);
-      __builtin_amdgcn_sched_barrier(0);
+      step_body(first, kdma, sb + kt + 2);
     };
     // The first and the last step are peeled (with the last step inside the
     // loop as a uniform branch the SwiGLU kernel measured 7% slower at c5).
@@ -796,19 +804,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_pipe_kernel(GemmArgs p) {
     wait_lds();
     barrier();
     set_read_slot(sb + ktiles);
-    mfma_unit(0, 1, false);
-    read_a(0, 0);
-    issue_half(more ? 1 : ktiles - 1, sb + ktiles + 1, 0);
-    sched_mix<32, 4, 8>();
-    mfma_unit(1, 0, false);
-    read_a(0, 1);
-    read_b(0);
-    issue_half(more ? 1 : ktiles - 1, sb + ktiles + 1, 1);
-    sched_mix<32, 12, 8>();
-    last_unit_reads();
-    sched_mix<32, 12, 0>();
-    read_a(1, 1);
-    __builtin_amdgcn_sched_barrier(0);
+    step_body(false, more ? 1 : ktiles - 1, sb + ktiles + 1);
     epilogue(cur);
     __builtin_amdgcn_sched_barrier(0);
     if (!more) break;
