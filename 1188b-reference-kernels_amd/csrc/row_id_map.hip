@@ -25,7 +25,17 @@
 //      per wave store) and the token-major rows through an LDS transpose.
 // Every global load of a thread is independent of its other loads, so a block
 // waits for memory about once per phase rather than once per element.
+#include <mutex>
+
 #include "moe_common.h"
+
+// Scratch memory of moe_row_id_map_noalloc (the chunk counts and expert totals
+// of one call): a file-scope device array, one copy per GPU the library runs
+// on, held until the process ends.  Host code never passes this name to a
+// kernel: it stands for a host-side shadow; the device address comes from
+// hipGetSymbolAddress, once per device (noalloc_scratch below).
+constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;  // 8 MiB
+static __device__ __align__(256) int32_t scratch[kNoAllocScratchBytes / sizeof(int32_t)];
 
 namespace moe {
 namespace {
@@ -237,6 +247,29 @@ __global__ __launch_bounds__(kThreads) void rim_fill_kernel(const uint8_t *mask,
   }
 }
 
+// Device address of `scratch` on the current device, looked up on the first
+// call for that device (with it current) and cached.
+int noalloc_scratch(const char *fn, void **out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void *cache[kMaxDevices] = {};
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MOE_ERR_LAUNCH, "%s: hipGetDevice: %s", fn, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MOE_ERR_CAPACITY, "%s: device %d >= %d", fn, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(mu);
+  if (cache[dev] == nullptr) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      return fail(MOE_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) on device %d: %s", fn, dev, hipGetErrorString(e));
+    }
+    cache[dev] = p;
+  }
+  *out = cache[dev];
+  return MOE_OK;
+}
+
 }  // namespace
 }  // namespace moe
 
@@ -291,6 +324,35 @@ int moe_row_id_map(const uint8_t *routing_map, int64_t T, int64_t E, int64_t *ro
   rim_fill_kernel<<<chunk_grid, dim3(kThreads), 0, s>>>(routing_map, T, E, counts, totals, row_expert_major,
                                                        row_token_major, row_expert_major_i32, expert_offsets, vec);
   return check_launch("moe_row_id_map(fill)");
+}
+
+int moe_row_id_map_noalloc(const uint8_t *routing_map, int64_t T, int64_t E, int64_t *row_expert_major,
+                           int64_t *row_token_major, int32_t *row_expert_major_i32, int32_t *expert_offsets,
+                           void *stream) {
+  using namespace moe;
+  static const char *fn = "moe_row_id_map_noalloc";
+  if (T < 0 || E < 0) return fail(MOE_ERR_SHAPE, "%s: negative size (T=%lld E=%lld)", fn, (long long)T, (long long)E);
+  if (E > kMaxE) return fail(MOE_ERR_CAPACITY, "%s: E=%lld exceeds %d", fn, (long long)E, kMaxE);
+  if (T * E >= (int64_t(1) << 31)) {
+    return fail(MOE_ERR_CAPACITY, "%s: T*E=%lld must stay below 2^31 (int32 rows)", fn, (long long)(T * E));
+  }
+  const size_t need = moe_row_id_map_workspace_size(T, E);
+  if (need > kNoAllocScratchBytes) {
+    return fail(MOE_ERR_CAPACITY,
+                "%s: T=%lld E=%lld needs %zu bytes of scratch (ceil(T/64)*E + E int32 values + 256), the static "
+                "scratch holds %zu; use moe_row_id_map with a workspace",
+                fn, (long long)T, (long long)E, need, kNoAllocScratchBytes);
+  }
+  if (T * E == 0) {
+    return moe_row_id_map(routing_map, T, E, row_expert_major, row_token_major, row_expert_major_i32,
+                          expert_offsets, nullptr, 0, stream);
+  }
+  if (routing_map == nullptr) return fail(MOE_ERR_INVALID_ARG, "%s: null routing_map", fn);
+  void *ws = nullptr;
+  const int st = noalloc_scratch(fn, &ws);
+  if (st != MOE_OK) return st;
+  return moe_row_id_map(routing_map, T, E, row_expert_major, row_token_major, row_expert_major_i32, expert_offsets,
+                        ws, kNoAllocScratchBytes, stream);
 }
 
 }  // extern "C"

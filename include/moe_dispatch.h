@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define MOE_DISPATCH_ABI_VERSION 6
+#define MOE_DISPATCH_ABI_VERSION 7
 
 typedef uint16_t moe_bf16_t;
 
@@ -120,6 +120,23 @@ int moe_row_id_map(const uint8_t *routing_map, int64_t T, int64_t E, int64_t *ro
                    int64_t *row_token_major, int32_t *row_expert_major_i32,
                    int32_t *expert_offsets, void *workspace, size_t workspace_bytes,
                    void *stream);
+
+/* ---- a3': row-id map without a workspace (allocates nothing) -------------
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): moe_row_id_map with the same arguments and results, whose
+ * scratch (ceil(T/64)*E + E int32 values) lives in an 8 MiB device array the
+ * library holds per GPU until the process ends.
+ * Limit: moe_row_id_map_workspace_size(T, E) <= 8 MiB (e.g. T = 65536 at
+ *   E = 1024, T = 16384 at E = 4096), else MOE_ERR_CAPACITY; other limits as
+ *   moe_row_id_map.
+ * Every call on a GPU shares that GPU's scratch: calls that overlap on one GPU
+ * (on different streams or host threads) race; calls ordered on one stream do
+ * not.  Nothing in the scratch needs to start at zero. */
+int moe_row_id_map_noalloc(const uint8_t *routing_map, int64_t T, int64_t E,
+                           int64_t *row_expert_major, int64_t *row_token_major,
+                           int32_t *row_expert_major_i32, int32_t *expert_offsets,
+                           void *stream);
 
 /* ---- a4/a5: permute -----------------------------------------------------
  * Replaces case17 kernel_function(x, row_id_map, probs) -> (out, permuted_probs)

@@ -17,7 +17,7 @@ L = pkg._lib
 def test_library_loads_and_exports_header_symbols():
     lib = L.lib()
     declared = L.header_functions()
-    assert len(declared) == len(L.SIGNATURES) == 25
+    assert len(declared) == len(L.SIGNATURES) == 26
     assert set(declared) == set(L.SIGNATURES)
     for name in declared:
         assert hasattr(lib, name), name
@@ -55,6 +55,10 @@ FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
     ("moe_row_id_map", (FAKE, 16, 8000, None, None, None, None, None, 0, None), L.MOE_ERR_CAPACITY, "4096"),
     ("moe_row_id_map", (FAKE, 16, 8, None, None, None, None, None, 0, None), L.MOE_ERR_WORKSPACE, "workspace"),
     ("moe_row_id_map", (None, 16, 8, None, None, None, None, FAKE, 1 << 20, None), L.MOE_ERR_INVALID_ARG, "null"),
+    ("moe_row_id_map_noalloc", (FAKE, 1 << 18, 4096, None, None, None, None, None), L.MOE_ERR_CAPACITY, "scratch"),
+    ("moe_row_id_map_noalloc", (FAKE, 16, 8000, None, None, None, None, None), L.MOE_ERR_CAPACITY, "4096"),
+    ("moe_row_id_map_noalloc", (FAKE, -16, 8, None, None, None, None, None), L.MOE_ERR_SHAPE, "negative"),
+    ("moe_row_id_map_noalloc", (None, 16, 8, None, None, None, None, None), L.MOE_ERR_INVALID_ARG, "null"),
     ("moe_topk", (FAKE, 4, 16, 0, FAKE, FAKE, None, None, None), L.MOE_ERR_SHAPE, "out of range"),
     ("moe_topk", (FAKE, 4, 16, 17, FAKE, FAKE, None, None, None), L.MOE_ERR_SHAPE, "out of range"),
     ("moe_topk", (FAKE, 4, 2048, 8, FAKE, FAKE, None, None, None), L.MOE_ERR_CAPACITY, "1024"),
