@@ -6,16 +6,37 @@ import torch
 from .. import ops
 
 
-def num_out_from_map(row_id_map: torch.Tensor) -> int:
-    """max(row_id_map) + 1 (0 if no entry is >= 0): the reference functions' output row count.
+def scatter_rows(row_id_map: torch.Tensor) -> tuple[int, bool]:
+    """(num_out, dense): num_out = max(row_id_map) + 1 (0 if no entry is >= 0), the reference
+    functions' output row count, and whether the entries >= 0 are as many as num_out -- for a map
+    whose entries are distinct, as a row-id map's are, that they name every output row.
 
-    Reads one scalar back to the host, exactly where the reference does
+    One pair of scalars is read back to the host, exactly where the reference reads its max
     (kernel_cases/case21_ref_permute_with_mask_map_trans.py:64,
     kernel_results/case17_moe_permute_with_mask_map/binding.cpp:24).
     """
     if row_id_map.numel() == 0:
-        return 0
-    return max(int(row_id_map.max().item()) + 1, 0)
+        return 0, True
+    mx, cnt = torch.stack([row_id_map.max().to(torch.int64), (row_id_map >= 0).sum()]).tolist()
+    num_out = max(int(mx) + 1, 0)
+    return num_out, int(cnt) == num_out
+
+
+def permute_from_map(inp: torch.Tensor, row_id_map: torch.Tensor, probs, layout: str):
+    """The reference scatter with num_out = max(row_id_map) + 1 and zero-initialised outputs
+    (new_zeros, kernel_cases/case22_ref_moe_permute_mask_kernel_true.py:63-67): a dense map
+    writes every row, so the outputs are not cleared first; any other map gets zeroed outputs,
+    so the rows no entry names stay zero.  Returns (out, permuted_probs or None)."""
+    num_out, dense = scatter_rows(row_id_map)
+    if num_out == 0:
+        return inp.new_empty((0, inp.shape[1])), (None if probs is None else probs.new_empty((0,), dtype=torch.float32))
+    out = pp = None
+    if not dense:
+        out = torch.zeros(num_out, inp.shape[1], dtype=inp.dtype, device=inp.device)
+        if probs is not None:
+            pp = torch.zeros(num_out, dtype=torch.float32, device=inp.device)
+    return ops.permute(inp, row_id_map, probs, num_out=num_out, layout=layout, zero_tail=False, out=out,
+                       permuted_probs=pp)
 
 
 def expert_major_map(selected_em: torch.Tensor, dtype=torch.int64, device="cuda") -> torch.Tensor:

@@ -3,6 +3,13 @@
 Drop-in for kernel_results/case06_cp_seq_chunk_index_select/kernel.py:4-7
 (`kernel_function(k_ag, v_ag, index) -> (index_select(k_ag,0,index), index_select(v_ag,0,index))`),
 math kernel_cases/case06_cp_seq_chunk_index_select.py:38-40, generator :47-52.
+
+Out-of-range indices: torch.index_select (the case's Model) raises, and the
+optimized bundle reads whatever memory the index points at (no bounds check,
+kernel_results/case06_cp_seq_chunk_index_select/kernel.mu:9).  Here an index
+outside [0, rows) gives a zero row: the kernel never reads out of bounds, and a
+caller that needs the exception checks the index on the host first (one
+min/max read, which the drop-in does not pay on every call).
 """
 from __future__ import annotations
 

@@ -10,7 +10,7 @@ beyond the routed count are zero, as the Model's new_zeros leaves them.
 from __future__ import annotations
 
 from .. import inputs, ops
-from ._common import num_out_from_map
+from ._common import permute_from_map
 
 TOKENS = 16384
 HID = 8192
@@ -49,12 +49,11 @@ def kernel_function(x, row_id_map, probs, num_out=None):
         raise RuntimeError("row_id_map must be [T,E]")
     if row_id_map.size(0) != x.size(0):
         raise RuntimeError("map/probs token dim mismatch")
-    zero_tail = num_out is not None
     if num_out is None:
-        num_out = num_out_from_map(row_id_map)
-    out, pp = ops.permute(x, row_id_map, probs.float(), num_out=num_out, layout=ops.TOKEN_MAJOR,
-                          zero_tail=zero_tail)
-    return out, pp
+        return permute_from_map(x, row_id_map, probs.float(), ops.TOKEN_MAJOR)
+    # num_out from the Model: no host read; the map is a row-id map (dense over its R rows),
+    # and rows R..num_out-1 are zero-filled on the device.
+    return ops.permute(x, row_id_map, probs.float(), num_out=num_out, layout=ops.TOKEN_MAJOR, zero_tail=True)
 
 
 class Model:

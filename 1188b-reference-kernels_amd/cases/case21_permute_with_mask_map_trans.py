@@ -10,7 +10,7 @@ from __future__ import annotations
 import torch
 
 from .. import inputs, ops
-from ._common import check_scatter_shapes, expert_major_map, num_out_from_map
+from ._common import check_scatter_shapes, expert_major_map, permute_from_map
 
 M = 16384
 HIDDEN = 8192
@@ -21,10 +21,7 @@ TOPK = 8
 def permute_with_mask_map_trans(inp: torch.Tensor, row_id_map: torch.Tensor) -> torch.Tensor:
     """Scatter inp[token] to output[row_id_map[expert, token]] when the id is not -1."""
     check_scatter_shapes(inp, row_id_map)
-    num_out = num_out_from_map(row_id_map)
-    if num_out == 0:
-        return inp.new_empty((0, inp.shape[1]))
-    out, _ = ops.permute(inp, row_id_map, num_out=num_out, layout=ops.EXPERT_MAJOR, zero_tail=True)
+    out, _ = permute_from_map(inp, row_id_map, None, ops.EXPERT_MAJOR)
     return out
 
 

@@ -10,7 +10,7 @@ from __future__ import annotations
 import torch
 
 from .. import inputs, ops
-from ._common import check_scatter_shapes, expert_major_map, num_out_from_map
+from ._common import check_scatter_shapes, expert_major_map, permute_from_map
 
 M = 16384
 HIDDEN = 8192
@@ -24,10 +24,7 @@ def permute_mask_with_probs(inp: torch.Tensor, row_id_map: torch.Tensor, probs: 
     experts, tokens = row_id_map.shape
     if probs.shape != (tokens, experts):
         raise ValueError(f"probs {tuple(probs.shape)} expected {(tokens, experts)}")
-    num_out = num_out_from_map(row_id_map)
-    if num_out == 0:
-        return inp.new_empty((0, inp.shape[1])), probs.new_empty((0,))
-    return ops.permute(inp, row_id_map, probs, num_out=num_out, layout=ops.EXPERT_MAJOR, zero_tail=True)
+    return permute_from_map(inp, row_id_map, probs, ops.EXPERT_MAJOR)
 
 
 def make_row_id_map(num_tokens: int = M, num_experts: int = NUM_EXPERTS, topk: int = TOPK, device="cuda"):

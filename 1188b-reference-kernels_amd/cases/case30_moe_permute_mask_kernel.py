@@ -9,7 +9,7 @@ from __future__ import annotations
 import torch
 
 from .. import inputs, ops
-from ._common import check_scatter_shapes, expert_major_map, num_out_from_map
+from ._common import check_scatter_shapes, expert_major_map, permute_from_map
 
 M = 16384
 HIDDEN = 8192
@@ -19,10 +19,7 @@ TOPK = 8
 
 def permute_mask(grad: torch.Tensor, row_id_map: torch.Tensor) -> torch.Tensor:
     check_scatter_shapes(grad, row_id_map)
-    num_out = num_out_from_map(row_id_map)
-    if num_out == 0:
-        return grad.new_empty((0, grad.shape[1]))
-    out, _ = ops.permute(grad, row_id_map, num_out=num_out, layout=ops.EXPERT_MAJOR, zero_tail=True)
+    out, _ = permute_from_map(grad, row_id_map, None, ops.EXPERT_MAJOR)
     return out
 
 

@@ -42,6 +42,8 @@ namespace moe {
 namespace {
 
 constexpr int kMaxThreads = 1024;
+constexpr int kMaxE = 4096;                 // the row-id map's limit
+constexpr size_t kMaxLds = 160 * 1024;      // gfx950 LDS per workgroup
 constexpr int kMaxWavesPerToken = kMaxThreads / kWave;
 constexpr int kBatch = 8;
 
@@ -262,7 +264,7 @@ int common_checks(const char *fn, const void *pin, int64_t R, int64_t H, const v
     return fail(MOE_ERR_SHAPE, "%s: negative size (R=%lld H=%lld E=%lld T=%lld)", fn, (long long)R,
                 (long long)H, (long long)E, (long long)T);
   }
-  if (E > 1024) return fail(MOE_ERR_CAPACITY, "%s: E=%lld exceeds 1024 experts", fn, (long long)E);
+  if (E > kMaxE) return fail(MOE_ERR_CAPACITY, "%s: E=%lld exceeds %d experts", fn, (long long)E, kMaxE);
   if (idx_dtype != MOE_IDX_I32 && idx_dtype != MOE_IDX_I64) {
     return fail(MOE_ERR_INVALID_ARG, "%s: idx_dtype %d is not MOE_IDX_I32/I64", fn, idx_dtype);
   }
@@ -282,7 +284,13 @@ int64_t shape_launch(UnpermuteArgs &a, bool vec) {
   a.waves_per_token = sh.waves_per_token;
   a.tokens_per_block = sh.tokens_per_block;
   a.nchunks = static_cast<int>(ceil_div(a.E, kWave));
-  return ceil_div(a.T, static_cast<int64_t>(sh.tokens_per_block));
+  // Staged map entries of every token of a workgroup must fit the LDS (49 KiB per token
+  // at E = 4096): fewer tokens per workgroup for short rows with many experts.
+  while (a.tokens_per_block > 1 && a.nchunks > 1 &&
+         a.tokens_per_block * lds_bytes_per_token(a.nchunks, true) > kMaxLds) {
+    a.tokens_per_block /= 2;
+  }
+  return ceil_div(a.T, static_cast<int64_t>(a.tokens_per_block));
 }
 
 }  // namespace

@@ -21,8 +21,10 @@ Data layout in HBM (T tokens, H hidden, F ffn, E experts, k top-k, R = T*k):
   out      bf16 [T, H]        sum_e probs[t, e] * z[row_map[t, e]]  (fp32, ascending e)
   W1       bf16 [E, 2F, H]    gate rows [0, F), up rows [F, 2F)  (out x in)
   W2       bf16 [E, H, F]
-Every buffer is allocated once per shape and reused; no host synchronisation
-happens inside forward() (R = T * k is known on the host).
+The intermediates (src, h, z, the row-id-map workspace) are allocated once per
+token count and reused by later calls; the output is a new tensor on every call
+(or the caller's `out=`), so a result stays valid across later forward() calls.
+No host synchronisation happens inside forward() (R = T * k is known on the host).
 """
 from __future__ import annotations
 
@@ -56,7 +58,6 @@ class MoEFFN:
                 "src": torch.empty(R, dtype=torch.int32, device=device),
                 "h": torch.empty(R, self.F, **bf),
                 "z": torch.empty(R, self.H, **bf),
-                "out": torch.empty(T, self.H, **bf),
                 "ws": torch.empty(ops._lib.lib().moe_row_id_map_workspace_size(T, self.E), dtype=torch.uint8,
                                   device=device),
             }
@@ -69,11 +70,14 @@ class MoEFFN:
                               workspace=self._buffers(logits.shape[0], logits.device)["ws"])
         return mask, probs, maps["token_major"], maps["expert_offsets"]
 
-    def forward(self, x: torch.Tensor, logits: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, logits: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
+        """out [T, H] bf16 for x [T, H] and router logits [T, E]; `out` may be given (contiguous bf16 [T, H])."""
         T = x.shape[0]
         if logits.shape != (T, self.E):
             raise ValueError(f"logits {tuple(logits.shape)} expected {(T, self.E)}")
         b = self._buffers(T, x.device)
+        if out is None:
+            out = torch.empty(T, self.H, dtype=torch.bfloat16, device=x.device)
         mask, probs, row_map, offsets = self.route(logits)
         if self.fused_permute:
             # every permuted row is named by the map (R = T * k), so no -1 fill is needed
@@ -83,8 +87,8 @@ class MoEFFN:
             ops.permute(x, row_map, num_out=T * self.k, layout=ops.TOKEN_MAJOR, zero_tail=False, out=b["xp"])
             ops.grouped_gemm(b["xp"], self.w1, offsets, swiglu=True, out=b["h"])
         ops.grouped_gemm(b["h"], self.w2, offsets, out=b["z"])
-        ops.unpermute(b["z"], row_map, probs, layout=ops.TOKEN_MAJOR, out=b["out"])
+        ops.unpermute(b["z"], row_map, probs, layout=ops.TOKEN_MAJOR, out=out)
         self.last = {"mask": mask, "probs": probs, "row_map": row_map, "offsets": offsets}
-        return b["out"]
+        return out
 
     __call__ = forward

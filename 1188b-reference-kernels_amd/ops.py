@@ -237,8 +237,11 @@ def permute(x: torch.Tensor, row_id_map: torch.Tensor, probs: Optional[torch.Ten
     """out[map(t,e)] = x[t]; permuted_probs[map(t,e)] = probs[t,e] for map >= 0.
 
     Rows of `out` at index >= R (R = number of entries >= 0) are zero when
-    `zero_tail` (the reference's new_zeros); pass zero_tail=False when num_out
-    is known to equal R.  Returns (out, permuted_probs or None).
+    `zero_tail` (the reference's new_zeros); that assumes the entries name the
+    rows 0..R-1, as a row-id map's do -- for other maps pass zeroed `out` /
+    `permuted_probs` and zero_tail=False (rows no entry names are left as they
+    are).  Pass zero_tail=False when num_out is known to equal R.
+    Returns (out, permuted_probs or None).
     """
     _on_gpu("x", x)
     _on_gpu("row_id_map", row_id_map)

@@ -149,9 +149,12 @@ int moe_row_id_map_noalloc(const uint8_t *routing_map, int64_t T, int64_t E,
  *   out   bf16 [num_out, H]; permuted_probs fp32 [num_out] (nullable)
  * zero_tail != 0: rows of out / permuted_probs at index >= R (R = number of
  *   map entries >= 0) are zero-filled, matching the reference's new_zeros
- *   when num_out exceeds R.  Needs moe_permute_workspace_size(T) bytes of
- *   workspace; with zero_tail == 0 the workspace may be NULL and num_out is
- *   expected to equal R (the usual case: R = T * topk).
+ *   when num_out exceeds R.  This assumes the entries >= 0 name exactly the
+ *   rows 0..R-1 (a map built by moe_row_id_map does); for any other map the
+ *   caller zeroes out / permuted_probs first and passes zero_tail == 0 (the
+ *   case21/22/30 drop-ins do, after reading max and count of the map).  Needs
+ *   moe_permute_workspace_size(T) bytes of workspace; with zero_tail == 0 the
+ *   workspace may be NULL and rows no entry names are left untouched.
  * Map entries >= num_out are skipped. */
 size_t moe_permute_workspace_size(int64_t T);
 int moe_permute(const moe_bf16_t *x, int64_t T, int64_t H, const void *row_id_map, int idx_dtype,
@@ -183,7 +186,7 @@ int moe_permute_index(const void *row_id_map, int idx_dtype, int map_layout, int
  *   pin bf16 [R, H]; merge_probs fp32 [T, E] (nullable); out bf16 [T, H];
  *   out_acc (nullable) fp32 [T, H]: the fp32 sums before rounding (the int32
  *   reference reference_unpermute_mask returns them, case24...py:66-68).
- * Map entries >= R are skipped. */
+ * Map entries >= R are skipped.  Limits: E <= 4096 (as moe_row_id_map). */
 int moe_unpermute(const moe_bf16_t *pin, int64_t R, int64_t H, const void *row_id_map,
                   int idx_dtype, int map_layout, int64_t E, int64_t T, const float *merge_probs,
                   moe_bf16_t *out, float *out_acc, void *stream);
@@ -195,7 +198,8 @@ int moe_unpermute(const moe_bf16_t *pin, int64_t R, int64_t H, const void *row_i
  *   dact[t]      = bf16_rne( sum_e ascending float(dperm_act[map(t, e)]) )
  *   dprobs[t, e] = dpp[map(t, e)] if map(t, e) >= 0 else 0
  *   dperm_act bf16 [R, H]; dpp fp32 [R]; dact bf16 [T, H]; dprobs fp32 [T, E];
- *   out_acc (nullable) fp32 [T, H]: the fp32 sums (case32...py:74-76 returns them). */
+ *   out_acc (nullable) fp32 [T, H]: the fp32 sums (case32...py:74-76 returns them).
+ * Limits: E <= 4096 (as moe_row_id_map). */
 int moe_permute_bwd(const moe_bf16_t *dperm_act, int64_t R, int64_t H, const float *dpp,
                     const void *row_id_map, int idx_dtype, int map_layout, int64_t E, int64_t T,
                     moe_bf16_t *dact, float *dprobs, float *out_acc, void *stream);

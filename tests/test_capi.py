@@ -49,7 +49,7 @@ FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
     ("moe_permute", (None, 4, 8, FAKE, 1, 0, 4, None, FAKE, None, 16, 0, None, 0, None), L.MOE_ERR_INVALID_ARG, "null"),
     ("moe_permute", (FAKE, 4, 8, FAKE, 1, 0, 4, None, FAKE, FAKE, 16, 0, None, 0, None), L.MOE_ERR_INVALID_ARG, "without probs"),
     ("moe_permute", (FAKE, 4, 8, FAKE, 1, 0, 4, None, FAKE, None, 16, 1, None, 0, None), L.MOE_ERR_WORKSPACE, "workspace"),
-    ("moe_unpermute", (FAKE, 8, 8, FAKE, 1, 1, 2000, 4, None, FAKE, None, None), L.MOE_ERR_CAPACITY, "1024"),
+    ("moe_unpermute", (FAKE, 8, 8, FAKE, 1, 1, 5000, 4, None, FAKE, None, None), L.MOE_ERR_CAPACITY, "4096"),
     ("moe_unpermute", (FAKE, 8, -8, FAKE, 1, 1, 4, 4, None, FAKE, None, None), L.MOE_ERR_SHAPE, "negative"),
     ("moe_permute_bwd", (FAKE, 8, 8, None, FAKE, 1, 1, 4, 4, FAKE, FAKE, None, None), L.MOE_ERR_INVALID_ARG, "dpp"),
     ("moe_row_id_map", (FAKE, 16, 8000, None, None, None, None, None, 0, None), L.MOE_ERR_CAPACITY, "4096"),

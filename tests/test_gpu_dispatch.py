@@ -151,6 +151,56 @@ def test_permute_with_probs_case22(pkg, dev):
     assert_bits_equal(pp, ref_pp, "case22 pp")
 
 
+def _padded_expert_major_map(T, E, k, pad, seed):
+    """Expert-major map whose experts start at multiples of `pad` rows (a capacity-padded layout):
+    the rows between one expert's last token and the next expert's first are named by no entry."""
+    g = torch.Generator().manual_seed(seed)
+    mask = torch.zeros(T, E, dtype=torch.bool).scatter_(1, torch.rand(T, E, generator=g).topk(k, 1).indices, True)
+    m = torch.full((E, T), -1, dtype=torch.int64)
+    base = 0
+    for e in range(E):
+        toks = mask[:, e].nonzero().squeeze(1)
+        m[e, toks] = base + torch.arange(toks.numel())
+        base += (toks.numel() + pad - 1) // pad * pad if toks.numel() else pad
+    return m
+
+
+@pytest.mark.parametrize("mod,fn,probs", [("case21_permute_with_mask_map_trans", "permute_with_mask_map_trans", False),
+                                          ("case30_moe_permute_mask_kernel", "permute_mask", False),
+                                          ("case22_moe_permute_mask_kernel_true", "permute_mask_with_probs", True)])
+def test_permute_sparse_maps_zero_the_unnamed_rows(pkg, dev, mod, fn, probs):
+    # Maps that do not name every row below their max: a capacity-padded expert-major layout
+    # and a hand-made one with holes. The unnamed rows are zero, as the reference's new_zeros
+    # leaves them (kernel_cases/case22_ref_moe_permute_mask_kernel_true.py:63-67).
+    case = getattr(pkg.cases, mod)
+    g = torch.Generator().manual_seed(9)
+    for m in (_padded_expert_major_map(300, 12, 3, pad=64, seed=4),
+              torch.tensor([[0, -1, 5], [-1, 2, -1]], dtype=torch.int64)):
+        E, T = m.shape
+        inp = torch.randn(T, 136, generator=g).to(torch.bfloat16)
+        pr = torch.rand(T, E, generator=g) * (m >= 0).t()
+        # the destination buffers first hold garbage, so stale rows would show
+        torch.empty(4 << 20, dtype=torch.uint8, device=dev).fill_(0x7F)
+        if probs:
+            out, pp = getattr(case, fn)(inp.to(dev), m.to(dev), pr.to(dev))
+            ref_out, ref_pp = ref_torch.permute_expert_major(inp, m, pr)
+            assert_bits_equal(pp, ref_pp, f"{mod} permuted probs")
+        else:
+            out = getattr(case, fn)(inp.to(dev), m.to(dev))
+            ref_out = ref_torch.permute_expert_major(inp, m)
+        assert_bits_equal(out, ref_out, f"{mod} out")
+        assert int(m.max()) + 1 > int((m >= 0).sum()), "the map has unnamed rows"
+    # case17 without num_out derives R = max + 1 the same way (token-major map)
+    m = _padded_expert_major_map(200, 8, 2, pad=32, seed=5)
+    x = torch.randn(200, 64, generator=g).to(torch.bfloat16)
+    pr = torch.rand(200, 8, generator=g)
+    tm = m.t().contiguous()
+    out, pp = pkg.cases.case17_moe_permute_with_mask_map.kernel_function(x.to(dev), tm.to(dev), pr.to(dev))
+    ref_out, ref_pp = ref_torch.permute_token_major(x, tm, pr * (tm >= 0), int(m.max()) + 1)
+    assert_bits_equal(out, ref_out, "case17 sparse out")
+    assert_bits_equal(pp, ref_pp, "case17 sparse pp")
+
+
 def test_permute_known_answer_on_gpu(pkg, dev):
     inp = (torch.arange(8, dtype=torch.bfloat16).reshape(2, 4) + 1).to(dev)
     m = torch.tensor([[0, -1], [-1, 2], [1, -1], [-1, -1]], dtype=torch.int64, device=dev)
@@ -173,10 +223,12 @@ def _wide(R, H, seed):
 # Shapes cover both launch forms: one wavefront per 1 KiB slice of the row (up to
 # 16 per token) and 4 tokens per workgroup for short rows (with a partial last
 # workgroup), each with the map read per wavefront (E <= 64) or staged in LDS
-# (E > 64, including a partial last 64-expert chunk and E = 1024), plus the
-# scalar path for rows that are not a multiple of 8 elements.
+# (E > 64, including a partial last 64-expert chunk, E = 1024, and E up to the
+# row-id map's 4096, where short rows put fewer tokens in a workgroup so the staged
+# entries fit the LDS), plus the scalar path for rows that are not a multiple of 8.
 @pytest.mark.parametrize("T,E,k,H", [(257, 8, 2, 2048), (96, 64, 8, 7168), (40, 320, 6, 72), (21, 9, 4, 11),
-                                     (43, 130, 3, 24), (29, 200, 5, 13), (33, 1024, 8, 4096)])
+                                     (43, 130, 3, 24), (29, 200, 5, 13), (33, 1024, 8, 4096),
+                                     (19, 2000, 7, 40), (13, 4096, 9, 16), (11, 4096, 3, 1000)])
 def test_unpermute_matches_oracle(pkg, dev, layout, idx, merge, T, E, k, H):
     rm = _mask(T, E, k, seed=T + 7 * E)
     em, tm = ref_torch.row_id_map(rm)
@@ -232,7 +284,7 @@ def test_unpermute_cases_24_32_modular(pkg, dev):
 
 # -------------------------------------------------------------- permute bwd
 @pytest.mark.parametrize("T,E,k,H", [(512, 320, 8, 1024), (200, 64, 8, 7168), (37, 6, 2, 20), (19, 130, 4, 40),
-                                     (23, 100, 3, 9)])
+                                     (23, 100, 3, 9), (17, 4096, 5, 24)])
 def test_permute_bwd_matches_oracle(pkg, dev, T, E, k, H):
     rm = _mask(T, E, k, seed=11 * T)
     em, _ = ref_torch.row_id_map(rm)
