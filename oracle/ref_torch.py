@@ -382,3 +382,26 @@ def moe_ffn_forward(x: torch.Tensor, logits: torch.Tensor, w1: torch.Tensor, w2:
     h = swiglu(y).to(torch.bfloat16)
     z = grouped_gemm(h, w2, sizes)
     return unpermute_merge(z, row_em, probs)
+
+
+def moe_ffn_forward_fp32(x: torch.Tensor, logits: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, topk_k: int):
+    """moe_ffn_forward with fp32-accumulated GEMMs (the golden of the bf16 tolerance checks).
+
+    Same chain as moe_ffn_forward, each grouped GEMM as grouped_gemm_fp32
+    (kernel_cases/case35_ref_musa_asm_bf16_gemm_nt_256x384.py:41-48 per group of
+    kernel_cases/case03_moe_grouped_gemm_fc1_fwd.py:57-64 and case04...:57-64),
+    rounded to bf16 where the layer stores its intermediates: h after SwiGLU
+    and z after fc2; then the merge of unpermute_merge.  Every output row
+    depends only on its own token, so a subset of tokens gives those tokens'
+    rows of the full layer.
+    """
+    E = logits.shape[1]
+    values, indices = topk(logits, topk_k)
+    rm, probs = mask_and_probs(values, indices, E)
+    row_em, row_tm = row_id_map(rm)
+    R = int(rm.sum())
+    xp, _ = permute_token_major(x, row_tm, probs, R)
+    sizes = rm.sum(dim=0).tolist()
+    h = swiglu(grouped_gemm_fp32(xp, w1, sizes)).to(torch.bfloat16)
+    z = grouped_gemm_fp32(h, w2, sizes).to(torch.bfloat16)
+    return unpermute_merge(z, row_em, probs)

@@ -61,27 +61,45 @@ def test_config_c2_round_trip_and_merge(pkg, dev):
     for e in (0, E // 2, E - 1):
         toks = mask[:, e].nonzero().squeeze(1)
         assert torch.equal(xp[int(offs[e]):int(offs[e + 1])], x[toks])
-    # Merge with probs summing to 1: within bf16 rounding of x; bit-exact vs the oracle on a slice.
+    # Merge with probs summing to 1: within bf16 rounding of x; bit-exact vs the oracle on every token
+    # (the oracle runs on the host in chunks of 1024 tokens; each token's sum depends on its own map column).
     merged = pkg.ops.unpermute(xp, maps["token_major"], probs, layout="token_major")
     torch.testing.assert_close(merged.float(), x.float(), rtol=1.6e-2, atol=1e-2)
-    sl = slice(0, 512)
-    em_slice = maps["expert_major"][:, sl].cpu()
-    rows = em_slice[em_slice >= 0]
-    ref = ref_torch.unpermute_merge(xp.cpu(), maps["expert_major"][:, sl].cpu(), probs[sl].cpu())
-    assert rows.numel() == 512 * k
-    assert_bits_equal(merged[sl], ref, "c2 merge slice")
-    # Permute backward with the seeded grad: dact equals the oracle on the same slice.
+    xp_c, em_c, probs_c, merged_c = xp.cpu(), maps["expert_major"].cpu(), probs.cpu(), merged.cpu()
+    # Permute backward with the seeded grad: dact and dprobs equal the oracle on every token.
     grad = pkg.inputs.randn_bf16((T * k, H), seed=20261212, device=dev)
     dpp = torch.randn(T * k, generator=torch.Generator(device=dev).manual_seed(5), device=dev)
     dact, dprobs = pkg.ops.permute_bwd(grad, dpp, maps["expert_major"], layout="expert_major")
-    ref_dact, ref_dprobs = ref_torch.permute_bwd(grad.cpu(), dpp.cpu(), maps["expert_major"][:, sl].cpu())
-    assert_bits_equal(dact[sl], ref_dact, "c2 dact slice")
-    assert_bits_equal(dprobs[sl], ref_dprobs, "c2 dprobs slice")
+    grad_c, dpp_c, dact_c, dprobs_c = grad.cpu(), dpp.cpu(), dact.cpu(), dprobs.cpu()
+    for t0 in range(0, T, 1024):
+        sl = slice(t0, t0 + 1024)
+        ref = ref_torch.unpermute_merge(xp_c, em_c[:, sl], probs_c[sl])
+        assert_bits_equal(merged_c[sl], ref, f"c2 merge tokens {t0}..")
+        ref_dact, ref_dprobs = ref_torch.permute_bwd(grad_c, dpp_c, em_c[:, sl])
+        assert_bits_equal(dact_c[sl], ref_dact, f"c2 dact tokens {t0}..")
+        assert_bits_equal(dprobs_c[sl], ref_dprobs, f"c2 dprobs tokens {t0}..")
 
 
-def test_config_c5_layer_properties(pkg, dev):
-    # c5 full layer: run once; routing is checked exactly against the oracle, the output
-    # on a token sample against an fp32 recomputation of those tokens.
+def _c5_sample(mask: torch.Tensor, n: int, seed: int) -> torch.Tensor:
+    """n token ids: the first and the last token of every expert's group (its rows in the
+    permuted order start and end there), the rest drawn at random."""
+    picks = set()
+    for e in range(mask.shape[1]):
+        toks = mask[:, e].nonzero().squeeze(1)
+        if toks.numel():
+            picks.update((int(toks[0]), int(toks[-1])))
+    g = torch.Generator().manual_seed(seed)
+    for t in torch.randperm(mask.shape[0], generator=g).tolist():
+        if len(picks) >= n:
+            break
+        picks.add(t)
+    return torch.tensor(sorted(picks))
+
+
+def test_config_c5_layer_matches_oracle(pkg, dev):
+    # c5 full layer: routing exact against the oracle; the output of 1024 tokens (covering
+    # both group ends of every expert the skewed router gives tokens) against the oracle's fp32-GEMM layer
+    # recomputed on the host for those tokens, at the task's bf16 tolerance.
     c = pkg.inputs.CONFIGS["c5"]
     T, H, E, k, F = c["tokens"], c["hidden"], c["experts"], c["topk"], c["ffn"]
     x = pkg.inputs.randn_bf16((T, H), seed=20261205, device=dev)
@@ -90,16 +108,36 @@ def test_config_c5_layer_properties(pkg, dev):
     w2 = pkg.inputs.randn_bf16((E, H, F), std=0.02, seed=20261225, device=dev)
     layer = pkg.moe_ffn.MoEFFN(w1, w2, k)
     out = layer(x, logits)
-    v, i = ref_torch.topk(logits.cpu(), k)
+    logits_c = logits.cpu()
+    v, i = ref_torch.topk(logits_c, k)
     rm, _ = ref_torch.mask_and_probs(v, i, E)
     assert torch.equal(layer.last["mask"].cpu(), rm)
     _, tm = ref_torch.row_id_map(rm)
     assert torch.equal(layer.last["row_map"].cpu(), tm)
-    probs = layer.last["probs"]
-    for t in (0, 1, T // 2, T - 1):
-        acc = torch.zeros(H, device=dev)
-        for e in sorted(i[t].tolist()):
-            y = x[t:t + 1].float() @ w1[e].float().t()
-            hh = ref_torch.swiglu(y).to(torch.bfloat16).float()
-            acc += probs[t, e] * (hh @ w2[e].float().t())[0]
-        torch.testing.assert_close(out[t].float(), acc, rtol=2e-2, atol=2e-2)
+    sample = _c5_sample(rm, 1024, seed=5)
+    used = rm.any(0)
+    assert sample.numel() == 1024 and torch.equal(rm[sample].any(0), used), "every expert with tokens is covered"
+    assert int(used.sum()) >= E // 2
+    ref = ref_torch.moe_ffn_forward_fp32(x.cpu()[sample], logits_c[sample], w1.cpu(), w2.cpu(), k)
+    torch.testing.assert_close(out.cpu()[sample].float(), ref.float(), rtol=1.6e-2, atol=1e-2)
+
+
+def test_moe_ffn_output_survives_a_second_call(pkg, dev):
+    # Each forward returns a new tensor (or the caller's out=): a second call with other
+    # inputs leaves the first result untouched.
+    g = torch.Generator().manual_seed(13)
+    T, H, F, E, k = 256, 256, 128, 8, 2
+    w1 = (torch.randn(E, 2 * F, H, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    w2 = (torch.randn(E, H, F, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    layer = pkg.moe_ffn.MoEFFN(w1, w2, k)
+    x1, x2 = (torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev) for _ in range(2))
+    l1, l2 = (torch.randn(T, E, generator=g).to(dev) for _ in range(2))
+    y1 = layer(x1, l1)
+    y1_copy = y1.clone()
+    y2 = layer(x2, l2)
+    torch.cuda.synchronize()
+    assert y1.data_ptr() != y2.data_ptr()
+    assert torch.equal(y1, y1_copy)
+    out = torch.empty_like(y1)
+    assert layer(x1, l1, out=out) is out
+    assert torch.equal(out, y1_copy)

@@ -424,3 +424,28 @@ def test_moe_ffn_composition_tiny():
             acc = acc + probs[t, e] * z
         expect[t] = acc
     torch.testing.assert_close(out.float(), expect, rtol=2e-2, atol=2e-2)
+
+
+def test_moe_ffn_fp32_composition_against_float64_brute_force():
+    # The fp32-GEMM layer oracle equals a per-token float64 loop (bf16 roundings of h and z at the
+    # same points), and a subset of tokens gives those tokens' rows of the full layer.
+    g = torch.Generator().manual_seed(73)
+    T, H, F, E, k = 23, 16, 8, 6, 3
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    logits = torch.randn(T, E, generator=g) + torch.randn(E, generator=g) * 1.5
+    w1 = (torch.randn(E, 2 * F, H, generator=g) * 0.5).to(torch.bfloat16)
+    w2 = (torch.randn(E, H, F, generator=g) * 0.5).to(torch.bfloat16)
+    out = ref_torch.moe_ffn_forward_fp32(x, logits, w1, w2, k)
+    v, i = ref_torch.topk(logits, k)
+    _, probs = ref_torch.mask_and_probs(v, i, E)
+    expect = torch.zeros(T, H, dtype=torch.float64)
+    for t in range(T):
+        for e in sorted(i[t].tolist()):
+            y = x[t].double() @ w1[e].double().t()
+            gate, up = y[:F], y[F:]
+            hh = (gate * torch.sigmoid(gate) * up).to(torch.bfloat16)
+            z = (hh.double() @ w2[e].double().t()).to(torch.bfloat16)
+            expect[t] += probs[t, e].double() * z.double()
+    torch.testing.assert_close(out.double(), expect, rtol=1e-2, atol=1e-2)
+    sub = torch.tensor([0, 5, 17, 22])
+    assert torch.equal(ref_torch.moe_ffn_forward_fp32(x[sub], logits[sub], w1, w2, k), out[sub])
