@@ -35,7 +35,7 @@ MOE_MAP_EXPERT_MAJOR = 1
 MOE_EPILOGUE_NONE = 0
 MOE_EPILOGUE_SWIGLU = 1
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -49,8 +49,8 @@ SIGNATURES = {
     "moe_last_error": (ctypes.c_char_p, []),
     "moe_topk": (_int, [_p, _i64, _i64, _i64, _p, _p, _p, _p, _p]),
     "moe_row_id_map_workspace_size": (_sz, [_i64, _i64]),
-    "moe_row_id_map": (_int, [_p, _i64, _i64, _p, _p, _p, _p, _p, _sz, _p]),
-    "moe_row_id_map_noalloc": (_int, [_p, _i64, _i64, _p, _p, _p, _p, _p]),
+    "moe_row_id_map": (_int, [_p, _i64, _i64, _p, _p, _p, _p, _p, _i64, _p, _sz, _p]),
+    "moe_row_id_map_noalloc": (_int, [_p, _i64, _i64, _p, _p, _p, _p, _p, _i64, _p]),
     "moe_permute_workspace_size": (_sz, [_i64]),
     "moe_permute": (_int, [_p, _i64, _i64, _p, _int, _int, _i64, _p, _p, _p, _i64, _int, _p, _sz, _p]),
     "moe_unpermute": (_int, [_p, _i64, _i64, _p, _int, _int, _i64, _i64, _p, _p, _p, _p]),

@@ -12,7 +12,8 @@ Data layout in HBM (T tokens, H hidden, F ffn, E experts, k top-k, R = T*k):
   probs    fp32 [T, E]        softmax over the k selected logits, 0 elsewhere
   row_map  int64 [T, E]       token-major destination row, -1 if unselected
   offsets  int32 [E + 1]      first permuted row of each expert; offsets[E] = R
-  src      int32 [R]          source token of each permuted row (inverse of row_map)
+  src      int32 [R]          source token of each permuted row (inverse of row_map; written
+                              by the row-id map's fill pass)
   xp       bf16 [R, H]        permuted rows x[src], expert-major (expert e = rows offsets[e]..);
                               only materialised with fused_permute=False — by default fc1
                               gathers its A rows from x through src (moe_grouped_gemm_gather)
@@ -64,10 +65,12 @@ class MoEFFN:
         return self._bufs
 
     def route(self, logits: torch.Tensor):
-        """(mask, probs, token-major row map, expert offsets) for router logits [T, E]."""
+        """(mask, probs, token-major row map, expert offsets) for router logits [T, E]; the
+        source token of every permuted row lands in the cached `src` buffer."""
+        b = self._buffers(logits.shape[0], logits.device)
         _, _, mask, probs = ops.topk(logits, self.k, with_mask=True, with_probs=True)
-        maps = ops.row_id_map(mask, expert_major=False, token_major=True, expert_offsets=True,
-                              workspace=self._buffers(logits.shape[0], logits.device)["ws"])
+        maps = ops.row_id_map(mask, expert_major=False, token_major=True, expert_offsets=True, src_out=b["src"],
+                              workspace=b["ws"])
         return mask, probs, maps["token_major"], maps["expert_offsets"]
 
     def forward(self, x: torch.Tensor, logits: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -80,8 +83,7 @@ class MoEFFN:
             out = torch.empty(T, self.H, dtype=torch.bfloat16, device=x.device)
         mask, probs, row_map, offsets = self.route(logits)
         if self.fused_permute:
-            # every permuted row is named by the map (R = T * k), so no -1 fill is needed
-            ops.permute_index(row_map, T * self.k, layout=ops.TOKEN_MAJOR, fill=False, out=b["src"])
+            # src holds the source token of every permuted row (R = T * k rows, all named by the map)
             ops.grouped_gemm_gather(x, b["src"], self.w1, offsets, swiglu=True, out=b["h"])
         else:
             ops.permute(x, row_map, num_out=T * self.k, layout=ops.TOKEN_MAJOR, zero_tail=False, out=b["xp"])

@@ -196,14 +196,17 @@ def router_wgrad_tf32(grad_output: torch.Tensor, inp: torch.Tensor) -> torch.Ten
 
 # ---------------------------------------------------------------- row-id map
 def row_id_map(routing_map: torch.Tensor, *, expert_major: bool = True, token_major: bool = True,
-               expert_major_i32: bool = False, expert_offsets: bool = False,
-               workspace: Optional[torch.Tensor] = None) -> dict:
+               expert_major_i32: bool = False, expert_offsets: bool = False, src_rows: Optional[int] = None,
+               src_out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None) -> dict:
     """Row-id map of a bool/uint8 routing mask [T, E].
 
     Returns a dict with the requested outputs: "expert_major" int64 [E,T],
-    "token_major" int64 [T,E], "expert_major_i32" int32 [E,T] and
+    "token_major" int64 [T,E], "expert_major_i32" int32 [E,T],
     "expert_offsets" int32 [E+1] (offsets[e] = first row of expert e,
-    offsets[E] = number of routed rows).
+    offsets[E] = number of routed rows R) and, with `src_rows` (or `src_out`),
+    "src_token" int32 [src_rows]: the source token of each permuted row
+    (src_token[map(t, e)] = t; src_rows = R, e.g. T * k for top-k routing,
+    gives every row; rows >= R are left unwritten).
     """
     _on_gpu("routing_map", routing_map)
     _dtype("routing_map", routing_map, torch.bool, torch.uint8)
@@ -221,12 +224,22 @@ def row_id_map(routing_map: torch.Tensor, *, expert_major: bool = True, token_ma
         res["expert_major_i32"] = torch.empty(E, T, dtype=torch.int32, device=dev)
     if expert_offsets:
         res["expert_offsets"] = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    if src_out is not None:
+        if src_out.dtype != torch.int32 or not src_out.is_contiguous() or src_out.ndim != 1:
+            raise ValueError("src_out must be a contiguous 1-d int32 tensor")
+        res["src_token"] = src_out
+    elif src_rows is not None:
+        if src_rows < 0:
+            raise ValueError(f"src_rows must be >= 0, got {src_rows}")
+        res["src_token"] = torch.empty(src_rows, dtype=torch.int32, device=dev)
+    src = res.get("src_token")
     ws_bytes = _lib.lib().moe_row_id_map_workspace_size(T, E)
     if workspace is None or workspace.numel() * workspace.element_size() < ws_bytes:
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     call("moe_row_id_map", ptr(m), T, E, ptr(res.get("expert_major")), ptr(res.get("token_major")),
-         ptr(res.get("expert_major_i32")), ptr(res.get("expert_offsets")), ptr(workspace),
-         workspace.numel() * workspace.element_size(), stream_handle())
+         ptr(res.get("expert_major_i32")), ptr(res.get("expert_offsets")), ptr(src),
+         0 if src is None else src.numel(), ptr(workspace), workspace.numel() * workspace.element_size(),
+         stream_handle())
     return res
 
 

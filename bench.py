@@ -55,10 +55,8 @@ def stage_work(T, H, F, E, k):
     return {
         # logits fp32 [T,E] in; values/indices [T,k], mask [T,E] u8, probs [T,E] fp32 out
         "topk": ("GB/s", 4 * T * E + 12 * T * k + T * E + 4 * T * E),
-        # mask [T,E] u8 in; token-major int64 map [T,E] + offsets out
-        "row_id_map": ("GB/s", T * E + 8 * T * E + 4 * (E + 1)),
-        # map [T,E] int64 in; source token per permuted row int32 [R] out
-        "permute_index": ("GB/s", 8 * T * E + 4 * R),
+        # mask [T,E] u8 in; token-major int64 map [T,E] + offsets + source token per permuted row int32 [R] out
+        "row_id_map": ("GB/s", T * E + 8 * T * E + 4 * (E + 1) + 4 * R),
         # x [T,H] bf16 + map [T,E] int64 in; permuted rows [R,H] bf16 out (stand-alone)
         "permute": ("GB/s", 2 * T * H + 8 * T * E + 2 * R * H),
         "fc1_swiglu": ("TFLOP/s", 2 * R * H * (2 * F)),
@@ -465,7 +463,7 @@ def main():
     layer = pkg.moe_ffn.MoEFFN(w1, w2, k)
     ops = pkg.ops
 
-    names = ["topk", "row_id_map", "permute_index", "fc1_swiglu", "fc2", "unpermute_merge"]
+    names = ["topk", "row_id_map", "fc1_swiglu", "fc2", "unpermute_merge"]
     out_buf = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
 
     def step(ev=None):
@@ -474,22 +472,21 @@ def main():
         rec(0)
         _, _, mask, probs = ops.topk(logits, k, with_mask=True, with_probs=True)
         rec(1)
-        maps = ops.row_id_map(mask, expert_major=False, token_major=True, expert_offsets=True, workspace=b["ws"])
+        maps = ops.row_id_map(mask, expert_major=False, token_major=True, expert_offsets=True, src_out=b["src"],
+                              workspace=b["ws"])
         row_map, offs = maps["token_major"], maps["expert_offsets"]
         rec(2)
-        ops.permute_index(row_map, T * k, layout=ops.TOKEN_MAJOR, fill=False, out=b["src"])
-        rec(3)
         ops.grouped_gemm_gather(x, b["src"], w1, offs, swiglu=True, out=b["h"])
-        rec(4)
+        rec(3)
         ops.grouped_gemm(b["h"], w2, offs, out=b["z"])
-        rec(5)
+        rec(4)
         ops.unpermute(b["z"], row_map, probs, layout=ops.TOKEN_MAJOR, out=out_buf)
-        rec(6)
+        rec(5)
         return out_buf
 
     for _ in range(args.warmup):
         step()
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(7)] for _ in range(args.steps)]
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s in range(args.steps):

@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define MOE_DISPATCH_ABI_VERSION 7
+#define MOE_DISPATCH_ABI_VERSION 8
 
 typedef uint16_t moe_bf16_t;
 
@@ -114,29 +114,36 @@ int moe_topk(const float *logits, int64_t T, int64_t E, int64_t k, float *values
  *   row_token_major      int64 [T, E]
  *   row_expert_major_i32 int32 [E, T]   (deep_ep dtype, case24...py:71-84)
  *   expert_offsets       int32 [E + 1]  offset[e]; [E] = R = total routed rows
+ *   src_token            int32 [src_capacity]: the source token of every
+ *                        permuted row, src_token[row[t, e]] = t for row < src_capacity
+ *                        (the inverse map; no reference function -- the token
+ *                        case17's permute copies into that row).  With
+ *                        src_capacity >= R every row 0..R-1 is written (the map
+ *                        is a bijection onto them); rows >= R are left as they are.
+ * Two kernel launches (a column scan of the mask, then the fill).
  * Workspace: moe_row_id_map_workspace_size(T, E) bytes.  E <= 4096. */
 size_t moe_row_id_map_workspace_size(int64_t T, int64_t E);
 int moe_row_id_map(const uint8_t *routing_map, int64_t T, int64_t E, int64_t *row_expert_major,
                    int64_t *row_token_major, int32_t *row_expert_major_i32,
-                   int32_t *expert_offsets, void *workspace, size_t workspace_bytes,
-                   void *stream);
+                   int32_t *expert_offsets, int32_t *src_token, int64_t src_capacity,
+                   void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---- a3': row-id map without a workspace (allocates nothing) -------------
  * No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): moe_row_id_map with the same arguments and results, whose
- * scratch (ceil(T/64)*E + E int32 values) lives in an 8 MiB device array the
- * library holds per GPU until the process ends.
- * Limit: moe_row_id_map_workspace_size(T, E) <= 8 MiB (e.g. T = 65536 at
- *   E = 1024, T = 16384 at E = 4096), else MOE_ERR_CAPACITY; other limits as
- *   moe_row_id_map.
+ * scratch (the per-super-chunk counts, at most 64 (E + ceil(E/32)) int32
+ * values) lives in a 2 MiB device array the library holds per GPU until the
+ * process ends.
+ * Limits: as moe_row_id_map (E <= 4096, T*E < 2^31), within which the 2 MiB
+ *   always suffice; a larger need would fail with MOE_ERR_CAPACITY.
  * Every call on a GPU shares that GPU's scratch: calls that overlap on one GPU
  * (on different streams or host threads) race; calls ordered on one stream do
  * not.  Nothing in the scratch needs to start at zero. */
 int moe_row_id_map_noalloc(const uint8_t *routing_map, int64_t T, int64_t E,
                            int64_t *row_expert_major, int64_t *row_token_major,
                            int32_t *row_expert_major_i32, int32_t *expert_offsets,
-                           void *stream);
+                           int32_t *src_token, int64_t src_capacity, void *stream);
 
 /* ---- a4/a5: permute -----------------------------------------------------
  * Replaces case17 kernel_function(x, row_id_map, probs) -> (out, permuted_probs)

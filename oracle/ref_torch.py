@@ -82,6 +82,23 @@ def permute_token_major(x: torch.Tensor, row_id_map: torch.Tensor, probs: torch.
     return out, permuted_probs
 
 
+def source_tokens(row_id_map: torch.Tensor, num_out: int) -> torch.Tensor:
+    """int32 [num_out]: the token each permuted row is copied from (-1 where no entry names the row).
+
+    No reference function: the inverse of the token-major map of case12
+    (kernel_cases/case12_moe_row_id_map_pass2.py:43-61), i.e. the index_select
+    source of case17's permute (kernel_cases/case17_moe_permute_with_mask_map.py:58-71):
+    permute_token_major(x, map, ...)[0][p] == x[source_tokens(map)[p]].
+    """
+    n, e = row_id_map.shape
+    dst = row_id_map.reshape(-1)
+    keep = (dst >= 0) & (dst < num_out)
+    tok = torch.arange(n, dtype=torch.int32).repeat_interleave(e)
+    out = torch.full((num_out,), -1, dtype=torch.int32)
+    out[dst[keep]] = tok[keep]
+    return out
+
+
 def permute_expert_major(inp: torch.Tensor, row_id_map: torch.Tensor, probs: Optional[torch.Tensor] = None):
     """Scatter for an expert-major [E,T] map, num_out = max + 1.
 

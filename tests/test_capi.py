@@ -52,13 +52,14 @@ FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
     ("moe_unpermute", (FAKE, 8, 8, FAKE, 1, 1, 5000, 4, None, FAKE, None, None), L.MOE_ERR_CAPACITY, "4096"),
     ("moe_unpermute", (FAKE, 8, -8, FAKE, 1, 1, 4, 4, None, FAKE, None, None), L.MOE_ERR_SHAPE, "negative"),
     ("moe_permute_bwd", (FAKE, 8, 8, None, FAKE, 1, 1, 4, 4, FAKE, FAKE, None, None), L.MOE_ERR_INVALID_ARG, "dpp"),
-    ("moe_row_id_map", (FAKE, 16, 8000, None, None, None, None, None, 0, None), L.MOE_ERR_CAPACITY, "4096"),
-    ("moe_row_id_map", (FAKE, 16, 8, None, None, None, None, None, 0, None), L.MOE_ERR_WORKSPACE, "workspace"),
-    ("moe_row_id_map", (None, 16, 8, None, None, None, None, FAKE, 1 << 20, None), L.MOE_ERR_INVALID_ARG, "null"),
-    ("moe_row_id_map_noalloc", (FAKE, 1 << 18, 4096, None, None, None, None, None), L.MOE_ERR_CAPACITY, "scratch"),
-    ("moe_row_id_map_noalloc", (FAKE, 16, 8000, None, None, None, None, None), L.MOE_ERR_CAPACITY, "4096"),
-    ("moe_row_id_map_noalloc", (FAKE, -16, 8, None, None, None, None, None), L.MOE_ERR_SHAPE, "negative"),
-    ("moe_row_id_map_noalloc", (None, 16, 8, None, None, None, None, None), L.MOE_ERR_INVALID_ARG, "null"),
+    ("moe_row_id_map", (FAKE, 16, 8000, None, None, None, None, None, 0, None, 0, None), L.MOE_ERR_CAPACITY, "4096"),
+    ("moe_row_id_map", (FAKE, 16, 8, None, None, None, None, None, 0, None, 0, None), L.MOE_ERR_WORKSPACE, "workspace"),
+    ("moe_row_id_map", (None, 16, 8, None, None, None, None, None, 0, FAKE, 1 << 20, None), L.MOE_ERR_INVALID_ARG, "null"),
+    ("moe_row_id_map_noalloc", (FAKE, 1 << 20, 4096, None, None, None, None, None, 0, None), L.MOE_ERR_CAPACITY, "2^31"),
+    ("moe_row_id_map_noalloc", (FAKE, 16, 8000, None, None, None, None, None, 0, None), L.MOE_ERR_CAPACITY, "4096"),
+    ("moe_row_id_map_noalloc", (FAKE, -16, 8, None, None, None, None, None, 0, None), L.MOE_ERR_SHAPE, "negative"),
+    ("moe_row_id_map_noalloc", (None, 16, 8, None, None, None, None, None, 0, None), L.MOE_ERR_INVALID_ARG, "null"),
+    ("moe_row_id_map", (FAKE, 16, 8, None, None, None, None, FAKE, -1, FAKE, 1 << 20, None), L.MOE_ERR_SHAPE, "src_capacity"),
     ("moe_topk", (FAKE, 4, 16, 0, FAKE, FAKE, None, None, None), L.MOE_ERR_SHAPE, "out of range"),
     ("moe_topk", (FAKE, 4, 16, 17, FAKE, FAKE, None, None, None), L.MOE_ERR_SHAPE, "out of range"),
     ("moe_topk", (FAKE, 4, 2048, 8, FAKE, FAKE, None, None, None), L.MOE_ERR_CAPACITY, "1024"),
@@ -149,9 +150,12 @@ def test_empty_problems_are_no_ops():
 
 def test_workspace_sizes():
     lib = L.lib()
-    # chunk counts [ceil(T/64), E] plus the expert totals [E], int32
-    assert lib.moe_row_id_map_workspace_size(16384, 64) >= (256 * 64 + 64) * 4
-    assert lib.moe_row_id_map_workspace_size(16385, 320) >= (257 * 320 + 320) * 4
+    # per super-chunk (S <= 64 of them, each a multiple of 256 tokens) the expert counts [S, E]
+    # and the 32-expert group sums [S, ceil(E/32)], int32
+    assert lib.moe_row_id_map_workspace_size(16384, 64) >= 64 * (64 + 2) * 4
+    assert lib.moe_row_id_map_workspace_size(16385, 320) >= 65 * (320 + 10) * 4 // 2
+    assert lib.moe_row_id_map_workspace_size(300001, 6) >= 62 * (6 + 1) * 4
+    assert lib.moe_row_id_map_workspace_size(1 << 26, 32) <= 64 * 33 * 4 + 256
     assert lib.moe_permute_workspace_size(16384) >= 4096 * 4
     assert lib.moe_row_id_map_workspace_size(-1, 4) == 0
     # router: one fp32 logits plane (used when the top-k call gets no logits output)

@@ -30,16 +30,26 @@ def _mask(T, E, k=None, p=None, seed=0):
     (1, 1, 1, None), (63, 3, None, 0.5), (64, 8, 2, None), (65, 7, None, 0.3), (1000, 130, None, 0.04),
     (4096, 8, 2, None), (16384, 64, 8, None), (300, 5, None, 0.0), (257, 1024, None, 0.01),
     (200, 48, 4, None), (70, 2000, None, 0.01), (33, 4096, None, 0.002), (5000, 160, 8, None),
+    # more than 4096 chunks of 64 tokens: the column scan carries its sums across rounds
+    (270000, 4, 1, None), (300001, 6, None, 0.3),
 ])
 def test_row_id_map_matches_oracle(pkg, dev, T, E, k, p):
     rm = _mask(T, E, k, p, seed=T + E)
+    R = int(rm.sum())
+    src = torch.full((R + 5,), -7, dtype=torch.int32, device=dev)
     r = pkg.ops.row_id_map(rm.to(dev), expert_major=True, token_major=True, expert_major_i32=True,
-                           expert_offsets=True)
+                           expert_offsets=True, src_out=src)
     em, tm = ref_torch.row_id_map(rm)
     assert_bits_equal(r["expert_major"], em, "expert-major map")
     assert_bits_equal(r["token_major"], tm, "token-major map")
     assert_bits_equal(r["expert_major_i32"], em.to(torch.int32), "int32 map")
     assert_bits_equal(r["expert_offsets"], ref_torch.expert_offsets(rm), "expert offsets")
+    # source token of every permuted row; rows past R are left as they were
+    assert_bits_equal(r["src_token"][:R], ref_torch.source_tokens(tm, R), "source tokens")
+    assert bool((r["src_token"][R:] == -7).all())
+    # only the source index (no map output): same rows, and a capacity below R writes the rows below it
+    r2 = pkg.ops.row_id_map(rm.to(dev), expert_major=False, token_major=False, src_rows=max(R // 2, 0))
+    assert_bits_equal(r2["src_token"], ref_torch.source_tokens(tm, max(R // 2, 0)), "source tokens, half")
 
 
 def test_row_id_map_reference_case12_full(pkg, dev):
@@ -49,6 +59,10 @@ def test_row_id_map_reference_case12_full(pkg, dev):
     ref_em, ref_tm = ref_torch.row_id_map(rm)
     assert_bits_equal(em, ref_em, "case12 [E,T]")
     assert_bits_equal(tm, ref_tm, "case12 [T,E]")
+    R = int(rm.sum())
+    r = pkg.ops.row_id_map(rm.to(dev), expert_major=False, token_major=False, expert_offsets=True, src_rows=R)
+    assert_bits_equal(r["src_token"], ref_torch.source_tokens(ref_tm, R), "case12 source tokens")
+    assert_bits_equal(r["expert_offsets"], ref_torch.expert_offsets(rm), "case12 offsets")
 
 
 def test_row_id_map_empty(pkg, dev):

@@ -449,3 +449,24 @@ def test_moe_ffn_fp32_composition_against_float64_brute_force():
     torch.testing.assert_close(out.double(), expect, rtol=1e-2, atol=1e-2)
     sub = torch.tensor([0, 5, 17, 22])
     assert torch.equal(ref_torch.moe_ffn_forward_fp32(x[sub], logits[sub], w1, w2, k), out[sub])
+
+
+def test_source_tokens_inverts_the_map_and_feeds_the_permute():
+    # Brute-force double loop, and the permute relation x[src] == permuted rows.
+    g = torch.Generator().manual_seed(79)
+    T, E, k, H = 40, 7, 3, 5
+    sel = torch.rand(T, E, generator=g).argsort(dim=1)[:, :k]
+    mask = torch.zeros(T, E, dtype=torch.bool).scatter_(1, sel, True)
+    mask[3] = False
+    _, tm = ref_torch.row_id_map(mask)
+    R = int(mask.sum())
+    src = ref_torch.source_tokens(tm, R + 4)
+    brute = torch.full((R + 4,), -1, dtype=torch.int32)
+    for t in range(T):
+        for e in range(E):
+            if tm[t, e] >= 0:
+                brute[tm[t, e]] = t
+    assert torch.equal(src, brute) and bool((src[:R] >= 0).all()) and bool((src[R:] == -1).all())
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    xp, _ = ref_torch.permute_token_major(x, tm, torch.zeros(T, E), R)
+    assert torch.equal(x[src[:R].long()], xp)

@@ -23,18 +23,20 @@ def _mask(T, E, k, seed):
     return torch.zeros(T, E, dtype=torch.uint8).scatter_(1, idx, 1)
 
 
-def _outputs(T, E, dev):
+def _outputs(T, E, k, dev):
     return (torch.full((E, T), -7, dtype=torch.int64, device=dev),
             torch.full((T, E), -7, dtype=torch.int64, device=dev),
             torch.full((E, T), -7, dtype=torch.int32, device=dev),
-            torch.full((E + 1,), -7, dtype=torch.int32, device=dev))
+            torch.full((E + 1,), -7, dtype=torch.int32, device=dev),
+            torch.full((T * k,), -7, dtype=torch.int32, device=dev))
 
 
 def _ptr(t):
     return ctypes.c_void_p(t.data_ptr())
 
 
-@pytest.mark.parametrize("shapes", [[(4096, 320, 8), (1000, 64, 2)], [(16384, 64, 8), (257, 16, 3)]])
+@pytest.mark.parametrize("shapes", [[(4096, 320, 8), (1000, 64, 2)], [(16384, 64, 8), (257, 16, 3)],
+                                    [(200000, 40, 4), (70, 4096, 5)]])
 def test_row_id_map_noalloc_matches_workspace_entry_point(dev, shapes):
     lib = L.lib()
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -43,20 +45,24 @@ def test_row_id_map_noalloc_matches_workspace_entry_point(dev, shapes):
         mask = _mask(T, E, k, seed=T * 7 + E).to(dev)
         ws_bytes = lib.moe_row_id_map_workspace_size(T, E)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-        ref = _outputs(T, E, dev)
-        got = _outputs(T, E, dev)
-        st = lib.moe_row_id_map(_ptr(mask), T, E, *(_ptr(t) for t in ref), _ptr(ws), ws_bytes, stream)
+        ref = _outputs(T, E, k, dev)
+        got = _outputs(T, E, k, dev)
+        st = lib.moe_row_id_map(_ptr(mask), T, E, *(_ptr(t) for t in ref), T * k, _ptr(ws), ws_bytes, stream)
         assert st == L.MOE_OK, lib.moe_last_error().decode()
-        st = lib.moe_row_id_map_noalloc(_ptr(mask), T, E, *(_ptr(t) for t in got), stream)
+        st = lib.moe_row_id_map_noalloc(_ptr(mask), T, E, *(_ptr(t) for t in got), T * k, stream)
         assert st == L.MOE_OK, lib.moe_last_error().decode()
         torch.cuda.synchronize()
-        for name, g, r in zip(("expert-major", "token-major", "int32 expert-major", "offsets"), got, ref):
+        for name, g, r in zip(("expert-major", "token-major", "int32 expert-major", "offsets", "source tokens"),
+                              got, ref):
             assert_bits_equal(g, r, f"call {i} {name}")
         assert int(got[3][-1]) == T * k
 
 
-def test_row_id_map_noalloc_rejects_oversized_input(dev):
+def test_row_id_map_noalloc_rejects_sizes_beyond_its_limits(dev):
+    # E above 4096 and T * E at 2^31 fail before any device work; everything below them fits
+    # the static scratch (the largest need, E = 4096, is 64 * (4096 + 128) int32 values).
     lib = L.lib()
-    T, E = 1 << 18, 4096  # ceil(T/64) * E int32 counts = 64 MiB > the 8 MiB scratch
-    st = lib.moe_row_id_map_noalloc(ctypes.c_void_p(0x1000), T, E, None, None, None, None, None)
-    assert st == L.MOE_ERR_CAPACITY and "scratch" in lib.moe_last_error().decode()
+    for T, E, needle in ((16, 5000, "4096"), (1 << 20, 4096, "2^31")):
+        st = lib.moe_row_id_map_noalloc(ctypes.c_void_p(0x1000), T, E, None, None, None, None, None, 0, None)
+        assert st == L.MOE_ERR_CAPACITY and needle in lib.moe_last_error().decode(), (T, E)
+    assert lib.moe_row_id_map_workspace_size((1 << 31) // 4096 - 1, 4096) <= 2 << 20
