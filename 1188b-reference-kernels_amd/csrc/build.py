@@ -32,6 +32,7 @@ SOURCES = [
     "grouped_gemm_bwd.hip",
     "router.hip",
     "cast.hip",
+    "probes.hip",
 ]
 
 ARCH = os.environ.get("MOE_OFFLOAD_ARCH", "gfx950")

@@ -92,9 +92,141 @@ def cpu_baseline(pkg, x, logits, w1, w2, k, run_s=2.5):
     times = [run(n) for _ in range(3)]
     med = statistics.median(times)
     return {"value": round(n / med, 1), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"first {n} tokens of the c5 batch through oracle/ref_torch.moe_ffn_forward "
                       f"(eager torch on the CPU, full E=64/H=7168/F=2048 bf16 weights), median of 3 runs "
                       f"of {[round(v, 3) for v in times]} s"}
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the platform's processor string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+class _PowerClock:
+    """Samples socket power (W) and shader clock (MHz) every 40 ms while active (amdsmi's GPU
+    metrics table); the middle half of the samples is averaged.  Empty when amdsmi is absent."""
+
+    def __init__(self):
+        import threading
+        self._threading = threading
+        try:
+            import amdsmi
+            amdsmi.amdsmi_init()
+            self._smi, self._h = amdsmi, amdsmi.amdsmi_get_processor_handles()[0]
+        except Exception:  # no amdsmi on this host: report nothing
+            self._smi = None
+
+    def measure(self, fn, seconds=1.5):
+        """Runs fn() back to back for `seconds`; returns (ms per call, power W or None, clock MHz or None)."""
+        samples, stop = [], self._threading.Event()
+
+        def loop():
+            while not stop.is_set():
+                try:
+                    m = self._smi.amdsmi_get_gpu_metrics_info(self._h)
+                    samples.append((m.get("current_socket_power"), m.get("current_gfxclk")))
+                except Exception:
+                    pass
+                time.sleep(0.04)
+
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        th = self._threading.Thread(target=loop) if self._smi is not None else None
+        if th:
+            th.start()
+        times, t0 = [], time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+            ev[0].record()
+            for i in range(4):
+                fn()
+                ev[i + 1].record()
+            torch.cuda.synchronize()
+            times += [ev[i].elapsed_time(ev[i + 1]) for i in range(4)]
+        if th:
+            stop.set()
+            th.join()
+        mid = samples[len(samples) // 4: 3 * len(samples) // 4] or samples
+        pw = [a for a, _ in mid if isinstance(a, (int, float))]
+        ck = [b for _, b in mid if isinstance(b, (int, float))]
+        return (statistics.median(times), round(statistics.mean(pw), 1) if pw else None,
+                round(statistics.mean(ck), 1) if ck else None)
+
+
+def ceilings(pkg, dev):
+    """Ceilings the roofline fractions are read against, measured on this GPU, plus the power and
+    clock the c5 GEMMs (and hipBLASLt on the fc1 shape) run at.  One JSON line."""
+    import ctypes
+
+    lib = pkg._lib.lib()
+    P, I64 = ctypes.c_void_p, ctypes.c_int64
+    lib.moe_probe_mfma.argtypes = [I64, I64, P, P]
+    lib.moe_probe_stream.argtypes = [ctypes.c_int, P, P, I64, I64, P]
+    s = torch.cuda.current_stream().cuda_stream
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    pc = _PowerClock()
+    out = {"metric": "ceilings", "device": torch.cuda.get_device_name(0), "cus": cus}
+
+    waves, iters = cus * 8, 80000  # about 20 ms per call
+    sink = torch.empty(waves * 64, dtype=torch.float32, device=dev)
+    ms, pw, ck = pc.measure(lambda: lib.moe_probe_mfma(waves, iters, sink.data_ptr(), s), seconds=3.0)
+    tf = waves * iters * 16 * 16384 / (ms * 1e-3) / 1e12
+    out["mfma_bf16_register_loop"] = {"TFLOP/s": round(tf, 1), "frac_of_peak": round(tf / BF16_PEAK_TFLOPS, 4),
+                                      "ms": round(ms, 3), "waves": waves, "power_W": pw, "clock_MHz": ck}
+
+    nbytes = 2 << 30
+    src = torch.empty(nbytes // 4, dtype=torch.int32, device=dev).fill_(7)
+    dst = torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
+    nvec, blocks = nbytes // 16, cus * 16
+    for mode, name, moved in ((0, "copy", 2 * nbytes), (1, "read_only", nbytes), (2, "write_only", nbytes),
+                              (4, "copy_nt", 2 * nbytes), (5, "read_only_nt", nbytes), (6, "write_only_nt", nbytes)):
+        ms, pw, ck = pc.measure(lambda: lib.moe_probe_stream(mode, src.data_ptr(), dst.data_ptr(), nvec, blocks, s),
+                                seconds=1.0)
+        gbs = moved / (ms * 1e-3) / 1e9
+        out[name] = {"GB/s": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4), "ms": round(ms, 3),
+                     "bytes": moved, "power_W": pw, "clock_MHz": ck}
+    del src, dst
+
+    # The c5 GEMMs of the timed step, and the library GEMM of the fc1 shape, under the same sampler.
+    T, H, F, E, k = CFG["tokens"], CFG["hidden"], CFG["ffn"], CFG["experts"], CFG["topk"]
+    inp, ops = pkg.inputs, pkg.ops
+    x = inp.randn_bf16((T, H), seed=SEED, device=dev)
+    logits = inp.router_logits(T, E, skew=CFG["skew"], seed=SEED, device=dev)
+    w1 = inp.randn_bf16((E, 2 * F, H), std=0.02, seed=SEED + 10, device=dev)
+    w2 = inp.randn_bf16((E, H, F), std=0.02, seed=SEED + 20, device=dev)
+    _, _, mask = ops.topk(logits, k, with_mask=True)
+    maps = ops.row_id_map(mask, expert_major=False, token_major=False, expert_offsets=True, src_rows=T * k)
+    offs, src_tok = maps["expert_offsets"], maps["src_token"]
+    h = torch.empty(T * k, F, dtype=torch.bfloat16, device=dev)
+    z = torch.empty(T * k, H, dtype=torch.bfloat16, device=dev)
+    for name, fn, flops in (
+            ("fc1_swiglu", lambda: ops.grouped_gemm_gather(x, src_tok, w1, offs, swiglu=True, out=h), 2 * T * k * H * 2 * F),
+            ("fc2", lambda: ops.grouped_gemm(h, w2, offs, out=z), 2 * T * k * F * H)):
+        ms, pw, ck = pc.measure(fn, seconds=3.0)
+        tf = flops / (ms * 1e-3) / 1e12
+        out[name] = {"TFLOP/s": round(tf, 1), "frac_of_peak": round(tf / BF16_PEAK_TFLOPS, 4), "ms": round(ms, 4),
+                     "power_W": pw, "clock_MHz": ck}
+    del x, w1, w2, h, z
+    m = T * k // E
+    a = torch.randn(E, m, H, device=dev, dtype=torch.bfloat16)
+    b = torch.randn(E, 2 * F, H, device=dev, dtype=torch.bfloat16).transpose(1, 2).contiguous()
+    c = torch.empty(E, m, 2 * F, device=dev, dtype=torch.bfloat16)
+    ms, pw, ck = pc.measure(lambda: torch.bmm(a, b, out=c), seconds=3.0)
+    tf = 2 * E * m * H * 2 * F / (ms * 1e-3) / 1e12
+    out["hipblaslt_bmm_fc1_shape"] = {"op": f"torch.bmm bf16 {E} x [{m}, {H}] @ [{H}, {2 * F}]", "TFLOP/s": round(tf, 1),
+                                      "frac_of_peak": round(tf / BF16_PEAK_TFLOPS, 4), "ms": round(ms, 4),
+                                      "power_W": pw, "clock_MHz": ck}
+    return out
 
 
 def library_reference(m, kdim, n, groups, dev, reps=5):
@@ -439,6 +571,10 @@ def main():
                     help="skip the backward grouped GEMMs (reported beside the forward, not in value)")
     ap.add_argument("--no-router", action="store_true",
                     help="skip the router front end / router backward timings (reported beside the forward)")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="instead of the step benchmark, print one JSON line with the measured ceilings: a "
+                         "register-only MFMA loop, copy / read-only / write-only streams, and the power and clock "
+                         "under them, under the c5 GEMMs and under hipBLASLt on the fc1 shape")
     ap.add_argument("--configs", action="store_true",
                     help="instead of the step benchmark, print one JSON line per baseline config (C1-C5) and the "
                          "reference shapes with per-kernel medians (50 calls, 1 GiB flushed before each)")
@@ -453,6 +589,9 @@ def main():
     if args.configs:
         for line in config_lines(pkg, dev):
             print(json.dumps(line), flush=True)
+        return
+    if args.ceilings:
+        print(json.dumps(ceilings(pkg, dev)), flush=True)
         return
     T, H, F, E, k = CFG["tokens"], CFG["hidden"], CFG["ffn"], CFG["experts"], CFG["topk"]
     inp = pkg.inputs

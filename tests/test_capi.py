@@ -187,3 +187,17 @@ def test_inputs_generators_cpu():
     assert pkg.inputs.uniform_group_sizes(4096, 40)[:2] == [103, 103] and sum(pkg.inputs.uniform_group_sizes(4096, 40)) == 4096
     rm, sel = pkg.inputs.reference_routing_mask(64, 16)
     assert rm.sum(1).tolist() == [6 if t % 4 == 1 else 5 for t in range(64)]
+
+
+def test_probe_entry_points_validate_before_launch():
+    # measurement probes (include/moe_probes.h): exported, and bad arguments fail on the host
+    lib = L.lib()
+    P, I64 = ctypes.c_void_p, ctypes.c_int64
+    lib.moe_probe_mfma.argtypes = [I64, I64, P, P]
+    lib.moe_probe_stream.argtypes = [ctypes.c_int, P, P, I64, I64, P]
+    assert lib.moe_probe_mfma(6, 10, FAKE, None) == L.MOE_ERR_SHAPE
+    assert lib.moe_probe_mfma(8, 10, None, None) == L.MOE_ERR_INVALID_ARG
+    assert lib.moe_probe_stream(3, FAKE, FAKE, 16, 1, None) == L.MOE_ERR_INVALID_ARG
+    assert lib.moe_probe_stream(7, FAKE, FAKE, 16, 1, None) == L.MOE_ERR_INVALID_ARG
+    assert lib.moe_probe_stream(0, None, FAKE, 16, 1, None) == L.MOE_ERR_INVALID_ARG
+    assert lib.moe_probe_stream(2, None, ctypes.c_void_p(0x1004), 16, 1, None) == L.MOE_ERR_ALIGN
