@@ -516,6 +516,448 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
   }
 }
 
+// ---- pipelined 256 x 256 kernel ---------------------------------------------
+// The kernel the host runs for every 256-row tile (dgrad with groups above
+// ~160 rows, wgrad, and the tf32 router GEMMs): the forward pipelined kernel's
+// shape with reduction-major operands.
+//   * v_mfma_f32_16x16x32_bf16, 8 x 8 blocks of 16 x 16 per wave (the board
+//     holds a higher clock under it than under the 32 x 32 x 16 form);
+//   * consecutive tiles of a workgroup follow each other without draining:
+//     a tile's second-to-last step DMAs the next tile's stage 0, its last step
+//     reads those fragments and DMAs stage 1, and the epilogue stores straight
+//     from registers after that DMA (bf16: v_permlane16_swap pairs two 16-column
+//     blocks so a lane holds 8 consecutive columns; fp32: 4 consecutive columns
+//     per lane and block as they are);
+//   * a tile has at least three reduction steps (the first and the last two
+//     are peeled; wgrad tiles of groups with at most 128 rows run steps over
+//     zeros: rows past the group's end lie past the operand's buffer resource;
+//     the host sends dgrad here only for N a multiple of 64, at least 192);
+//   * reduction-major fragments: in 16-lane group G, lane 4 j + q reads rows
+//     8 G + j and 8 G + j + 4 of the K half (ds_read_b64_tr_b16), columns
+//     c + 4 q .. c + 3q + 3 of a 16-column block, so lane 16 G + i holds the 8
+//     reduction values 8 G .. 8 G + 7 of column c + i, the 16 x 16 x 32 operand
+//     layout. The 16-byte chunks of a 512-byte LDS row are XOR-swizzled by
+//     rm16_swz (row bits 0-1 and 3 into chunk bits 1-3): the 8 rows one
+//     half-wave reads at a time fall on 8 distinct 32-byte bank groups.
+__device__ __forceinline__ int rm16_swz(int krow) { return ((krow & 3) << 2) | (((krow >> 3) & 1) << 1); }
+
+template <bool kWgrad, int kOut>
+__global__ __launch_bounds__(256) void grouped_gemm_bwd_pipe_kernel(BwdArgs p) {
+  constexpr int kBM = 256;
+  constexpr int kWaves = 4;
+  constexpr int kThreads = 256;
+  constexpr int kStages = 2;
+  constexpr int kOpBytes = 256 * kBK * 2;            // 32 KiB: one operand of a stage
+  constexpr int kStageBytes = 2 * kOpBytes;
+  constexpr int kDma = kOpBytes / 1024 / kWaves;     // 8 DMA instructions per operand per stage
+  constexpr int kMaxG = 4096;
+  constexpr int kStores = kOut == 0 ? 32 : 0;        // bf16 stores per lane and tile (fp32: the next waits take all)
+  constexpr int kAR = kWgrad ? 2 : 1;                // LDS reads per A fragment
+  constexpr int kMI = 8, kNI = 8;
+  static_assert(kStores + 2 * kDma <= 63, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) char smem[kStages * kStageBytes];
+  __shared__ int32_t s_offs[kMaxG + 1];
+  lds_char *const sbase = (lds_char *)smem;
+  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sbase));
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+  const int64_t P = gridDim.x;
+  const int64_t b = blockIdx.x;
+  const int64_t N = p.N, K = p.K;
+  const bool chunked = p.offsets == nullptr;
+
+  if (!chunked) {
+    for (int64_t i = tid; i <= p.G; i += kThreads) s_offs[i] = p.offsets[i];
+  }
+  __syncthreads();
+
+  // ---- tile walker (group offsets from LDS; 32-bit: the host keeps M below
+  // 2^31). The values are wave-uniform and read into scalar registers.
+  const int m32 = static_cast<int>(p.M);
+  auto group_range = [&](int g, int &lo, int &hi) {
+    if (chunked) {
+      lo = static_cast<int>(min(static_cast<int64_t>(g) * p.chunk, p.M));
+      hi = static_cast<int>(min(static_cast<int64_t>(lo) + p.chunk, p.M));
+      return;
+    }
+    lo = min(max(__builtin_amdgcn_readfirstlane(s_offs[g]), 0), m32);
+    hi = min(max(__builtin_amdgcn_readfirstlane(s_offs[g + 1]), lo), m32);
+  };
+  const int g_count = static_cast<int>(p.G);
+  const uint32_t ntl = static_cast<uint32_t>(p.ntiles);
+  const uint32_t wg_rows = static_cast<uint32_t>(ceil_div(N, kBM));  // wgrad: row tiles per group
+  auto row_tiles = [&](int lo, int hi) -> uint32_t {
+    return kWgrad ? wg_rows : static_cast<uint32_t>(hi - lo + kBM - 1) / kBM;
+  };
+  int g_cur = 0, g_lo, g_hi;
+  uint32_t tiles_before = 0;
+  group_range(0, g_lo, g_hi);
+  uint32_t mt_g = row_tiles(g_lo, g_hi);
+  struct Tile {
+    int g, lo, hi;   // group and its row range (dgrad: output rows; wgrad: reduction rows)
+    int i0;          // first output row of the tile (dgrad: in dx; wgrad: in dw[g])
+    uint32_t nt;     // column tile
+    int rows_valid;  // output rows of the tile
+    int ktiles;      // reduction steps (at least 3)
+  };
+  const uint32_t P32 = static_cast<uint32_t>(P);
+  const uint32_t L0 = static_cast<uint32_t>((b % 8) * (P / 8) + b / 8);
+  auto find_tile = [&](uint32_t round, Tile &t) -> bool {
+    const uint32_t L = round * P32 + L0;
+    while (g_cur < g_count && L >= tiles_before + mt_g * ntl) {
+      tiles_before += mt_g * ntl;
+      ++g_cur;
+      if (g_cur < g_count) {
+        group_range(g_cur, g_lo, g_hi);
+        mt_g = row_tiles(g_lo, g_hi);
+      }
+    }
+    if (g_cur >= g_count) return false;
+    const uint32_t q = L - tiles_before;
+    const uint32_t per_grp = kGroupM * ntl;
+    const uint32_t full = mt_g / kGroupM;
+    uint32_t mt, nt;
+    if (q < full * per_grp) {
+      const uint32_t grp = q / per_grp, r = q - grp * per_grp;
+      nt = r / kGroupM;
+      mt = grp * kGroupM + r % kGroupM;
+    } else {
+      const uint32_t r = q - full * per_grp, gm = mt_g - full * kGroupM;
+      nt = r / gm;
+      mt = full * kGroupM + (r - nt * gm);
+    }
+    t.g = g_cur;
+    t.lo = g_lo;
+    t.hi = g_hi;
+    t.i0 = (kWgrad ? 0 : g_lo) + static_cast<int>(mt) * kBM;
+    t.nt = nt;
+    t.rows_valid = min((kWgrad ? static_cast<int>(N) : g_hi) - t.i0, kBM);
+    const int red = kWgrad ? g_hi - g_lo : static_cast<int>(N);
+    t.ktiles = max((red + kBK - 1) / kBK, 3);
+    return true;
+  };
+
+  // ---- DMA sources of the tile being loaded (32-bit offsets: the host bounds
+  // every operand panel below 2 GiB)
+  __amdgpu_buffer_rsrc_t ra, rb;
+  int a_off[kDma], b_off[kDma];
+  int a_step = 0, b_step = 0;  // bytes per reduction step
+  const uint32_t n32 = static_cast<uint32_t>(N), k32 = static_cast<uint32_t>(K);
+  auto setup_dma = [&](const Tile &t) {
+    // Recomputed per tile (not kept live across the tile loop): the lane's
+    // DMA row and chunk from an opaque copy of the lane index. A
+    // reduction-major DMA block holds reduction rows 2 blk, 2 blk + 1.
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int rm_row = ln >> 5, rm_pchunk = ln & 31;
+    if constexpr (kWgrad) {
+      const uint32_t rows = static_cast<uint32_t>(t.hi - t.lo);
+      ra = make_rsrc(p.a + static_cast<int64_t>(t.lo) * N, rows * n32 * 2u);
+      rb = make_rsrc(p.b + static_cast<int64_t>(t.lo) * K, rows * k32 * 2u);
+      a_step = kBK * static_cast<int>(n32) * 2;
+#pragma unroll
+      for (int j = 0; j < kDma; ++j) {
+        const int krow = (j * kWaves + wave) * 2 + rm_row;
+        const uint32_t lchunk = static_cast<uint32_t>(rm_pchunk ^ rm16_swz(krow));
+        a_off[j] = static_cast<int>(static_cast<uint32_t>(krow) * n32 * 2u + static_cast<uint32_t>(t.i0) * 2u + lchunk * 16u);
+      }
+    } else {
+      ra = make_rsrc(p.a + static_cast<int64_t>(t.i0) * N, static_cast<uint32_t>(t.rows_valid) * n32 * 2u);
+      rb = make_rsrc(p.b + static_cast<int64_t>(t.g) * N * K, static_cast<uint32_t>(N * K * 2));
+      a_step = kBK * 2;
+#pragma unroll
+      for (int j = 0; j < kDma; ++j) {
+        const int r = (j * kWaves + wave) * 8 + (ln >> 3);
+        const uint32_t lchunk = static_cast<uint32_t>((ln & 7) ^ kc_swz(r));
+        // Rows past the group's end read as zeros (results dropped).
+        a_off[j] = r < t.rows_valid ? static_cast<int>(static_cast<uint32_t>(r) * n32 * 2u + lchunk * 16u)
+                                    : static_cast<int>(kNoAccess);
+      }
+    }
+    b_step = kBK * static_cast<int>(k32) * 2;
+    const uint32_t col0 = t.nt * static_cast<uint32_t>(kBN);
+#pragma unroll
+    for (int j = 0; j < kDma; ++j) {
+      const int krow = (j * kWaves + wave) * 2 + rm_row;
+      const uint32_t lchunk = static_cast<uint32_t>(rm_pchunk ^ rm16_swz(krow));
+      b_off[j] = static_cast<int>(static_cast<uint32_t>(krow) * k32 * 2u + col0 * 2u + lchunk * 16u);
+    }
+  };
+  // Operand `op` (0 = A, 1 = B) of reduction step `kt` of the tile set up last into ring slot `slot`.
+  auto issue_half = [&](int kt, int slot, int op) {
+    const uint32_t st = lds_base + (slot % kStages) * kStageBytes + op * kOpBytes;
+    const int soff = kt * (op ? b_step : a_step);
+#pragma unroll
+    for (int j = 0; j < kDma; ++j) {
+      const uint32_t blk = j * kWaves + wave;
+      dma16b(op ? rb : ra, (lds_void *)(uintptr_t)(st + blk * 1024), op ? b_off[j] : a_off[j], soff);
+    }
+  };
+  // ---- fragments
+  // KC (dgrad's dy): lane l reads row (block + l % 16), the 8 values
+  // 8 (l / 16) .. + 7 of K half ks (logical chunk 4 ks + l / 16).
+  const int fq = lane >> 4;
+  const int ra0 = wm * 128 + (lane & 15);
+  const uint32_t fa0 = ra0 * kKCRow + ((fq ^ kc_swz(ra0)) << 4);
+  // RM: the lane's row and column bytes within a 16-column block whose 32-byte
+  // position is XORed with rmx (the swizzle of the lane's rows).
+  const int rg = lane >> 4, rj = (lane >> 2) & 3, rq = lane & 3;
+  const uint32_t rm0 = (8 * rg + rj) * kRMRow + ((rq >> 1) << 4) + (rq & 1) * 8;
+  const uint32_t rmx = static_cast<uint32_t>((rj << 1) | (rg & 1)) << 5;
+  const uint32_t rma0 = rm0 + wm * 256;              // wgrad A: output rows wm 128 ..
+  const uint32_t rmb0 = kOpBytes + rm0 + wn * 256;   // B: output columns wn 128 ..
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  f32x4 acc[kMI][kNI];
+  uint32_t rd_so = 0;
+  auto set_read_slot = [&](int slot) { rd_so = lds_base + (slot % kStages) * kStageBytes; };
+  bf16x8 fa[2][kMI], fb[2][kNI];
+  // RM fragment of 16-column block blk, K half ks (base: slot + operand + lane).
+  auto rm_frag = [&](uint32_t base, uint32_t x, int blk, int ks) -> bf16x8 {
+    const uint32_t a = base + ((static_cast<uint32_t>(blk) * 32u) ^ x) + ks * 32 * kRMRow;
+    return read_rm_frag(a);
+  };
+  // A fragments of row blocks 4 ih .. 4 ih + 3 / all B fragments of K half ks.
+  auto read_a = [&](int ks, int ih) {
+    if constexpr (kWgrad) {
+      uint32_t x = rmx;
+      asm volatile("" : "+v"(x));
+      const uint32_t base = rd_so + rma0;
+#pragma unroll
+      for (int i = 4 * ih; i < 4 * ih + 4; ++i) fa[ks][i] = rm_frag(base, x, i, ks);
+    } else {
+      const uint32_t base = (rd_so + fa0) ^ (ks << 6);
+#pragma unroll
+      for (int i = 4 * ih; i < 4 * ih + 4; ++i)
+        fa[ks][i] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)(base + i * 16 * kKCRow));
+    }
+  };
+  auto read_b = [&](int ks) {
+    uint32_t x = rmx;
+    asm volatile("" : "+v"(x));
+    const uint32_t base = rd_so + rmb0;
+#pragma unroll
+    for (int j = 0; j < kNI; ++j) fb[ks][j] = rm_frag(base, x, j, ks);
+  };
+  auto read_all = [&]() {
+    read_a(0, 0);
+    read_a(0, 1);
+    read_b(0);
+    read_a(1, 0);
+    read_a(1, 1);
+    read_b(1);
+  };
+  // The step's last unit (K half 1, row blocks 4..7) column by column: after
+  // column block j's 4 MFMAs its B fragment is free and the next stage's is
+  // read into it (with A blocks 0..3, freed by the unit before).
+  auto last_unit_reads = [&]() {
+    uint32_t x = rmx;
+    asm volatile("" : "+v"(x));
+    const uint32_t base_b = rd_so + rmb0;
+    const uint32_t base_a = kWgrad ? rd_so + rma0 : (rd_so + fa0) ^ (1 << 6);
+#pragma unroll
+    for (int j = 0; j < kNI; ++j) {
+#pragma unroll
+      for (int i = 4; i < 8; ++i) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[1][j], fa[1][i], acc[i][j], 0, 0, 0);
+      }
+      fb[1][j] = rm_frag(base_b, x, j, 1);
+      if (j < 4) {
+        if constexpr (kWgrad) {
+          fa[1][j] = rm_frag(base_a, x, j, 1);
+        } else {
+          fa[1][j] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)(base_a + j * 16 * kKCRow));
+        }
+      }
+    }
+  };
+  // 32 MFMAs: K half ks, row blocks 4 ih .. 4 ih + 3, all column blocks.
+  auto mfma_unit = [&](int ks, int ih, bool zero) {
+#pragma unroll
+    for (int i = 4 * ih; i < 4 * ih + 4; ++i)
+#pragma unroll
+      for (int j = 0; j < kNI; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[ks][j], fa[ks][i], zero ? f32x4{} : acc[i][j], 0, 0, 0);
+  };
+
+  // Epilogue of tile t from the accumulators: register r of lane l in block
+  // (i, j) holds output row i * 16 + l % 16 and column j * 16 + 4 (l / 16) + r
+  // of this wave's part. Stores go through a resource over the wave's valid
+  // rows (rows past it are dropped); columns past K get an offset past it.
+  auto epilogue = [&](const Tile &t) {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int eq = ln >> 4;
+    const int64_t gbase = kWgrad ? static_cast<int64_t>(t.g) * N * K : 0;
+    const int kcols = static_cast<int>(k32);
+    if constexpr (kOut == 0) {
+      // One resource over the tile's valid rows (below 2^31 bytes: K < 2^22).
+      const uint32_t ld = k32 * 2u;
+      const __amdgpu_buffer_rsrc_t ro = make_rsrc(static_cast<const uint16_t *>(p.out) + gbase + static_cast<int64_t>(t.i0) * K,
+                                                  static_cast<uint32_t>(t.rows_valid) * ld);
+      // After rounding, a block is two packed words per lane; v_permlane16_swap
+      // trades rows (16 lanes) 1 and 3 of block j's words with rows 0 and 2 of
+      // block j + 1's, so lanes of row q hold the 8 consecutive columns
+      // (q / 2) 8 .. + 7 of block j + q % 2.
+      const int wcol0 = static_cast<int>(t.nt) * kBN + wn * 128 + (eq & 1) * 16 + (eq >> 1) * 8;
+#pragma unroll
+      for (int i = 0; i < kMI; ++i) {
+        const uint32_t orow = static_cast<uint32_t>(wm * 128 + i * 16 + (ln & 15));
+#pragma unroll
+        for (int jp = 0; jp < kNI; jp += 2) {
+          uint32_t w[2][2];
+#pragma unroll
+          for (int d = 0; d < 2; ++d) {
+            const bf16x2 lo = {(__bf16)acc[i][jp + d][0], (__bf16)acc[i][jp + d][1]};
+            const bf16x2 hi = {(__bf16)acc[i][jp + d][2], (__bf16)acc[i][jp + d][3]};
+            w[d][0] = __builtin_bit_cast(uint32_t, lo);
+            w[d][1] = __builtin_bit_cast(uint32_t, hi);
+          }
+          u32x4 o;
+#if defined(__HIP_DEVICE_COMPILE__)
+          const auto s0 = __builtin_amdgcn_permlane16_swap(w[0][0], w[1][0], false, false);
+          const auto s1 = __builtin_amdgcn_permlane16_swap(w[0][1], w[1][1], false, false);
+          o = u32x4{s0[0], s1[0], s0[1], s1[1]};
+#else
+          o = u32x4{0u, 0u, 0u, 0u};
+#endif
+          const int gcol = wcol0 + jp * 16;
+          const uint32_t off = gcol < kcols ? orow * ld + static_cast<uint32_t>(gcol) * 2u : kNoAccess;
+#if defined(__HIP_DEVICE_COMPILE__)
+          __builtin_amdgcn_raw_buffer_store_b128(o, ro, static_cast<int>(off), 0, 0);
+#else
+          (void)off;
+          (void)ro;
+          (void)o;
+#endif
+        }
+        // One row block at a time: bounds the registers the epilogue holds.
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      // fp32: 4 consecutive columns per lane and block, stored as 16 bytes
+      // through a resource over the wave's valid rows (below 2^31 bytes: K < 2^22).
+      const int64_t wrow0 = t.i0 + wm * 128;
+      const int rows_out = max(min(t.rows_valid - wm * 128, 128), 0);
+      const uint32_t ld = k32 * 4u;
+      const __amdgpu_buffer_rsrc_t ro = make_rsrc(static_cast<float *>(p.out) + gbase + (rows_out > 0 ? wrow0 * K : 0),
+                                                  static_cast<uint32_t>(rows_out) * ld);
+      const int wcol0 = static_cast<int>(t.nt) * kBN + wn * 128 + eq * 4;
+#pragma unroll
+      for (int i = 0; i < kMI; ++i) {
+        const uint32_t orow = static_cast<uint32_t>(i * 16 + (ln & 15));
+#pragma unroll
+        for (int j = 0; j < kNI; ++j) {
+          const int gcol = wcol0 + j * 16;
+          const uint32_t off = gcol < kcols ? orow * ld + static_cast<uint32_t>(gcol) * 4u : kNoAccess;
+          const u32x4 v = {__float_as_uint(acc[i][j][0]), __float_as_uint(acc[i][j][1]),
+                           __float_as_uint(acc[i][j][2]), __float_as_uint(acc[i][j][3])};
+#if defined(__HIP_DEVICE_COMPILE__)
+          __builtin_amdgcn_raw_buffer_store_b128(v, ro, static_cast<int>(off), 0, 0);
+#else
+          (void)off;
+          (void)v;
+          (void)ro;
+#endif
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+
+  // The part of a reduction step after its barrier: MFMA units 1-3 of the
+  // fragments in VGPRs, the next stage's fragments read from the LDS slot set
+  // by set_read_slot into the registers each unit frees, and the DMA of stage
+  // `kdma` (of the tile set up last) into ring slot `wr`.
+  auto step_body = [&](bool zero, int kdma, int wr) __attribute__((always_inline)) {
+    mfma_unit(0, 1, zero);
+    read_a(0, 0);
+    issue_half(kdma, wr, 0);
+    sched_mix<32, 4 * kAR, kDma>();
+    mfma_unit(1, 0, false);
+    read_a(0, 1);
+    read_b(0);
+    issue_half(kdma, wr, 1);
+    sched_mix<32, 4 * kAR + 2 * kNI, kDma>();
+    last_unit_reads();
+    sched_mix<32, 2 * kNI + 4 * kAR, 0>();
+    read_a(1, 1);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // ---- first tile: stages 0 and 1 in flight, stage 0 read into VGPRs
+  Tile cur{}, nxt{};
+  if (!find_tile(0, cur)) return;
+  setup_dma(cur);
+  issue_half(0, 0, 0);
+  issue_half(0, 0, 1);
+  issue_half(1, 1, 0);
+  issue_half(1, 1, 1);
+  bool more = find_tile(1, nxt);
+  wait_vm_n<2 * kDma>();
+  barrier();
+  set_read_slot(0);
+  read_all();
+
+  int sb = 0;  // ring slot of the current tile's stage 0
+  for (uint32_t round = 0;; ++round) {
+    const int ktiles = cur.ktiles;
+    // One reduction step: MFMAs of stage kt (fragments in VGPRs), fragments of
+    // stage kt + 1 read from LDS, DMA of the stage two ahead (this tile's
+    // kt + 2 or, past its end, the next tile's kt + 2 - ktiles) into the slot of stage kt.
+    auto step = [&](int kt, bool first, bool last) __attribute__((always_inline)) {
+      mfma_unit(0, 0, first);
+      __builtin_amdgcn_sched_barrier(0);
+      // Stage kt + 1 has landed. In a tile's first step the previous tile's
+      // bf16 output stores were issued after it and may still be in flight.
+      if (first && round > 0 && kStores > 0) {
+        wait_vm_n<kStores>();
+      } else {
+        wait_dma();
+      }
+      wait_lds();
+      barrier();
+      // The second-to-last step DMAs the next tile's stage 0 (without a next
+      // tile it re-reads this tile's last stage into the free slot).
+      if (last && more) setup_dma(nxt);
+      const int kdma = !last ? kt + 2 : (more ? 0 : ktiles - 1);
+      set_read_slot(sb + kt + 1);
+      step_body(first, kdma, sb + kt + 2);
+    };
+    step(0, true, false);
+    for (int kt = 1; kt + 2 < ktiles; ++kt) step(kt, false, false);
+    step(ktiles - 2, false, true);
+
+    // Last step of the tile: it reads the next tile's stage 0 (DMA'd in the
+    // step above) and DMAs its stage 1 (without a next tile: reads and DMA of
+    // data nobody uses, so the code has no branch).
+    mfma_unit(0, 0, false);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_dma();
+    wait_lds();
+    barrier();
+    set_read_slot(sb + ktiles);
+    step_body(false, more ? 1 : ktiles - 1, sb + ktiles + 1);
+    epilogue(cur);
+    __builtin_amdgcn_sched_barrier(0);
+    if (!more) break;
+    cur = nxt;
+    sb += ktiles;
+    more = find_tile(round + 2, nxt);
+  }
+  wait_dma();  // no LDS DMA outlives the workgroup
+}
+
+template <bool kWgrad, int kOut = 0>
+void launch_pipe(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
+  int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
+  grid = std::max<int64_t>(8, (grid + 7) / 8 * 8);
+  grouped_gemm_bwd_pipe_kernel<kWgrad, kOut><<<dim3(grid), dim3(256), 0, s>>>(p);
+}
+
 template <bool kWgrad, int kBM, int kWavesM, int kStages, int kOut = 0>
 void launch(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
   int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
@@ -613,6 +1055,7 @@ int check_common(const char *fn, int64_t M_total, int64_t N, int64_t K, int64_t 
                 (long long)N, (long long)K, (long long)G);
   }
   if (G < 1 || G > 4096) return fail(MOE_ERR_CAPACITY, "%s: G=%lld outside [1, 4096]", fn, (long long)G);
+  if (M_total > (int64_t(1) << 31) - 1) return fail(MOE_ERR_CAPACITY, "%s: M=%lld rows exceed 2^31 - 1", fn, (long long)M_total);
   if (N % 8 != 0 || K % 8 != 0) {
     return fail(MOE_ERR_SHAPE, "%s: N=%lld and K=%lld must be multiples of 8", fn, (long long)N, (long long)K);
   }
@@ -657,11 +1100,12 @@ int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, con
   p.chunk = 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   // 128-row tiles when the groups average at most 160 rows (less padding in
-  // every group's last row tile), 256-row tiles otherwise.
-  if (M_total <= 160 * G) {
+  // every group's last row tile) and for reductions that are not whole steps
+  // of at least three (N % 64 != 0 or N < 192); the pipelined 256-row kernel otherwise.
+  if (M_total <= 160 * G || N % kBK != 0 || N < 3 * kBK) {
     launch<false, 128, 1, 3>(p, (ceil_div(M_total, 128) + G) * p.ntiles, s);
   } else {
-    launch<false, 256, 2, 2>(p, (ceil_div(M_total, 256) + G) * p.ntiles, s);
+    launch_pipe<false>(p, (ceil_div(M_total, 256) + G) * p.ntiles, s);
   }
   return check_launch(fn);
 }
@@ -698,7 +1142,7 @@ int moe_grouped_gemm_wgrad(const moe_bf16_t *dy, const moe_bf16_t *x, int64_t M_
   p.G = G;
   p.ntiles = ceil_div(K, kBN);
   p.chunk = 0;
-  launch<true, 256, 2, 2>(p, G * ceil_div(N, 256) * p.ntiles, static_cast<hipStream_t>(stream));
+  launch_pipe<true>(p, G * ceil_div(N, 256) * p.ntiles, static_cast<hipStream_t>(stream));
   return check_launch(fn);
 }
 
@@ -752,8 +1196,8 @@ int moe_router_dgrad_tf32(const float *grad_output, int64_t M, int64_t K, const 
   p.G = 1;
   p.ntiles = ceil_div(N, kBN);
   p.chunk = M;
-  if (M <= 160) launch<false, 128, 1, 3, 1>(p, (ceil_div(M, 128) + 1) * p.ntiles, s);
-  else launch<false, 256, 2, 2, 1>(p, (ceil_div(M, 256) + 1) * p.ntiles, s);
+  if (M <= 160 || (3 * K) % kBK != 0 || 3 * K < 3 * kBK) launch<false, 128, 1, 3, 1>(p, (ceil_div(M, 128) + 1) * p.ntiles, s);
+  else launch_pipe<false, 1>(p, (ceil_div(M, 256) + 1) * p.ntiles, s);
   return check_launch(fn);
 }
 
@@ -762,35 +1206,30 @@ int moe_router_dgrad_tf32(const float *grad_output, int64_t M, int64_t K, const 
 namespace {
 
 // Reduction split of the tf32 router wgrad: the output has few tiles
-// (case31: 2 x 32 for 256 CUs), so the 2M + M stacked rows are cut into
-// uniform chunks run as groups of one launch each, every chunk writing its own
-// fp32 partial [N, K]; a last pass adds the partials in chunk order.
+// (case31: 2 x 32 for 256 CUs), so the 3M stacked rows are cut into uniform
+// chunks run as groups of one launch, every chunk writing its own fp32 partial
+// [N, K]; a last pass adds the partials in chunk order.
 struct WgradPlan {
-  int64_t s1, s2;       // chunks of pass 1 (2M rows) and pass 2 (M rows); 1 and 1 = no split
-  int64_t c1, c2;       // rows per chunk
+  int64_t s;  // chunks (1 = no split)
+  int64_t c;  // rows per chunk
 };
 
 WgradPlan wgrad_plan(int64_t M, int64_t N, int64_t K) {
-  WgradPlan pl{1, 1, 2 * M, M};
+  const int64_t rows = 3 * M;
+  WgradPlan pl{1, rows};
   const int64_t tiles = moe::ceil_div(N, 256) * moe::ceil_div(K, 256);
   if (M == 0 || tiles >= 256) return pl;
-  auto chunks = [&](int64_t rows) {
-    int64_t s = std::min<int64_t>(moe::ceil_div(512, tiles), std::max<int64_t>(1, rows / 512));
-    return std::max<int64_t>(1, std::min<int64_t>(s, 64));
-  };
-  pl.s1 = chunks(2 * M);
-  pl.s2 = chunks(M);
-  if (pl.s1 == 1 && pl.s2 == 1) return pl;
+  int64_t s = std::min<int64_t>(moe::ceil_div(512, tiles), std::max<int64_t>(1, rows / 512));
+  s = std::max<int64_t>(1, std::min<int64_t>(s, 64));
+  if (s == 1) return pl;
   // Chunks are multiples of 64 rows (whole reduction steps).
-  pl.c1 = moe::ceil_div(moe::ceil_div(2 * M, pl.s1), 64) * 64;
-  pl.c2 = moe::ceil_div(moe::ceil_div(M, pl.s2), 64) * 64;
-  pl.s1 = moe::ceil_div(2 * M, pl.c1);
-  pl.s2 = moe::ceil_div(M, pl.c2);
+  pl.c = moe::ceil_div(moe::ceil_div(rows, s), 64) * 64;
+  pl.s = moe::ceil_div(rows, pl.c);
   return pl;
 }
 
 size_t wgrad_planes_bytes(const WgradPlan &pl, int64_t N, int64_t K) {
-  return (pl.s1 == 1 && pl.s2 == 1) ? 0 : moe::align_up(static_cast<size_t>(pl.s1 + pl.s2) * N * K * 4);
+  return pl.s == 1 ? 0 : moe::align_up(static_cast<size_t>(pl.s) * N * K * 4);
 }
 
 }  // namespace
@@ -799,8 +1238,8 @@ extern "C" {
 
 size_t moe_router_wgrad_tf32_workspace_size(int64_t M, int64_t N, int64_t K) {
   if (M < 0 || N < 0 || K < 0) return 0;
-  return moe::align_up(static_cast<size_t>(2 * M) * N * 2) + moe::align_up(static_cast<size_t>(M) * N * 2) +
-         moe::align_up(static_cast<size_t>(2 * M) * K * 2) + wgrad_planes_bytes(wgrad_plan(M, N, K), N, K);
+  return moe::align_up(static_cast<size_t>(3 * M) * N * 2) + moe::align_up(static_cast<size_t>(3 * M) * K * 2) +
+         wgrad_planes_bytes(wgrad_plan(M, N, K), N, K);
 }
 
 int moe_router_wgrad_tf32(const float *grad_output, int64_t M, int64_t N, const float *inp, int64_t K,
@@ -811,8 +1250,8 @@ int moe_router_wgrad_tf32(const float *grad_output, int64_t M, int64_t N, const 
     return fail(MOE_ERR_SHAPE, "%s: negative size (M=%lld N=%lld K=%lld)", fn, (long long)M, (long long)N, (long long)K);
   }
   if (K % 8 != 0 || N % 8 != 0) return fail(MOE_ERR_SHAPE, "%s: N=%lld and K=%lld must be multiples of 8", fn, (long long)N, (long long)K);
-  if (2 * M * N > (int64_t(1) << 30) - 1 || 2 * M * K > (int64_t(1) << 30) - 1 || N * K > (int64_t(1) << 30) - 1) {
-    return fail(MOE_ERR_CAPACITY, "%s: M=%lld N=%lld K=%lld exceed the 32-bit offsets (2M*N, 2M*K, N*K < 2^30)", fn,
+  if (3 * M * N > (int64_t(1) << 30) - 1 || 3 * M * K > (int64_t(1) << 30) - 1 || N * K > (int64_t(1) << 30) - 1) {
+    return fail(MOE_ERR_CAPACITY, "%s: M=%lld N=%lld K=%lld exceed the 32-bit offsets (3M*N, 3M*K, N*K < 2^30)", fn,
                 (long long)M, (long long)N, (long long)K);
   }
   if (N == 0 || K == 0) return MOE_OK;
@@ -828,54 +1267,38 @@ int moe_router_wgrad_tf32(const float *grad_output, int64_t M, int64_t N, const 
                 workspace == nullptr ? size_t(0) : workspace_bytes);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // Pass 1: [A_hi; A_hi]^T [B_hi; B_lo] over 2M stacked rows; pass 2:
-  // A_lo^T B_hi.  A = grad_output [M, N], B = inp [M, K].
+  // One wgrad over 3M stacked rows: [A_hi; A_hi; A_lo]^T [B_hi; B_lo; B_hi] =
+  // A_hi^T B_hi + A_hi^T B_lo + A_lo^T B_hi.  A = grad_output [M, N], B = inp [M, K].
   char *w = static_cast<char *>(workspace);
-  const size_t sz_a1 = align_up(static_cast<size_t>(2 * M) * N * 2), sz_a2 = align_up(static_cast<size_t>(M) * N * 2);
-  const size_t sz_b1 = align_up(static_cast<size_t>(2 * M) * K * 2);
-  uint16_t *a1 = reinterpret_cast<uint16_t *>(w);
-  uint16_t *a2 = reinterpret_cast<uint16_t *>(w + sz_a1);
-  uint16_t *b1 = reinterpret_cast<uint16_t *>(w + sz_a1 + sz_a2);
-  float *planes = reinterpret_cast<float *>(w + sz_a1 + sz_a2 + sz_b1);
+  const size_t sz_a = align_up(static_cast<size_t>(3 * M) * N * 2), sz_b = align_up(static_cast<size_t>(3 * M) * K * 2);
+  uint16_t *a3 = reinterpret_cast<uint16_t *>(w);
+  uint16_t *b3 = reinterpret_cast<uint16_t *>(w + sz_a);
+  float *planes = reinterpret_cast<float *>(w + sz_a + sz_b);
   if (M > 0) {
-    SplitArgs sa{grad_output, M, N, a1, a1 + M * N, a2, N, N, N};
-    SplitArgs sb{inp, M, K, b1, nullptr, b1 + M * K, K, 0, K};
+    SplitArgs sa{grad_output, M, N, a3, a3 + M * N, a3 + 2 * M * N, N, N, N};
+    SplitArgs sb{inp, M, K, b3, b3 + 2 * M * K, b3 + M * K, K, K, K};
     launch_split(sa, s);
     launch_split(sb, s);
     if (int rc = check_launch(fn)) return rc;
   }
   const WgradPlan pl = wgrad_plan(M, N, K);
-  const bool split = !(pl.s1 == 1 && pl.s2 == 1);
+  const bool split = pl.s > 1;
   BwdArgs p;
-  p.a = a1;
-  p.b = b1;
+  p.a = a3;
+  p.b = b3;
   p.offsets = nullptr;
   p.out = split ? static_cast<void *>(planes) : static_cast<void *>(grad_weight);
-  p.M = 2 * M;
+  p.M = 3 * M;
   p.N = N;
   p.K = K;
-  p.G = pl.s1;
+  p.G = pl.s;
   p.ntiles = ceil_div(K, kBN);
-  p.chunk = pl.c1;
-  const int64_t tiles = ceil_div(N, 256) * p.ntiles;
-  launch<true, 256, 2, 2, 1>(p, tiles * p.G, s);
-  if (M > 0) {
-    p.a = a2;
-    p.M = M;
-    p.G = pl.s2;
-    p.chunk = pl.c2;
-    if (split) {
-      p.out = planes + pl.s1 * N * K;
-      launch<true, 256, 2, 2, 1>(p, tiles * p.G, s);
-    } else {
-      launch<true, 256, 2, 2, 2>(p, tiles, s);
-    }
-  }
+  p.chunk = pl.c;
+  launch_pipe<true, 1>(p, ceil_div(N, 256) * p.ntiles * p.G, s);
   if (split) {
     const int64_t q = N * K / 4;
     const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(ceil_div(q, 256), 4096));
-    sum_planes_kernel<<<dim3(grid), dim3(256), 0, s>>>(planes, static_cast<int>(pl.s1 + (M > 0 ? pl.s2 : 0)), N * K,
-                                                       grad_weight);
+    sum_planes_kernel<<<dim3(grid), dim3(256), 0, s>>>(planes, static_cast<int>(pl.s), N * K, grad_weight);
   }
   return check_launch(fn);
 }

@@ -263,8 +263,8 @@ int moe_grouped_gemm_gather(const moe_bf16_t *x, int64_t x_rows, const int32_t *
  *   w   bf16 [G, N, K]    (the forward's [out, in] weights; dx = dy @ w[g])
  *   group_offsets int32 [G + 1] on the device, as moe_grouped_gemm
  *   dx  bf16 [M_total, K] (rows beyond group_offsets[G] are not written)
- * Limits: N % 8 == 0, K % 8 == 0, 1 <= G <= 4096, N, K < 2^22, N * K < 2^30;
- *   dy, w, dx 16-byte aligned. N == 0 gives zeros.
+ * Limits: N % 8 == 0, K % 8 == 0, 1 <= G <= 4096, M_total < 2^31, N, K < 2^22,
+ *   N * K < 2^30; dy, w, dx 16-byte aligned. N == 0 gives zeros.
  * Workspace: none (pass NULL, 0). */
 int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, const moe_bf16_t *w,
                            int64_t G, int64_t K, const int32_t *group_offsets, moe_bf16_t *dx,
@@ -334,9 +334,10 @@ int moe_cast_f32_to_bf16(const float *src, int64_t n, moe_bf16_t *dst, void *str
  *   dgrad: grad_input [M, N] = tf32(grad_output [M, K]) @ tf32(weight [K, N])
  *   wgrad: grad_weight [N, K] = tf32(grad_output [M, N])^T @ tf32(inp [M, K])
  * Limits: the column counts (K and N) % 8 == 0; dgrad 3K, N < 2^22 and
- *   3K*N < 2^30; wgrad 2M*N, 2M*K, N*K < 2^30; 16-byte aligned tensors.
+ *   3K*N < 2^30; wgrad 3M*N, 3M*K, N*K < 2^30; 16-byte aligned tensors.
  * Workspace: the *_workspace_size bytes, 256-byte aligned (the bf16 hi/lo
- *   planes; case31: 2 M K + 3 M N bf16 values). */
+ *   planes, 3 M K + 3 M N bf16 values for the wgrad, plus fp32 partial sums
+ *   when its reduction is split over chunks). */
 size_t moe_router_dgrad_tf32_workspace_size(int64_t M, int64_t K, int64_t N);
 int moe_router_dgrad_tf32(const float *grad_output, int64_t M, int64_t K, const float *weight, int64_t N,
                           float *grad_input, void *workspace, size_t workspace_bytes, void *stream);
