@@ -76,27 +76,6 @@ __device__ __forceinline__ void dma16b(__amdgpu_buffer_rsrc_t rsrc, lds_void *ld
 #endif
 }
 
-// Instruction-group order for one sub-step: each of the first 8 MFMAs followed
-// by one instruction of kind kFirst (0x100 LDS read, 0x020 vector-memory read),
-// each of the last 8 by one of kind kSecond (0 = none).
-template <int kFirst, int kSecond>
-__device__ __forceinline__ void sched_pattern() {
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kFirst, 1, 0);
-  }
-  if constexpr (kSecond != 0) {
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSecond, 1, 0);
-    }
-  } else {
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-  }
-}
-
 // Instruction-group order spreading kReads LDS reads and kVmem vector-memory
 // reads evenly behind kMfma MFMAs.
 template <int kMfma, int kReads, int kVmem, int kR = 0>

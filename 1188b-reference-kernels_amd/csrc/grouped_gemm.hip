@@ -22,11 +22,11 @@
 //   * LDS rows are XOR-swizzled in 16-byte chunks (chunk ^ (row / 2) % 8), which
 //     makes both the DMA writes (lane-linear 1 KiB blocks) and the MFMA operand
 //     reads (16 lanes x 16 B) bank-conflict-free;
-//   * the operand fragments of a whole K step live in VGPRs: while the MFMAs of
-//     step kt run from them, the fragments of step kt + 1 are read from LDS one
-//     sub-step at a time, and the DMA of step kt + 2 is issued, one instruction
-//     after each MFMA (instruction-group scheduling); one workgroup barrier per
-//     step, after the first sub-step's MFMAs;
+//   * operand fragments in two register sets of one MFMA sub-step (K 16)
+//     each: while the MFMAs of one set run, the other set's next sub-step is
+//     read from LDS; one workgroup barrier per K step, after its second
+//     sub-step, then the DMA of step kt + 2 goes out under the MFMAs of
+//     sub-steps 2 and 3 (instruction-group scheduling);
 //   * w is the MFMA's first operand, so the accumulators hold the transposed
 //     block and each lane owns 4 consecutive output columns per 4 registers:
 //     the epilogue rounds them to bf16 in hardware (RNE) and writes 8-byte
@@ -71,7 +71,6 @@ constexpr int kOperandBytes = 256 * kRowBytes;    // 32 KiB: one 256-row operand
 constexpr int kStageBytes = 2 * kOperandBytes;    // A + B
 constexpr int kStages = 2;
 constexpr int kRowsPerKiB = 1024 / kRowBytes;     // 8 rows per DMA instruction
-constexpr int kSubSteps = kBK / 16;               // MFMA K sub-steps per K step
 
 struct GemmArgs {
   const uint16_t *a;       // A rows, or the gather source x [a_src_rows, K]
@@ -101,11 +100,9 @@ __device__ __forceinline__ int64_t b_row_clamped(int64_t nt, int r, int64_t ncol
 
 
 // Four wavefronts (one per SIMD), each 128 x 128 of the 256 x 256 tile as 4 x 4
-// blocks of 32 x 32. The operand fragments of a whole K step (4 sub-steps x 8
-// fragments) live in VGPRs: while the MFMAs of step kt run from them, the
-// fragments of step kt + 1 are read from LDS sub-step by sub-step. One barrier
-// per step, after the first sub-step's MFMAs, publishes stage kt + 1 (its DMA
-// has landed) and frees the LDS slot of stage kt for the DMA of stage kt + 2.
+// blocks of 32 x 32. Fragments of two MFMA sub-steps (K 16 each) live in VGPRs.
+// One barrier per step, after its second sub-step, publishes stage kt + 1 (its
+// DMA has landed) and frees the LDS slot of stage kt for the DMA of stage kt + 2.
 template <bool kSwiglu, bool kGather>
 __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
   constexpr int kWaves = 4;
@@ -139,27 +136,6 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
   group_rows(0, m_lo, m_hi);
   int64_t mt_g = ceil_div(m_hi - m_lo, kBM);
 
-  const int dma_row = lane / kChunks;
-  const int dma_pchunk = lane % kChunks;
-
-  int fa_base[kMI], fb_base[kNI];
-#pragma unroll
-  for (int i = 0; i < kMI; ++i) {
-    const int r = wm * 128 + i * 32 + (lane & 31);
-    fa_base[i] = r * kRowBytes | (swz(r) << 4);
-  }
-#pragma unroll
-  for (int j = 0; j < kNI; ++j) {
-    int r;
-    if constexpr (kSwiglu) {
-      const int jj = j % (kNI / 2);
-      r = (j < kNI / 2 ? 0 : 128) + wn * 64 + jj * 32 + (lane & 31);
-    } else {
-      r = wn * 128 + j * 32 + (lane & 31);
-    }
-    fb_base[j] = r * kRowBytes | (swz(r) << 4);
-  }
-  const int khalf = lane >> 5;
 
   for (int64_t round = 0;; ++round) {
     const int64_t L = round * P + (b % 8) * (P / 8) + b / 8;
@@ -172,6 +148,21 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
       }
     }
     if (g_cur >= p.G) break;
+    // Per-lane values from an opaque copy of the lane index, recomputed per
+    // tile rather than hoisted out of the tile loop (where they would stay
+    // live across the K loop and spill).
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    // Fragment rows 32 apart share the swizzle ((row / 2) % 8 changes by 16), so
+    // block i (j) of a wave lies at its first block's address + i (j) x 32 rows
+    // (an immediate ds_read offset): one address register per operand. SwiGLU
+    // tiles: B blocks 0, 1 are gate rows wn 64 .., blocks 2, 3 the up rows 128 further.
+    const int fra = wm * 128 + (ln & 31);
+    const int frb = (kSwiglu ? wn * 64 : wn * 128) + (ln & 31);
+    const uint32_t fa0 = fra * kRowBytes | (swz(fra) << 4);
+    const uint32_t fb0 = frb * kRowBytes | (swz(frb) << 4);
+    auto b_blk_rows = [](int j) { return kSwiglu ? (j / (kNI / 2)) * 128 + (j % (kNI / 2)) * 32 : j * 32; };
+    const int khalf = ln >> 5;
 
     // Position inside the group (32-bit: a group's tile count exceeds 2^32 only
     // for outputs of more than 2^48 elements).
@@ -200,6 +191,8 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
                 : make_rsrc(p.a + row0 * K, static_cast<uint32_t>(rows_valid * K * 2));
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(wg, static_cast<uint32_t>(p.N * K * 2));
     int a_off[kDma], b_off[kDma];
+    const int dma_row = ln / kChunks;
+    const int dma_pchunk = ln % kChunks;
 #pragma unroll
     for (int j = 0; j < kDma; ++j) {
       const int blk = j * kWaves + wave;
@@ -261,31 +254,31 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
 
     // LDS byte addresses of this lane's fragment rows in the slot read next
     // (logical chunk khalf); sub-step ks reads chunk 2 ks + khalf = addr ^ (ks << 5).
-    uint32_t rd_a[kMI], rd_b[kNI];
+    uint32_t rd_a = 0, rd_b = 0;
     auto set_read_slot = [&](int kt) {
       const uint32_t so = lds_base + (kt % kStages) * kStageBytes;
-#pragma unroll
-      for (int i = 0; i < kMI; ++i) rd_a[i] = so + (fa_base[i] ^ (khalf << 4));
-#pragma unroll
-      for (int j = 0; j < kNI; ++j) rd_b[j] = so + kOperandBytes + (fb_base[j] ^ (khalf << 4));
+      rd_a = so + (fa0 ^ (khalf << 4));
+      rd_b = so + kOperandBytes + (fb0 ^ (khalf << 4));
     };
-    bf16x8 fa[kSubSteps][kMI], fb[kSubSteps][kNI];
+    // Two register sets of fragments: sub-steps 0 and 2 of a stage use set 0,
+    // 1 and 3 set 1.
+    bf16x8 fa[2][kMI], fb[2][kNI];
     auto read_frags = [&](int ks) {
 #pragma unroll
       for (int i = 0; i < kMI; ++i)
-        fa[ks][i] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)(rd_a[i] ^ (ks << 5)));
+        fa[ks & 1][i] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)((rd_a ^ (ks << 5)) + i * 32 * kRowBytes));
 #pragma unroll
       for (int j = 0; j < kNI; ++j)
-        fb[ks][j] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)(rd_b[j] ^ (ks << 5)));
+        fb[ks & 1][j] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)((rd_b ^ (ks << 5)) + b_blk_rows(j) * kRowBytes));
     };
-    auto mfma_ks = [&](int ks) {
+    auto mfma_set = [&](int set) {
 #pragma unroll
       for (int i = 0; i < kMI; ++i)
 #pragma unroll
         for (int j = 0; j < kNI; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks][j], fa[ks][i], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[set][j], fa[set][i], acc[i][j], 0, 0, 0);
     };
-    // Prologue: stages 0 and 1 in flight; stage 0 published and read into VGPRs.
+    // Prologue: stages 0 and 1 in flight; sub-steps 0 and 1 of stage 0 read into VGPRs.
     barrier();  // the previous tile's epilogue is done with the LDS
     issue_stage(0);
     if (ktiles > 1) {
@@ -301,14 +294,21 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
       barrier();
     }
     set_read_slot(0);
-#pragma unroll
-    for (int ks = 0; ks < kSubSteps; ++ks) read_frags(ks);
+    read_frags(0);
+    read_frags(1);
 
+    // Step kt: sub-steps 0 and 1 of stage kt while its sub-steps 2 and 3 are
+    // read; one barrier (stage kt + 1 has landed, every wave is done reading
+    // stage kt); sub-steps 2 and 3 while the DMA of stage kt + 2 is issued into
+    // the slot of stage kt and sub-steps 0 and 1 of stage kt + 1 are read.
     for (int kt = 0; kt + 1 < ktiles; ++kt) {
-      mfma_ks(0);
+      mfma_set(0);
+      read_frags(2);
+      sched_mix<kMI * kNI, kMI + kNI, 0>();
+      mfma_set(1);
+      read_frags(3);
+      sched_mix<kMI * kNI, kMI + kNI, 0>();
       __builtin_amdgcn_sched_barrier(0);
-      // This thread's DMA of stage kt + 1 has landed and its reads of stage kt
-      // are done; after the barrier, everyone's.
       wait_dma();
       wait_lds();
       barrier();
@@ -317,28 +317,26 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
         wait_lds();
         barrier();
       }
-      // Stage kt + 2 into the slot of stage kt (the last steps re-read the
+      // Stage kt + 2 into the slot of stage kt (the last step re-reads the
       // final stage into that free slot, so the region below has no branch).
       const int kdma = min(kt + 2, ktiles - 1);
-      set_read_slot(kt + 1);
-      read_frags(0);          // sub-step 0 of stage kt + 1 (its old fragments are used)
-      mfma_ks(1);
+      mfma_set(0);
       issue_half(kdma, kt + 2, 0);
-      sched_pattern<0x100, 0x020>();  // ks 1: the 8 reads above, then 8 DMAs of A
-      mfma_ks(2);
-      read_frags(1);
+      set_read_slot(kt + 1);
+      read_frags(0);
+      sched_mix<kMI * kNI, kMI + kNI, kDma>();
+      mfma_set(1);
       issue_half(kdma, kt + 2, 1);
-      sched_pattern<0x100, 0x020>();  // ks 2: reads of sub-step 1, then 8 DMAs of B
-      mfma_ks(3);
-      read_frags(2);
-      sched_pattern<0x100, 0>();      // ks 3: reads of sub-step 2
-      read_frags(3);
+      read_frags(1);
+      sched_mix<kMI * kNI, kMI + kNI, kDma>();
       __builtin_amdgcn_sched_barrier(0);
     }
-    mfma_ks(0);
-    mfma_ks(1);
-    mfma_ks(2);
-    mfma_ks(3);
+    mfma_set(0);
+    read_frags(2);
+    mfma_set(1);
+    read_frags(3);
+    mfma_set(0);
+    mfma_set(1);
     wait_dma();  // the re-reads of the last steps have landed before the LDS is reused
 
     barrier();  // every wave is done reading the last stage
@@ -348,13 +346,13 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
     // are rounded (RNE, hardware) and written to the LDS tile as one 8-byte word.
 #pragma unroll
     for (int i = 0; i < kMI; ++i) {
-      const int row = wm * 128 + i * 32 + (lane & 31);
+      const int row = wm * 128 + i * 32 + (ln & 31);
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         if constexpr (kSwiglu) {
 #pragma unroll
           for (int j = 0; j < kNI / 2; ++j) {
-            const int col = wn * 64 + j * 32 + g * 8 + (lane >> 5) * 4;
+            const int col = wn * 64 + j * 32 + g * 8 + (ln >> 5) * 4;
             float h[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -368,7 +366,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
         } else {
 #pragma unroll
           for (int j = 0; j < kNI; ++j) {
-            const int col = wn * 128 + j * 32 + g * 8 + (lane >> 5) * 4;
+            const int col = wn * 128 + j * 32 + g * 8 + (ln >> 5) * 4;
             const bf16x4 v = {(__bf16)acc[i][j][4 * g], (__bf16)acc[i][j][4 * g + 1], (__bf16)acc[i][j][4 * g + 2],
                               (__bf16)acc[i][j][4 * g + 3]};
             *reinterpret_cast<lds_bf16x4 *>(sbase + row * kEpiRow + col * 2) = v;
@@ -378,20 +376,25 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
     }
     wait_lds();
     barrier();
-    const int64_t col0 = nt * kEpiCols;
+    // 32-bit row and column arithmetic (ncols < 2^27: the host bounds N K
+    // below 2^30) from an opaque copy of the thread index.
+    int tq = tid;
+    asm volatile("" : "+v"(tq));
+    const int ncols32 = static_cast<int>(p.ncols);
+    const int col0 = static_cast<int>(nt) * kEpiCols;
+    uint16_t *const obase = p.out + row0 * p.ncols;
     constexpr int kChunksPerRow = kEpiCols / 8;
 #pragma unroll 4
-    for (int idx = tid; idx < kBM * kChunksPerRow; idx += kThreads) {
+    for (int idx = tq; idx < kBM * kChunksPerRow; idx += kThreads) {
       const int r = idx / kChunksPerRow, c = idx % kChunksPerRow;
-      const int64_t grow = row0 + r;
-      const int64_t gcol = col0 + c * 8;
-      if (grow >= m_hi || gcol >= p.ncols) continue;
+      const int gcol = col0 + c * 8;
+      if (r >= rows_valid || gcol >= ncols32) continue;
       const lds_char *src = sbase + r * kEpiRow + c * 16;
-      uint16_t *dst = p.out + grow * p.ncols + gcol;
-      if (p.vec_out && gcol + 8 <= p.ncols) {
+      uint16_t *dst = obase + static_cast<int64_t>(r) * p.ncols + gcol;
+      if (p.vec_out && gcol + 8 <= ncols32) {
         __builtin_nontemporal_store(*reinterpret_cast<const lds_u32x4 *>(src), reinterpret_cast<u32x4 *>(dst));
       } else {
-        for (int e = 0; e < 8 && gcol + e < p.ncols; ++e) dst[e] = *reinterpret_cast<const lds_u16 *>(src + 2 * e);
+        for (int e = 0; e < 8 && gcol + e < ncols32; ++e) dst[e] = *reinterpret_cast<const lds_u16 *>(src + 2 * e);
       }
     }
   }

@@ -15,29 +15,35 @@
 // index in memory: w[g] is [N][K] with the reduction over N, and in wgrad both
 // dy and x are reduced over their rows. Such an operand ("reduction-major",
 // RM) is staged in LDS as it lies in memory, 64 reduction rows x 256 columns
-// per stage (512-byte rows, 16-byte chunks XOR-swizzled by (row % 4) * 4), and
-// its MFMA fragments are read with ds_read_b64_tr_b16: in each group of 16
-// lanes, lane 4j + q addresses row j, columns 4q .. 4q + 3 of a 4 x 16 block
-// and lane i receives column i of rows 0..3, so two such reads give a lane the
-// 8 consecutive reduction values of one column that v_mfma_f32_32x32x16_bf16
-// takes. dgrad's dy is reduced along its rows' contiguous axis ("KC") and is
+// per stage (512-byte rows, 16-byte chunks XOR-swizzled per row), and its MFMA
+// fragments are read with ds_read_b64_tr_b16: in each group of 16 lanes,
+// lane 4j + q addresses row j, columns 4q .. 4q + 3 of a 4 x 16 block and
+// lane i receives column i of rows 0..3, so two such reads (rows 4 apart) give
+// a lane 8 consecutive reduction values of one column, the MFMA operand
+// layout. dgrad's dy is reduced along its rows' contiguous axis ("KC") and is
 // staged like the forward kernel's operands (128-byte rows, ds_read_b128).
 //
-// Kernel shape: persistent, one workgroup of 4 wavefronts per CU; output tile
-// kBM x 256 (kBM = 256: 2 x 2 waves of 128 x 128; kBM = 128: 1 x 4 waves of
-// 128 x 64, for groups of at most ~160 rows); reduction step 64; LDS ring of
-// two stages (three for 128-row tiles, whose stream of w is HBM-bound and needs
-// two stages in flight) filled by buffer_load ... lds ahead of the MFMAs; the next
-// step's fragments are read while the current step's MFMAs run (as in the
-// forward kernel). The accumulators hold the transposed block (the column
-// operand is the MFMA's first operand); the epilogue rounds to bf16 (RNE,
-// hardware), pairs register groups across the two half-waves with
-// v_permlane32_swap so each lane holds 8 consecutive columns, and stores 16
-// bytes per lane straight from registers through a buffer resource (stores
-// past the tile's valid rows or columns are dropped), after the next tile's
-// first stages have been issued. Reduction rows past the end come from past
-// the operand's buffer resource and read as zeros (dgrad's dy columns past N
-// are zeroed in LDS).
+// Two kernels, both persistent with one workgroup of 4 wavefronts per CU, a
+// reduction step of 64 and an LDS ring filled by buffer_load ... lds ahead of
+// the MFMAs:
+//   * grouped_gemm_bwd_pipe_kernel (every 256 x 256 tile: dgrad with groups
+//     above ~160 rows, wgrad, the tf32 router GEMMs): the forward pipelined
+//     kernel's shape, v_mfma_f32_16x16x32_bf16 on 2 x 2 waves of 128 x 128,
+//     two stages, tiles chained without draining the pipeline, epilogue from
+//     registers; described above the kernel;
+//   * grouped_gemm_dgrad128_kernel (dgrad with groups of at most ~160 rows, or
+//     a reduction that is not whole steps): 128 x 256 tiles (1 x 4 waves of
+//     128 x 64, less padding in every group's last row tile),
+//     v_mfma_f32_32x32x16_bf16, three stages (its stream of w is HBM-bound and
+//     needs two stages in flight); the next step's fragments are read while
+//     the current step's MFMAs run; the epilogue rounds to bf16 (RNE,
+//     hardware), pairs register groups across the two half-waves with
+//     v_permlane32_swap so each lane holds 8 consecutive columns, and stores
+//     16 bytes per lane straight from registers through a buffer resource
+//     (stores past the tile's valid rows or columns are dropped), after the
+//     next tile's first stages have been issued.
+// Reduction rows past the end come from past the operand's buffer resource and
+// read as zeros (the 128-row kernel zeroes dy's columns past N in LDS).
 //
 // Tiles are numbered group by group; inside a group in patches of 8 row tiles
 // x all column tiles; workgroup b takes tile round * P + (b % 8) * (P / 8) + b / 8
@@ -71,6 +77,8 @@ struct BwdArgs {
 };
 
 __device__ __forceinline__ int kc_swz(int row) { return (row >> 1) & 7; }
+// RM chunk swizzle of the 128-row kernel's 32 x 32 x 16 fragments (a half-wave
+// reads 4 rows x 64 bytes: (row % 4) x 4 chunks spreads them over all banks).
 __device__ __forceinline__ int rm_swz(int krow) { return (krow & 3) << 2; }
 
 // One transposing LDS read. The restrict-qualified pointer gives the access
@@ -99,27 +107,29 @@ __device__ __forceinline__ bf16x8 read_rm_frag(uint32_t addr) {
 #endif
 }
 
-// kOut: 0 = bf16 output, 1 = fp32 output, 2 = fp32 output added to what out
-// holds.  The fp32 outputs issue the next tile's stages after the stores.
-template <bool kWgrad, int kBM, int kWavesM, int kStages, int kOut>
-__global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
+// The 128-row dgrad kernel (groups of at most ~160 rows, reductions that are
+// not whole steps): 1 x 4 waves of 128 x 64, a three-stage ring (the stream of
+// w is HBM-bound here and needs two stages in flight), v_mfma_f32_32x32x16_bf16.
+// kOut: 0 = bf16 output, 1 = fp32 output (the next tile's stages are then
+// issued after the stores).
+template <int kOut>
+__global__ __launch_bounds__(256) void grouped_gemm_dgrad128_kernel(BwdArgs p) {
+  constexpr int kBM = 128, kWavesM = 1, kStages = 3;
   constexpr int kWaves = 4;
   constexpr int kWavesN = kWaves / kWavesM;
   constexpr int kWaveRows = kBM / kWavesM;
   constexpr int kWaveCols = kBN / kWavesN;
   constexpr int kMI = kWaveRows / 32, kNI = kWaveCols / 32;
-  constexpr bool kARM = kWgrad;                 // A (output rows) reduction-major
   constexpr int kABytes = kBM * kBK * 2;
   constexpr int kBBytes = kBN * kBK * 2;
   constexpr int kStageBytes = kABytes + kBBytes;
   constexpr int kDmaA = kABytes / 1024 / kWaves, kDmaB = kBBytes / 1024 / kWaves;
   constexpr bool kLate = kOut != 0;             // next tile's stages issued after the stores
   constexpr int kStores = kLate ? 0 : kMI * kNI * 2;  // stores younger than the next stages
-  constexpr int kReads = (kARM ? 2 * kMI : kMI) + 2 * kNI;  // LDS reads per sub-step
+  constexpr int kReads = kMI + 2 * kNI;          // LDS reads per sub-step
   constexpr int kMfma = kMI * kNI;              // MFMAs per sub-step
   static_assert(kStages * kStageBytes <= 160 * 1024, "LDS budget");
   static_assert(kStores + (kStages - 1) * (kDmaA + kDmaB) <= 63, "vmcnt range");
-  static_assert(!kARM || kBM == 256, "a reduction-major A tile is 256 columns wide");
   __shared__ __attribute__((aligned(1024))) char smem[kStages * kStageBytes];
   lds_char *const sbase = (lds_char *)smem;
   const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sbase));
@@ -132,7 +142,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
   const int64_t P = gridDim.x;
   const int64_t b = blockIdx.x;
   const int64_t N = p.N, K = p.K;
-  const bool a_ktail = !kWgrad && (N % kBK) != 0;  // dgrad: dy columns past N in the last step
+  const bool a_ktail = (N % kBK) != 0;  // dy columns past N in the last step
 
   // ---- tile walker
   auto group_range = [&](int64_t g, int64_t &lo, int64_t &hi) {
@@ -144,15 +154,13 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
     lo = min(max(static_cast<int64_t>(p.offsets[g]), int64_t(0)), p.M);
     hi = min(max(static_cast<int64_t>(p.offsets[g + 1]), lo), p.M);
   };
-  auto row_tiles = [&](int64_t lo, int64_t hi) -> int64_t {
-    return kWgrad ? ceil_div(N, kBM) : ceil_div(hi - lo, kBM);
-  };
+  auto row_tiles = [&](int64_t lo, int64_t hi) -> int64_t { return ceil_div(hi - lo, kBM); };
   int64_t g_cur = 0, tiles_before = 0, g_lo, g_hi;
   group_range(0, g_lo, g_hi);
   int64_t mt_g = row_tiles(g_lo, g_hi);
   struct Tile {
-    int64_t g, lo, hi;  // group and its row range (dgrad: output rows; wgrad: reduction rows)
-    int64_t i0;         // first output row of the tile (dgrad: in dx; wgrad: in dw[g])
+    int64_t g, lo, hi;  // group and its rows
+    int64_t i0;         // first output row of the tile
     uint32_t nt;        // column tile
     int ktiles;         // reduction steps (at least 1: an empty reduction reads zeros)
   };
@@ -183,10 +191,9 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
     t.g = g_cur;
     t.lo = g_lo;
     t.hi = g_hi;
-    t.i0 = (kWgrad ? 0 : g_lo) + static_cast<int64_t>(mt) * kBM;
+    t.i0 = g_lo + static_cast<int64_t>(mt) * kBM;
     t.nt = nt;
-    const int64_t red = kWgrad ? g_hi - g_lo : N;
-    t.ktiles = static_cast<int>(max(ceil_div(red, kBK), int64_t(1)));
+    t.ktiles = static_cast<int>(max(ceil_div(N, kBK), int64_t(1)));
     return true;
   };
 
@@ -197,19 +204,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
   auto setup_dma = [&](const Tile &t) {
     // RM operand lane map: DMA block blk holds reduction rows 2 blk, 2 blk + 1.
     const int rm_krow = lane >> 5, rm_pchunk = lane & 31;
-    if constexpr (kWgrad) {
-      const uint32_t rows = static_cast<uint32_t>(t.hi - t.lo);
-      ra = make_rsrc(p.a + t.lo * N, rows * static_cast<uint32_t>(N) * 2u);
-      rb = make_rsrc(p.b + t.lo * K, rows * static_cast<uint32_t>(K) * 2u);
-      a_step = kBK * static_cast<int>(N) * 2;
-#pragma unroll
-      for (int j = 0; j < kDmaA; ++j) {
-        const int krow = (j * kWaves + wave) * 2 + rm_krow;
-        const int lchunk = rm_pchunk ^ rm_swz(krow);
-        a_off[j] = static_cast<int>(static_cast<uint32_t>(krow) * static_cast<uint32_t>(N) * 2u +
-                                    static_cast<uint32_t>(t.i0) * 2u + lchunk * 16);
-      }
-    } else {
+    {
       const int rows_valid = static_cast<int>(min(t.hi - t.i0, int64_t(kBM)));
       ra = make_rsrc(p.a + t.i0 * N, static_cast<uint32_t>(rows_valid) * static_cast<uint32_t>(N) * 2u);
       rb = make_rsrc(p.b + t.g * N * K, static_cast<uint32_t>(N * K * 2));
@@ -266,12 +261,8 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
   int fa_base[kMI], fb_base[kNI];
 #pragma unroll
   for (int i = 0; i < kMI; ++i) {
-    if constexpr (kARM) {
-      fa_base[i] = rm_base(wm * kWaveRows + i * 32);
-    } else {
-      const int r = wm * kWaveRows + i * 32 + (lane & 31);
-      fa_base[i] = (r * kKCRow | (kc_swz(r) << 4)) ^ (khalf << 4);
-    }
+    const int r = wm * kWaveRows + i * 32 + (lane & 31);
+    fa_base[i] = (r * kKCRow | (kc_swz(r) << 4)) ^ (khalf << 4);
   }
 #pragma unroll
   for (int j = 0; j < kNI; ++j) fb_base[j] = kABytes + rm_base(wn * kWaveCols + j * 32);
@@ -288,13 +279,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
   bf16x8 fa[kSubSteps][kMI], fb[kSubSteps][kNI];
   auto read_frags = [&](int ks) {
 #pragma unroll
-    for (int i = 0; i < kMI; ++i) {
-      if constexpr (kARM) {
-        fa[ks][i] = read_rm_frag(rd_a[i] + ks * 16 * kRMRow);
-      } else {
-        fa[ks][i] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)(rd_a[i] ^ (ks << 5)));
-      }
-    }
+    for (int i = 0; i < kMI; ++i) fa[ks][i] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)(rd_a[i] ^ (ks << 5)));
 #pragma unroll
     for (int j = 0; j < kNI; ++j) fb[ks][j] = read_rm_frag(rd_b[j] + ks * 16 * kRMRow);
   };
@@ -344,23 +329,14 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
     for (int kt = 0; kt + 1 < ktiles; ++kt) {
       mfma_ks(0);
       __builtin_amdgcn_sched_barrier(0);
-      // This thread's DMA of stage kt + 1 has landed and its reads of stage kt
-      // are done; after the barrier, everyone's.
-      // Stage kt + 1 has landed. Younger and allowed to be in flight: stage
-      // kt + 2 (three stages) and, in the first steps after a tile change, the
+      // Stage kt + 1 has landed (and, after the barrier, everyone's; this
+      // thread's reads of stage kt are done). Younger and allowed to be in
+      // flight: stage kt + 2 and, in the first steps after a tile change, the
       // previous tile's output stores, issued after this tile's first stages.
-      if constexpr (kStages == 2) {
-        if (kt == 0 && round > 0) {
-          wait_vm_n<kStores>();
-        } else {
-          wait_dma();
-        }
+      if (kt <= kStages - 2 && round > 0) {
+        wait_vm_n<(kStages - 2) * (kDmaA + kDmaB) + kStores>();
       } else {
-        if (kt <= kStages - 2 && round > 0) {
-          wait_vm_n<(kStages - 2) * (kDmaA + kDmaB) + kStores>();
-        } else {
-          wait_vm_n<(kStages - 2) * (kDmaA + kDmaB)>();
-        }
+        wait_vm_n<(kStages - 2) * (kDmaA + kDmaB)>();
       }
       wait_lds();
       barrier();
@@ -418,11 +394,10 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
     // 8g + 8 .. 8g + 15: one 16-byte store each.
     if constexpr (kOut != 0) {
       // fp32: register group g of block (i, j) is 4 consecutive columns of
-      // one row, stored (or added to the stored values) as 16 bytes.
+      // one row, stored as 16 bytes.
       const int64_t wrow0 = cur.i0 + wm * kWaveRows;
-      const int64_t row_end = kWgrad ? N : cur.hi;
-      const int rows_out = static_cast<int>(min(max(row_end - wrow0, int64_t(0)), int64_t(kWaveRows)));
-      float *const obase = static_cast<float *>(p.out) + (kWgrad ? cur.g * N * K : 0);
+      const int rows_out = static_cast<int>(min(max(cur.hi - wrow0, int64_t(0)), int64_t(kWaveRows)));
+      float *const obase = static_cast<float *>(p.out);
       const uint32_t ld = static_cast<uint32_t>(K) * 4u;
       const __amdgpu_buffer_rsrc_t ro =
           make_rsrc(obase + (rows_out > 0 ? wrow0 * K : 0), static_cast<uint32_t>(rows_out) * ld);
@@ -437,16 +412,9 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
           for (int g = 0; g < 4; ++g) {
             const int64_t gcol = tcol0 + j * 32 + g * 8 + half * 4;
             const uint32_t off = gcol < K ? static_cast<uint32_t>(orow) * ld + static_cast<uint32_t>(gcol) * 4u : kNoAccess;
-            u32x4 v = {__float_as_uint(acc[i][j][4 * g]), __float_as_uint(acc[i][j][4 * g + 1]),
-                       __float_as_uint(acc[i][j][4 * g + 2]), __float_as_uint(acc[i][j][4 * g + 3])};
+            const u32x4 v = {__float_as_uint(acc[i][j][4 * g]), __float_as_uint(acc[i][j][4 * g + 1]),
+                             __float_as_uint(acc[i][j][4 * g + 2]), __float_as_uint(acc[i][j][4 * g + 3])};
 #if defined(__HIP_DEVICE_COMPILE__)
-            if constexpr (kOut == 2) {
-              const u32x4 old = __builtin_amdgcn_raw_buffer_load_b128(ro, static_cast<int>(off), 0, 0);
-              v = u32x4{__float_as_uint(__uint_as_float(old.x) + __uint_as_float(v.x)),
-                        __float_as_uint(__uint_as_float(old.y) + __uint_as_float(v.y)),
-                        __float_as_uint(__uint_as_float(old.z) + __uint_as_float(v.z)),
-                        __float_as_uint(__uint_as_float(old.w) + __uint_as_float(v.w))};
-            }
             __builtin_amdgcn_raw_buffer_store_b128(v, ro, static_cast<int>(off), 0, 0);
 #else
             (void)off;
@@ -458,9 +426,8 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_kernel(BwdArgs p) {
       }
     } else {
       const int64_t wrow0 = cur.i0 + wm * kWaveRows;
-      const int64_t row_end = kWgrad ? N : cur.hi;
-      const int rows_out = static_cast<int>(min(max(row_end - wrow0, int64_t(0)), int64_t(kWaveRows)));
-      const uint16_t *obase = static_cast<const uint16_t *>(p.out) + (kWgrad ? cur.g * N * K : 0);
+      const int rows_out = static_cast<int>(min(max(cur.hi - wrow0, int64_t(0)), int64_t(kWaveRows)));
+      const uint16_t *obase = static_cast<const uint16_t *>(p.out);
       const uint32_t ld = static_cast<uint32_t>(K) * 2u;
       const __amdgpu_buffer_rsrc_t ro =
           make_rsrc(obase + (rows_out > 0 ? wrow0 * K : 0), static_cast<uint32_t>(rows_out) * ld);
@@ -958,11 +925,11 @@ void launch_pipe(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
   grouped_gemm_bwd_pipe_kernel<kWgrad, kOut><<<dim3(grid), dim3(256), 0, s>>>(p);
 }
 
-template <bool kWgrad, int kBM, int kWavesM, int kStages, int kOut = 0>
-void launch(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
+template <int kOut = 0>
+void launch_dgrad128(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
   int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
   grid = std::max<int64_t>(8, (grid + 7) / 8 * 8);
-  grouped_gemm_bwd_kernel<kWgrad, kBM, kWavesM, kStages, kOut><<<dim3(grid), dim3(256), 0, s>>>(p);
+  grouped_gemm_dgrad128_kernel<kOut><<<dim3(grid), dim3(256), 0, s>>>(p);
 }
 
 // ---- tf32 GEMMs of the router backward on the bf16 matrix cores ---------
@@ -1103,7 +1070,7 @@ int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, con
   // every group's last row tile) and for reductions that are not whole steps
   // of at least three (N % 64 != 0 or N < 192); the pipelined 256-row kernel otherwise.
   if (M_total <= 160 * G || N % kBK != 0 || N < 3 * kBK) {
-    launch<false, 128, 1, 3>(p, (ceil_div(M_total, 128) + G) * p.ntiles, s);
+    launch_dgrad128(p, (ceil_div(M_total, 128) + G) * p.ntiles, s);
   } else {
     launch_pipe<false>(p, (ceil_div(M_total, 256) + G) * p.ntiles, s);
   }
@@ -1196,7 +1163,7 @@ int moe_router_dgrad_tf32(const float *grad_output, int64_t M, int64_t K, const 
   p.G = 1;
   p.ntiles = ceil_div(N, kBN);
   p.chunk = M;
-  if (M <= 160 || (3 * K) % kBK != 0 || 3 * K < 3 * kBK) launch<false, 128, 1, 3, 1>(p, (ceil_div(M, 128) + 1) * p.ntiles, s);
+  if (M <= 160 || (3 * K) % kBK != 0 || 3 * K < 3 * kBK) launch_dgrad128<1>(p, (ceil_div(M, 128) + 1) * p.ntiles, s);
   else launch_pipe<false, 1>(p, (ceil_div(M, 256) + 1) * p.ntiles, s);
   return check_launch(fn);
 }
