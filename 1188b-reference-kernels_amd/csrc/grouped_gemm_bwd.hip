@@ -74,6 +74,7 @@ struct BwdArgs {
   int64_t M, N, K, G;
   int64_t ntiles;           // column tiles, ceil(K / 256)
   int64_t chunk;            // rows per group when offsets is nullptr
+  int64_t kchunk;           // split dgrad: reduction columns of split g = [g kchunk, (g + 1) kchunk), the last to N
 };
 
 __device__ __forceinline__ int kc_swz(int row) { return (row >> 1) & 7; }
@@ -508,8 +509,13 @@ __global__ __launch_bounds__(256) void grouped_gemm_dgrad128_kernel(BwdArgs p) {
 //     half-wave reads at a time fall on 8 distinct 32-byte bank groups.
 __device__ __forceinline__ int rm16_swz(int krow) { return ((krow & 3) << 2) | (((krow >> 3) & 1) << 1); }
 
-template <bool kWgrad, int kOut>
+// kSplit (dgrad, fp32 output): a reduction split of one group. "Group" g is
+// split g: the rows of group 0 (group_offsets[0] .. [1] - 1), reduction columns
+// [g kchunk, ...) of dy and the same rows of w, written into fp32 plane g
+// [M, K] of out (at the same row indices).
+template <bool kWgrad, int kOut, bool kSplit = false>
 __global__ __launch_bounds__(256) void grouped_gemm_bwd_pipe_kernel(BwdArgs p) {
+  static_assert(!kSplit || (!kWgrad && kOut == 1), "the split is a dgrad with fp32 planes");
   constexpr int kBM = 256;
   constexpr int kWaves = 4;
   constexpr int kThreads = 256;
@@ -538,7 +544,8 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_pipe_kernel(BwdArgs p) {
   const bool chunked = p.offsets == nullptr;
 
   if (!chunked) {
-    for (int64_t i = tid; i <= p.G; i += kThreads) s_offs[i] = p.offsets[i];
+    const int64_t n_offs = kSplit ? 1 : p.G;  // a split reads group 0's offsets only
+    for (int64_t i = tid; i <= n_offs; i += kThreads) s_offs[i] = p.offsets[i];
   }
   __syncthreads();
 
@@ -546,6 +553,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_pipe_kernel(BwdArgs p) {
   // 2^31). The values are wave-uniform and read into scalar registers.
   const int m32 = static_cast<int>(p.M);
   auto group_range = [&](int g, int &lo, int &hi) {
+    if constexpr (kSplit) g = 0;  // every split covers the rows of group 0
     if (chunked) {
       lo = static_cast<int>(min(static_cast<int64_t>(g) * p.chunk, p.M));
       hi = static_cast<int>(min(static_cast<int64_t>(lo) + p.chunk, p.M));
@@ -559,6 +567,12 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_pipe_kernel(BwdArgs p) {
   const uint32_t wg_rows = static_cast<uint32_t>(ceil_div(N, kBM));  // wgrad: row tiles per group
   auto row_tiles = [&](int lo, int hi) -> uint32_t {
     return kWgrad ? wg_rows : static_cast<uint32_t>(hi - lo + kBM - 1) / kBM;
+  };
+  // Reduction columns of split g (kSplit): [k0, k0 + kred).
+  const int kchunk32 = static_cast<int>(p.kchunk);
+  auto split_red = [&](int g, int &k0, int &kred) {
+    k0 = g * kchunk32;
+    kred = g + 1 == g_count ? static_cast<int>(N) - k0 : kchunk32;
   };
   int g_cur = 0, g_lo, g_hi;
   uint32_t tiles_before = 0;
@@ -603,7 +617,11 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_pipe_kernel(BwdArgs p) {
     t.i0 = (kWgrad ? 0 : g_lo) + static_cast<int>(mt) * kBM;
     t.nt = nt;
     t.rows_valid = min((kWgrad ? static_cast<int>(N) : g_hi) - t.i0, kBM);
-    const int red = kWgrad ? g_hi - g_lo : static_cast<int>(N);
+    int red = kWgrad ? g_hi - g_lo : static_cast<int>(N);
+    if constexpr (kSplit) {
+      int k0;
+      split_red(g_cur, k0, red);
+    }
     t.ktiles = max((red + kBK - 1) / kBK, 3);
     return true;
   };
@@ -633,8 +651,18 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_pipe_kernel(BwdArgs p) {
         a_off[j] = static_cast<int>(static_cast<uint32_t>(krow) * n32 * 2u + static_cast<uint32_t>(t.i0) * 2u + lchunk * 16u);
       }
     } else {
-      ra = make_rsrc(p.a + static_cast<int64_t>(t.i0) * N, static_cast<uint32_t>(t.rows_valid) * n32 * 2u);
-      rb = make_rsrc(p.b + static_cast<int64_t>(t.g) * N * K, static_cast<uint32_t>(N * K * 2));
+      if constexpr (kSplit) {
+        // dy columns [k0, k0 + kred) of the tile's rows (the resource ends at the
+        // last row's k0 + kred) and w rows [k0, k0 + kred).
+        int k0, kred;
+        split_red(t.g, k0, kred);
+        ra = make_rsrc(p.a + static_cast<int64_t>(t.i0) * N + k0,
+                       static_cast<uint32_t>(t.rows_valid - 1) * n32 * 2u + static_cast<uint32_t>(kred) * 2u);
+        rb = make_rsrc(p.b + static_cast<int64_t>(k0) * K, static_cast<uint32_t>(kred) * k32 * 2u);
+      } else {
+        ra = make_rsrc(p.a + static_cast<int64_t>(t.i0) * N, static_cast<uint32_t>(t.rows_valid) * n32 * 2u);
+        rb = make_rsrc(p.b + static_cast<int64_t>(t.g) * N * K, static_cast<uint32_t>(N * K * 2));
+      }
       a_step = kBK * 2;
 #pragma unroll
       for (int j = 0; j < kDma; ++j) {
@@ -758,7 +786,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_pipe_kernel(BwdArgs p) {
     int ln = lane;
     asm volatile("" : "+v"(ln));
     const int eq = ln >> 4;
-    const int64_t gbase = kWgrad ? static_cast<int64_t>(t.g) * N * K : 0;
+    const int64_t gbase = kWgrad ? static_cast<int64_t>(t.g) * N * K : kSplit ? static_cast<int64_t>(t.g) * p.M * K : 0;
     const int kcols = static_cast<int>(k32);
     if constexpr (kOut == 0) {
       // One resource over the tile's valid rows (below 2^31 bytes: K < 2^22).
@@ -918,11 +946,11 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_pipe_kernel(BwdArgs p) {
   wait_dma();  // no LDS DMA outlives the workgroup
 }
 
-template <bool kWgrad, int kOut = 0>
+template <bool kWgrad, int kOut = 0, bool kSplit = false>
 void launch_pipe(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
   int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
   grid = std::max<int64_t>(8, (grid + 7) / 8 * 8);
-  grouped_gemm_bwd_pipe_kernel<kWgrad, kOut><<<dim3(grid), dim3(256), 0, s>>>(p);
+  grouped_gemm_bwd_pipe_kernel<kWgrad, kOut, kSplit><<<dim3(grid), dim3(256), 0, s>>>(p);
 }
 
 template <int kOut = 0>
@@ -1007,6 +1035,32 @@ __global__ __launch_bounds__(256) void sum_planes_kernel(const float *part, int 
   }
 }
 
+// dx rows r of group 0 (offsets[0] <= r < offsets[1], clamped to [0, M)):
+// dx[r][c] = bf16 RNE of the sum over s of part[s][r][c], s ascending; other
+// rows are not written (K % 4 == 0, 16-byte aligned part, 8-byte aligned dx).
+__global__ __launch_bounds__(256) void sum_planes_rows_bf16_kernel(const float *part, int planes, int64_t M, int64_t K,
+                                                                   const int32_t *offsets, uint16_t *dx) {
+  const int64_t lo = min(max(static_cast<int64_t>(offsets[0]), int64_t(0)), M);
+  const int64_t hi = min(max(static_cast<int64_t>(offsets[1]), lo), M);
+  const int64_t n = M * K;
+  const int64_t q_lo = lo * K / 4, q_hi = hi * K / 4;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  for (int64_t i = q_lo + static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < q_hi; i += stride) {
+    const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(part) + i);
+    float x = __uint_as_float(a.x), y = __uint_as_float(a.y), z = __uint_as_float(a.z), w = __uint_as_float(a.w);
+    for (int s = 1; s < planes; ++s) {
+      const u32x4 b = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(part + s * n) + i);
+      x += __uint_as_float(b.x);
+      y += __uint_as_float(b.y);
+      z += __uint_as_float(b.z);
+      w += __uint_as_float(b.w);
+    }
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 o = {f32_to_bf16_rne(x) | (f32_to_bf16_rne(y) << 16), f32_to_bf16_rne(z) | (f32_to_bf16_rne(w) << 16)};
+    *reinterpret_cast<u32x2 *>(dx + 4 * i) = o;
+  }
+}
+
 constexpr size_t kWsAlign = 256;
 size_t align_up(size_t x) { return (x + kWsAlign - 1) / kWsAlign * kWsAlign; }
 
@@ -1030,16 +1084,44 @@ int check_common(const char *fn, int64_t M_total, int64_t N, int64_t K, int64_t 
   return MOE_OK;
 }
 
+// Reduction split of a one-group dgrad whose output has fewer tiles than half
+// the CUs (case37: 2 x 32 tiles): s splits of whole 64-column steps (at least
+// three each; the last split takes the remainder), at most one split per
+// otherwise idle CU and 16 in all. s = 1: no split.
+struct DgradSplit {
+  int64_t s, kchunk;
+};
+
+DgradSplit dgrad_split_plan(int64_t M, int64_t N, int64_t K, int64_t G) {
+  using namespace moe;
+  DgradSplit pl{1, 0};
+  if (G != 1 || M <= 160 || M > (int64_t(1) << 31) - 1 || N % kBK != 0 || N < 6 * kBK || K == 0) return pl;
+  const int64_t tiles = ceil_div(M, 256) * ceil_div(K, kBN);
+  const int64_t cus = gemm::num_cus();
+  if (2 * tiles > cus) return pl;
+  const int64_t ksteps = N / kBK;
+  const int64_t s = std::min<int64_t>(std::min<int64_t>(cus / tiles, ksteps / 3), 16);
+  if (s < 2) return pl;
+  const int64_t kc = ksteps / s;  // >= 3
+  pl.s = ksteps / kc;
+  pl.kchunk = kc * kBK;
+  return pl;
+}
+
 }  // namespace
 
 extern "C" {
+
+size_t moe_grouped_gemm_dgrad_workspace_size(int64_t M_total, int64_t N, int64_t K, int64_t G) {
+  if (M_total < 0 || N < 0 || K < 0 || G < 1) return 0;
+  const DgradSplit sp = dgrad_split_plan(M_total, N, K, G);
+  return sp.s > 1 ? moe::align_up(static_cast<size_t>(sp.s) * M_total * K * 4) : 0;
+}
 
 int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, const moe_bf16_t *w, int64_t G,
                            int64_t K, const int32_t *group_offsets, moe_bf16_t *dx, void *workspace,
                            size_t workspace_bytes, void *stream) {
   using namespace moe;
-  (void)workspace;
-  (void)workspace_bytes;
   const char *fn = "moe_grouped_gemm_dgrad";
   if (int rc = check_common(fn, M_total, N, K, G, group_offsets)) return rc;
   // 32-bit buffer offsets: a 256-row panel of dy and one expert's w stay below 2 GiB.
@@ -1065,7 +1147,24 @@ int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, con
   p.G = G;
   p.ntiles = ceil_div(K, kBN);
   p.chunk = 0;
+  p.kchunk = 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // One group with few output tiles (fewer than half the CUs) and a workspace
+  // for the fp32 partials: the reduction is split over the idle CUs.
+  const DgradSplit sp = dgrad_split_plan(M_total, N, K, G);
+  const size_t need = sp.s > 1 ? align_up(static_cast<size_t>(sp.s) * M_total * K * 4) : 0;
+  if (sp.s > 1 && workspace != nullptr && workspace_bytes >= need && is_aligned(workspace, kWsAlign)) {
+    float *planes = static_cast<float *>(workspace);
+    p.out = planes;
+    p.G = sp.s;
+    p.kchunk = sp.kchunk;
+    launch_pipe<false, 1, true>(p, ceil_div(M_total, 256) * p.ntiles * sp.s, s);
+    const int64_t q = M_total * K / 4;
+    const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(ceil_div(q, 256), 4096));
+    sum_planes_rows_bf16_kernel<<<dim3(grid), dim3(256), 0, s>>>(planes, static_cast<int>(sp.s), M_total, K,
+                                                                group_offsets, reinterpret_cast<uint16_t *>(dx));
+    return check_launch(fn);
+  }
   // 128-row tiles when the groups average at most 160 rows (less padding in
   // every group's last row tile) and for reductions that are not whole steps
   // of at least three (N % 64 != 0 or N < 192); the pipelined 256-row kernel otherwise.
@@ -1109,6 +1208,7 @@ int moe_grouped_gemm_wgrad(const moe_bf16_t *dy, const moe_bf16_t *x, int64_t M_
   p.G = G;
   p.ntiles = ceil_div(K, kBN);
   p.chunk = 0;
+  p.kchunk = 0;
   launch_pipe<true>(p, G * ceil_div(N, 256) * p.ntiles, static_cast<hipStream_t>(stream));
   return check_launch(fn);
 }
@@ -1163,6 +1263,7 @@ int moe_router_dgrad_tf32(const float *grad_output, int64_t M, int64_t K, const 
   p.G = 1;
   p.ntiles = ceil_div(N, kBN);
   p.chunk = M;
+  p.kchunk = 0;
   if (M <= 160 || (3 * K) % kBK != 0 || 3 * K < 3 * kBK) launch_dgrad128<1>(p, (ceil_div(M, 128) + 1) * p.ntiles, s);
   else launch_pipe<false, 1>(p, (ceil_div(M, 256) + 1) * p.ntiles, s);
   return check_launch(fn);
@@ -1261,6 +1362,7 @@ int moe_router_wgrad_tf32(const float *grad_output, int64_t M, int64_t N, const 
   p.G = pl.s;
   p.ntiles = ceil_div(K, kBN);
   p.chunk = pl.c;
+  p.kchunk = 0;
   launch_pipe<true, 1>(p, ceil_div(N, 256) * p.ntiles * p.G, s);
   if (split) {
     const int64_t q = N * K / 4;

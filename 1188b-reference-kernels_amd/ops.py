@@ -472,7 +472,10 @@ def grouped_gemm_dgrad(dy: torch.Tensor, w: torch.Tensor, group_offsets: torch.T
     M = dy.shape[0]
     dyc, wc, oc = dy.contiguous(), w.contiguous(), group_offsets.contiguous()
     out = _out(out, (M, K), torch.bfloat16, dy.device)
-    call("moe_grouped_gemm_dgrad", ptr(dyc), M, N, ptr(wc), G, K, ptr(oc), ptr(out), None, 0, stream_handle())
+    # A one-group dgrad with few output tiles splits its reduction into fp32 partials in a workspace.
+    nbytes = _lib.lib().moe_grouped_gemm_dgrad_workspace_size(M, N, K, G)
+    ws = _ws(nbytes, dy.device)
+    call("moe_grouped_gemm_dgrad", ptr(dyc), M, N, ptr(wc), G, K, ptr(oc), ptr(out), ptr(ws), nbytes, stream_handle())
     return out
 
 

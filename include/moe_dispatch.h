@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define MOE_DISPATCH_ABI_VERSION 8
+#define MOE_DISPATCH_ABI_VERSION 9
 
 typedef uint16_t moe_bf16_t;
 
@@ -265,7 +265,14 @@ int moe_grouped_gemm_gather(const moe_bf16_t *x, int64_t x_rows, const int32_t *
  *   dx  bf16 [M_total, K] (rows beyond group_offsets[G] are not written)
  * Limits: N % 8 == 0, K % 8 == 0, 1 <= G <= 4096, M_total < 2^31, N, K < 2^22,
  *   N * K < 2^30; dy, w, dx 16-byte aligned. N == 0 gives zeros.
- * Workspace: none (pass NULL, 0). */
+ * Workspace: optional. With at least moe_grouped_gemm_dgrad_workspace_size
+ *   bytes (256-byte aligned), a single group whose output has fewer tiles
+ *   than half the CUs (case37) splits its reduction over the idle CUs into
+ *   fp32 partial planes in the workspace, summed in split order (deterministic)
+ *   and rounded once; otherwise (NULL, 0, or a smaller size) one pass as above.
+ *   The size is 0 where no split applies; it depends on the current device's
+ *   CU count. */
+size_t moe_grouped_gemm_dgrad_workspace_size(int64_t M_total, int64_t N, int64_t K, int64_t G);
 int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, const moe_bf16_t *w,
                            int64_t G, int64_t K, const int32_t *group_offsets, moe_bf16_t *dx,
                            void *workspace, size_t workspace_bytes, void *stream);

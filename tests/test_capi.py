@@ -17,7 +17,7 @@ L = pkg._lib
 def test_library_loads_and_exports_header_symbols():
     lib = L.lib()
     declared = L.header_functions()
-    assert len(declared) == len(L.SIGNATURES) == 26
+    assert len(declared) == len(L.SIGNATURES) == 27
     assert set(declared) == set(L.SIGNATURES)
     for name in declared:
         assert hasattr(lib, name), name
@@ -161,6 +161,16 @@ def test_workspace_sizes():
     # router: one fp32 logits plane (used when the top-k call gets no logits output)
     assert lib.moe_router_workspace_size(16384, 8192, 320) == 16384 * 320 * 4
     assert lib.moe_router_workspace_size(0, 8192, 320) == 0
+    # one-group dgrad reduction split (no GPU here: the CU count reads as 256): case37
+    # [288 x 5120] @ [5120 x 8192] has 2 x 32 output tiles -> 4 splits of 20 steps, fp32 planes
+    assert lib.moe_grouped_gemm_dgrad_workspace_size(288, 5120, 8192, 1) == 4 * 288 * 8192 * 4
+    assert lib.moe_grouped_gemm_dgrad_workspace_size(4096, 5120, 8192, 1) == 0   # 512 tiles: no split
+    assert lib.moe_grouped_gemm_dgrad_workspace_size(288, 5120, 8192, 2) == 0    # several groups
+    assert lib.moe_grouped_gemm_dgrad_workspace_size(160, 5120, 8192, 1) == 0    # 128-row tiles
+    assert lib.moe_grouped_gemm_dgrad_workspace_size(288, 320, 8192, 1) == 0     # too short a reduction
+    assert lib.moe_grouped_gemm_dgrad_workspace_size(288, 5128, 8192, 1) == 0    # N % 64 != 0
+    # router tf32 wgrad: [A_hi; A_hi; A_lo] and [B_hi; B_lo; B_hi] over 3M rows (+ fp32 planes when split)
+    assert lib.moe_router_wgrad_tf32_workspace_size(4096, 64, 1000) >= 3 * 4096 * (64 + 1000) * 2
 
 
 def test_status_strings():

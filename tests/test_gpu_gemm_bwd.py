@@ -114,6 +114,29 @@ def test_case37_single_expert_dgrad(pkg, dev):
     _check(got, golden, "case37")
 
 
+def test_dgrad_split_reduction(pkg, dev):
+    # One group with few output tiles (3 x 2 here) and a workspace: the reduction runs as 5 splits
+    # (3, 3, 3, 3 and 4 steps of 64) into fp32 planes summed in split order. Only the group's rows
+    # (offsets 40 .. 560 of 600) are written, the result matches the fp32 oracle, and a second
+    # call is bit-identical (no atomics: the order is fixed).
+    lib = pkg._lib.lib()
+    M, N, K = 600, 1024, 512
+    assert lib.moe_grouped_gemm_dgrad_workspace_size(M, N, K, 1) == 5 * M * K * 4
+    g = torch.Generator().manual_seed(37)
+    dy = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    w = (torch.randn(1, N, K, generator=g) * 0.05).to(torch.bfloat16)
+    offs = torch.tensor([40, 560], dtype=torch.int32, device=dev)
+    outs = []
+    for _ in range(2):
+        buf = torch.full((M * K + 4096,), 7.0, dtype=torch.bfloat16, device=dev)
+        out = buf[:M * K].view(M, K)
+        pkg.ops.grouped_gemm_dgrad(dy.to(dev), w.to(dev), offs, out=out)
+        assert torch.all(out[:40] == 7.0) and torch.all(buf[560 * K:] == 7.0)
+        outs.append(out.cpu())
+    _check(outs[0][40:560], ref_torch.grouped_gemm_dgrad_fp32(dy[40:560], w, [520]), "split dgrad")
+    assert_bits_equal(outs[0], outs[1], "split dgrad repeat")
+
+
 # ------------------------------------------------------------------ wgrad
 @pytest.mark.parametrize("sizes,N,K", [
     ([64], 256, 256),                       # one tile, one step
