@@ -1,0 +1,35 @@
+"""CPU: the grouped GEMM kernels keep every value in registers (no scratch spills).
+
+The GEMM kernels hold 256 fp32 accumulators in AGPRs and a K step of operand fragments in
+VGPRs; a spill there puts scratch loads (which wait on the vector-memory counter, and so on
+the LDS DMA in flight) inside the MFMA stream. The compiler's kernel-resource-usage remarks
+for the device code must report 0 scratch bytes per lane for every instantiation.
+"""
+from __future__ import annotations
+
+import shutil
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+import pytest
+
+CSRC = Path(__file__).resolve().parents[1] / "1188b-reference-kernels_amd" / "csrc"
+sys.path.insert(0, str(CSRC))
+
+pytestmark = pytest.mark.skipif(not (Path("/opt/rocm/bin/hipcc").exists() or shutil.which("hipcc")),
+                                reason="needs hipcc (device compile only, no GPU)")
+
+
+def test_gemm_kernels_do_not_spill():
+    import resource_usage as ru
+    hipcc = ru._hipcc()
+    srcs = ["grouped_gemm.hip", "grouped_gemm_bwd.hip"]
+    with ThreadPoolExecutor(max_workers=2) as ex:
+        results = list(ex.map(lambda s: ru.usage(s, hipcc), srcs))
+    rows = [r for res in results for r in res]
+    assert len(rows) >= 15, rows
+    spilled = [(name, v) for name, v in rows if v.get("scratch", 0) != 0]
+    assert not spilled, spilled
+    assert all(v.get("agpr") in (128, 256) for name, v in rows if "gemm" in name and "kernel" in name and "sum_planes" not in name
+               and "split" not in name)
