@@ -1,9 +1,11 @@
 """Helpers shared by the case modules."""
 from __future__ import annotations
 
+from types import SimpleNamespace
+
 import torch
 
-from .. import ops
+from .. import inputs, ops
 
 
 def scatter_rows(row_id_map: torch.Tensor) -> tuple[int, bool]:
@@ -89,3 +91,78 @@ def grouped_wgrad(dy: torch.Tensor, x: torch.Tensor, m_splits) -> torch.Tensor:
     offsets = _split_offsets(m_splits, dy.shape[0], len(m_splits), f"dy {tuple(dy.shape)} and x {tuple(x.shape)}",
                              dy.device)
     return ops.grouped_gemm_wgrad(dy, x, offsets)
+
+
+def grouped_gemm_case(kind: str, *, case_id: int, name: str, num_groups: int, tokens: int, n: int, k: int,
+                      seed: int) -> SimpleNamespace:
+    """The module attributes of a grouped-GEMM case (the reference cases 03/04 "fwd", 07/08/13/19 "dgrad",
+    05/09 "wgrad" share one shape: kernel_cases/case07_moe_grouped_gemm_fc1_dgrad.py:37-73 and its siblings):
+
+    * NUM_GROUPS, TOKENS, N, K, CASE and group_sizes (uniform m_splits, the first `total % groups` one larger, :43-46);
+    * kernel_function for ragged groups -- fwd: (x [T,K], w [G,N,K], m_splits=None, swiglu=False) ->
+      cat_g(x[seg_g] @ w[g].T); dgrad: (dy [T,N], w [G,N,K], m_splits=None) -> cat_g(dy[seg_g] @ w[g]);
+      wgrad: (dy [T,N], x [T,K], m_splits=None, num_groups=NUM_GROUPS) -> stack_g(dy[seg_g].T @ x[seg_g]);
+    * Model(num_groups, tokens) whose forward is kernel_function with the uniform sizes (:49-64);
+    * get_init_inputs and a seeded get_inputs (the reference's :71-73 is unseeded), N(0,1) bf16 tensors drawn in
+      the order of the forward's arguments.
+    """
+    if kind not in ("fwd", "dgrad", "wgrad"):
+        raise ValueError(f"kind {kind!r}")
+
+    def group_sizes(total, groups):
+        return inputs.uniform_group_sizes(total, groups)
+
+    if kind == "fwd":
+        def kernel_function(x, w, m_splits=None, swiglu=False):
+            """out[seg_g] = x[seg_g] @ w[g].T for consecutive row segments of sizes m_splits."""
+            if m_splits is None:
+                m_splits = group_sizes(x.shape[0], w.shape[0])
+            offsets = _split_offsets(m_splits, x.shape[0], w.shape[0], f"x {tuple(x.shape)} and w {tuple(w.shape)}",
+                                     x.device)
+            return ops.grouped_gemm(x, w, offsets, swiglu=swiglu)
+    elif kind == "dgrad":
+        def kernel_function(dy, w, m_splits=None):
+            """dx[seg_g] = dy[seg_g] @ w[g] for consecutive row segments of sizes m_splits."""
+            if m_splits is None:
+                m_splits = group_sizes(dy.shape[0], w.shape[0])
+            return grouped_dgrad(dy, w, m_splits)
+    else:
+        def kernel_function(dy, x, m_splits=None, num_groups=num_groups):
+            """dw[g] = dy[seg_g].T @ x[seg_g] for consecutive row segments of sizes m_splits."""
+            if m_splits is None:
+                m_splits = group_sizes(dy.shape[0], num_groups)
+            return grouped_wgrad(dy, x, m_splits)
+
+    class Model:
+        """Model(num_groups, tokens).forward(a, b) with uniform group sizes."""
+
+        def __init__(self, num_groups=num_groups, tokens=tokens):
+            self.num_groups = num_groups
+            self.sizes = group_sizes(tokens, num_groups)
+
+        def __call__(self, a, b):
+            return kernel_function(a, b, self.sizes)
+
+        forward = __call__
+
+    def get_init_inputs():
+        return [num_groups, tokens]
+
+    if kind == "wgrad":
+        def get_inputs(device="cuda", seed: int = seed, tokens: int = tokens, n: int = n, k: int = k):
+            g = torch.Generator().manual_seed(seed)
+            dy = torch.randn(tokens, n, generator=g).to(torch.bfloat16)
+            x = torch.randn(tokens, k, generator=g).to(torch.bfloat16)
+            return [dy.to(device), x.to(device)]
+    else:
+        def get_inputs(device="cuda", seed: int = seed, tokens: int = tokens, groups: int = num_groups, n: int = n,
+                       k: int = k):
+            g = torch.Generator().manual_seed(seed)
+            a = torch.randn(tokens, k if kind == "fwd" else n, generator=g).to(torch.bfloat16)
+            w = torch.randn(groups, n, k, generator=g).to(torch.bfloat16)
+            return [a.to(device), w.to(device)]
+
+    case = {"id": case_id, "name": name, "dtype": "bf16 in / fp32 accumulate / bf16 out", "backward": False}
+    return SimpleNamespace(NUM_GROUPS=num_groups, TOKENS=tokens, N=n, K=k, CASE=case, group_sizes=group_sizes,
+                           kernel_function=kernel_function, Model=Model, get_init_inputs=get_init_inputs,
+                           get_inputs=get_inputs)

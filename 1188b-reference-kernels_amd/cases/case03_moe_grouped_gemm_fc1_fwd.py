@@ -9,55 +9,14 @@ reference get_inputs (:71-73) is unseeded; get_inputs here takes a seed.
 """
 from __future__ import annotations
 
-import torch
+from .. import inputs
+from ._common import grouped_gemm_case
 
-from .. import inputs, ops
-from ._common import cached_offsets
-
-NUM_GROUPS = 40
-TOKENS = 4096
-N = 5120
-K = 8192
-
-CASE = {"id": 3, "name": "moe_grouped_gemm_fc1_fwd", "dtype": "bf16 in / fp32 accumulate / bf16 out",
-        "backward": False}
-
-
-def group_sizes(total, groups):
-    return inputs.uniform_group_sizes(total, groups)
-
-
-def kernel_function(x, w, m_splits=None, swiglu=False):
-    """out[seg_g] = x[seg_g] @ w[g].T for consecutive row segments of sizes m_splits."""
-    if m_splits is None:
-        m_splits = group_sizes(x.shape[0], w.shape[0])
-    if len(m_splits) != w.shape[0] or sum(m_splits) != x.shape[0]:
-        raise ValueError(f"m_splits (len {len(m_splits)}, sum {sum(m_splits)}) does not match x {tuple(x.shape)} "
-                         f"and w {tuple(w.shape)}")
-    offsets = cached_offsets(m_splits, x.device)
-    return ops.grouped_gemm(x, w, offsets, swiglu=swiglu)
-
-
-class Model:
-    """Model(num_groups, tokens).forward(x, w) with uniform group sizes."""
-
-    def __init__(self, num_groups=NUM_GROUPS, tokens=TOKENS):
-        self.num_groups = num_groups
-        self.sizes = group_sizes(tokens, num_groups)
-
-    def __call__(self, x, w):
-        return kernel_function(x, w, self.sizes)
-
-    forward = __call__
-
-
-def get_init_inputs():
-    return [NUM_GROUPS, TOKENS]
-
-
-def get_inputs(device="cuda", seed: int = inputs.SEED_CASE03, tokens: int = TOKENS, groups: int = NUM_GROUPS,
-               n: int = N, k: int = K):
-    g = torch.Generator().manual_seed(seed)
-    x = torch.randn(tokens, k, generator=g).to(torch.bfloat16)
-    w = torch.randn(groups, n, k, generator=g).to(torch.bfloat16)
-    return [x.to(device), w.to(device)]
+_CASE = grouped_gemm_case("fwd", case_id=3, name="moe_grouped_gemm_fc1_fwd", num_groups=40, tokens=4096,
+                          n=5120, k=8192, seed=inputs.SEED_CASE03)
+NUM_GROUPS, TOKENS, N, K, CASE = _CASE.NUM_GROUPS, _CASE.TOKENS, _CASE.N, _CASE.K, _CASE.CASE
+group_sizes = _CASE.group_sizes
+kernel_function = _CASE.kernel_function
+Model = _CASE.Model
+get_init_inputs = _CASE.get_init_inputs
+get_inputs = _CASE.get_inputs

@@ -11,50 +11,14 @@ unseeded; get_inputs here takes a seed.
 """
 from __future__ import annotations
 
-import torch
-
 from .. import inputs
-from ._common import grouped_wgrad
+from ._common import grouped_gemm_case
 
-NUM_GROUPS = 40
-TOKENS = 4096
-N = 8192
-K = 2560
-
-CASE = {"id": 5, "name": "moe_grouped_gemm_fc2_wgrad", "dtype": "bf16 in / fp32 accumulate / bf16 out",
-        "backward": False}
-
-
-def group_sizes(total, groups):
-    return inputs.uniform_group_sizes(total, groups)
-
-
-def kernel_function(dy, x, m_splits=None, num_groups=NUM_GROUPS):
-    """dw[g] = dy[seg_g].T @ x[seg_g] for consecutive row segments of sizes m_splits."""
-    if m_splits is None:
-        m_splits = group_sizes(dy.shape[0], num_groups)
-    return grouped_wgrad(dy, x, m_splits)
-
-
-class Model:
-    """Model(num_groups, tokens).forward(dy, x) with uniform group sizes."""
-
-    def __init__(self, num_groups=NUM_GROUPS, tokens=TOKENS):
-        self.num_groups = num_groups
-        self.sizes = group_sizes(tokens, num_groups)
-
-    def __call__(self, dy, x):
-        return kernel_function(dy, x, self.sizes)
-
-    forward = __call__
-
-
-def get_init_inputs():
-    return [NUM_GROUPS, TOKENS]
-
-
-def get_inputs(device="cuda", seed: int = inputs.SEED_CONFIG_BASE + 55, tokens: int = TOKENS, n: int = N, k: int = K):
-    g = torch.Generator().manual_seed(seed)
-    dy = torch.randn(tokens, n, generator=g).to(torch.bfloat16)
-    x = torch.randn(tokens, k, generator=g).to(torch.bfloat16)
-    return [dy.to(device), x.to(device)]
+_CASE = grouped_gemm_case("wgrad", case_id=5, name="moe_grouped_gemm_fc2_wgrad", num_groups=40, tokens=4096,
+                          n=8192, k=2560, seed=inputs.SEED_CONFIG_BASE + 55)
+NUM_GROUPS, TOKENS, N, K, CASE = _CASE.NUM_GROUPS, _CASE.TOKENS, _CASE.N, _CASE.K, _CASE.CASE
+group_sizes = _CASE.group_sizes
+kernel_function = _CASE.kernel_function
+Model = _CASE.Model
+get_init_inputs = _CASE.get_init_inputs
+get_inputs = _CASE.get_inputs

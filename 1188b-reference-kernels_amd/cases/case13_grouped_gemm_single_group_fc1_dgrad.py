@@ -10,51 +10,14 @@ get_inputs (:71-73) is unseeded; get_inputs here takes a seed.
 """
 from __future__ import annotations
 
-import torch
-
 from .. import inputs
-from ._common import grouped_dgrad
+from ._common import grouped_gemm_case
 
-NUM_GROUPS = 1
-TOKENS = 4096
-N = 5120
-K = 8192
-
-CASE = {"id": 13, "name": "grouped_gemm_single_group_fc1_dgrad", "dtype": "bf16 in / fp32 accumulate / bf16 out",
-        "backward": False}
-
-
-def group_sizes(total, groups):
-    return inputs.uniform_group_sizes(total, groups)
-
-
-def kernel_function(dy, w, m_splits=None):
-    """dx[seg_g] = dy[seg_g] @ w[g] for consecutive row segments of sizes m_splits."""
-    if m_splits is None:
-        m_splits = group_sizes(dy.shape[0], w.shape[0])
-    return grouped_dgrad(dy, w, m_splits)
-
-
-class Model:
-    """Model(num_groups, tokens).forward(dy, w) with uniform group sizes."""
-
-    def __init__(self, num_groups=NUM_GROUPS, tokens=TOKENS):
-        self.num_groups = num_groups
-        self.sizes = group_sizes(tokens, num_groups)
-
-    def __call__(self, dy, w):
-        return kernel_function(dy, w, self.sizes)
-
-    forward = __call__
-
-
-def get_init_inputs():
-    return [NUM_GROUPS, TOKENS]
-
-
-def get_inputs(device="cuda", seed: int = inputs.SEED_CONFIG_BASE + 63, tokens: int = TOKENS, groups: int = NUM_GROUPS,
-               n: int = N, k: int = K):
-    g = torch.Generator().manual_seed(seed)
-    dy = torch.randn(tokens, n, generator=g).to(torch.bfloat16)
-    w = torch.randn(groups, n, k, generator=g).to(torch.bfloat16)
-    return [dy.to(device), w.to(device)]
+_CASE = grouped_gemm_case("dgrad", case_id=13, name="grouped_gemm_single_group_fc1_dgrad", num_groups=1, tokens=4096,
+                          n=5120, k=8192, seed=inputs.SEED_CONFIG_BASE + 63)
+NUM_GROUPS, TOKENS, N, K, CASE = _CASE.NUM_GROUPS, _CASE.TOKENS, _CASE.N, _CASE.K, _CASE.CASE
+group_sizes = _CASE.group_sizes
+kernel_function = _CASE.kernel_function
+Model = _CASE.Model
+get_init_inputs = _CASE.get_init_inputs
+get_inputs = _CASE.get_inputs
