@@ -35,7 +35,7 @@ MOE_MAP_EXPERT_MAJOR = 1
 MOE_EPILOGUE_NONE = 0
 MOE_EPILOGUE_SWIGLU = 1
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -52,6 +52,8 @@ SIGNATURES = {
     "moe_row_id_map": (_int, [_p, _i64, _i64, _p, _p, _p, _p, _p, _i64, _p, _sz, _p]),
     "moe_row_id_map_noalloc": (_int, [_p, _i64, _i64, _p, _p, _p, _p, _p, _i64, _p]),
     "moe_permute_workspace_size": (_sz, [_i64]),
+    "moe_map_extent_workspace_size": (_sz, [_i64]),
+    "moe_map_extent": (_int, [_p, _int, _i64, _p, _p, _sz, _p]),
     "moe_permute": (_int, [_p, _i64, _i64, _p, _int, _int, _i64, _p, _p, _p, _i64, _int, _p, _sz, _p]),
     "moe_unpermute": (_int, [_p, _i64, _i64, _p, _int, _int, _i64, _i64, _p, _p, _p, _p]),
     "moe_permute_bwd": (_int, [_p, _i64, _i64, _p, _p, _int, _int, _i64, _i64, _p, _p, _p, _p]),

@@ -13,15 +13,15 @@ def scatter_rows(row_id_map: torch.Tensor) -> tuple[int, bool]:
     functions' output row count, and whether the entries >= 0 are as many as num_out -- for a map
     whose entries are distinct, as a row-id map's are, that they name every output row.
 
-    One pair of scalars is read back to the host, exactly where the reference reads its max
+    One pass over the map (moe_map_extent) and one read-back of the pair, where the reference reads its max
     (kernel_cases/case21_ref_permute_with_mask_map_trans.py:64,
     kernel_results/case17_moe_permute_with_mask_map/binding.cpp:24).
     """
     if row_id_map.numel() == 0:
         return 0, True
-    mx, cnt = torch.stack([row_id_map.max().to(torch.int64), (row_id_map >= 0).sum()]).tolist()
-    num_out = max(int(mx) + 1, 0)
-    return num_out, int(cnt) == num_out
+    mx, cnt = ops.map_extent(row_id_map)
+    num_out = mx + 1
+    return num_out, cnt == num_out
 
 
 def permute_from_map(inp: torch.Tensor, row_id_map: torch.Tensor, probs, layout: str):

@@ -3,19 +3,17 @@
 Drop-in for reference_permute_mask_with_probs
 (kernel_cases/case22_ref_moe_permute_mask_kernel_true.py:47-69):
 (out [num_out,H], permuted_probs [num_out]) with num_out = max(row_id_map)+1;
-the hidden row is copied, not scaled.  make_probs follows :88-103.
+the hidden row is copied, not scaled.  make_probs follows :88-103; the routing
+generator (:72-85) and the shape constants (:41-44) are case21's, taken from
+its module.
 """
 from __future__ import annotations
 
 import torch
 
 from .. import inputs, ops
-from ._common import check_scatter_shapes, expert_major_map, permute_from_map
-
-M = 16384
-HIDDEN = 8192
-NUM_EXPERTS = 320
-TOPK = 8
+from ._common import check_scatter_shapes, permute_from_map
+from .case21_permute_with_mask_map_trans import HIDDEN, M, NUM_EXPERTS, TOPK, make_row_id_map  # noqa: F401
 
 
 def permute_mask_with_probs(inp: torch.Tensor, row_id_map: torch.Tensor, probs: torch.Tensor):
@@ -25,10 +23,6 @@ def permute_mask_with_probs(inp: torch.Tensor, row_id_map: torch.Tensor, probs: 
     if probs.shape != (tokens, experts):
         raise ValueError(f"probs {tuple(probs.shape)} expected {(tokens, experts)}")
     return permute_from_map(inp, row_id_map, probs, ops.EXPERT_MAJOR)
-
-
-def make_row_id_map(num_tokens: int = M, num_experts: int = NUM_EXPERTS, topk: int = TOPK, device="cuda"):
-    return expert_major_map(inputs.modular_routing_mask(num_tokens, num_experts, topk), torch.int64, device)
 
 
 def make_probs(row_id_map: torch.Tensor, seed: int = 0, device="cuda") -> torch.Tensor:

@@ -253,6 +253,78 @@ __global__ __launch_bounds__(256) void permute_index_kernel(const void *map, int
   }
 }
 
+// Extent of a row-id map: max(-1, max entry) and the number of entries >= 0,
+// in one pass. Each block reduces a grid-stride share of the entries (16-byte
+// loads when kVec) into partials [2 * gridDim.x]; map_extent_final_kernel adds
+// them up in block order.
+constexpr int kExtentMaxBlocks = 1024;
+template <bool kI64, bool kVec>
+__global__ __launch_bounds__(256) void map_extent_partial_kernel(const void *map, int64_t n, int64_t *partials) {
+  int64_t mx = -1, cnt = 0;
+  auto take = [&](int64_t e) {
+    mx = e > mx ? e : mx;
+    cnt += e >= 0;
+  };
+  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t gstride = static_cast<int64_t>(gridDim.x) * 256;
+  constexpr int kPer = kI64 ? 2 : 4;  // entries per 16-byte vector
+  const int64_t nvec = kVec ? n / kPer : 0;
+  for (int64_t i = gtid; i < nvec; i += gstride) {
+    const u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(map) + i);
+    if constexpr (kI64) {
+      take(static_cast<int64_t>(static_cast<uint64_t>(q.x) | (static_cast<uint64_t>(q.y) << 32)));
+      take(static_cast<int64_t>(static_cast<uint64_t>(q.z) | (static_cast<uint64_t>(q.w) << 32)));
+    } else {
+      take(static_cast<int32_t>(q.x));
+      take(static_cast<int32_t>(q.y));
+      take(static_cast<int32_t>(q.z));
+      take(static_cast<int32_t>(q.w));
+    }
+  }
+  for (int64_t i = nvec * kPer + gtid; i < n; i += gstride) take(load_idx<kI64>(map, i));
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const int64_t omx = __shfl_xor(mx, off);
+    mx = omx > mx ? omx : mx;
+    cnt += __shfl_xor(cnt, off);
+  }
+  __shared__ int64_t s_mx[256 / kWave], s_cnt[256 / kWave];
+  const int wave = threadIdx.x / kWave;
+  if (lane_id() == 0) {
+    s_mx[wave] = mx;
+    s_cnt[wave] = cnt;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 256 / kWave; ++w) {
+      mx = s_mx[w] > mx ? s_mx[w] : mx;
+      cnt += s_cnt[w];
+    }
+    partials[2 * blockIdx.x] = mx;
+    partials[2 * blockIdx.x + 1] = cnt;
+  }
+}
+
+__global__ __launch_bounds__(64) void map_extent_final_kernel(const int64_t *partials, int nblocks, int64_t *out) {
+  int64_t mx = -1, cnt = 0;
+  for (int b = threadIdx.x; b < nblocks; b += 64) {
+    mx = partials[2 * b] > mx ? partials[2 * b] : mx;
+    cnt += partials[2 * b + 1];
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const int64_t omx = __shfl_xor(mx, off);
+    mx = omx > mx ? omx : mx;
+    cnt += __shfl_xor(cnt, off);
+  }
+  if (threadIdx.x == 0) {
+    out[0] = mx;
+    out[1] = cnt;
+  }
+}
+
+int64_t map_extent_blocks(int64_t n) { return std::max<int64_t>(1, std::min<int64_t>(kExtentMaxBlocks, ceil_div(n, 256 * 16))); }
+
 __global__ __launch_bounds__(256) void fill_i32_kernel(int32_t *p, int64_t n, int32_t v) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
        i += static_cast<int64_t>(gridDim.x) * 256) {
@@ -334,6 +406,37 @@ int moe_permute(const moe_bf16_t *x, int64_t T, int64_t H, const void *row_id_ma
     return check_launch("moe_permute(zero tail)");
   }
   return MOE_OK;
+}
+
+size_t moe_map_extent_workspace_size(int64_t n) {
+  if (n < 0) return 0;
+  return static_cast<size_t>(moe::map_extent_blocks(n)) * 2 * sizeof(int64_t);
+}
+
+int moe_map_extent(const void *row_id_map, int idx_dtype, int64_t n, int64_t *out, void *workspace,
+                   size_t workspace_bytes, void *stream) {
+  using namespace moe;
+  if (n < 0) return fail(MOE_ERR_SHAPE, "moe_map_extent: negative size n=%lld", (long long)n);
+  if (idx_dtype != MOE_IDX_I32 && idx_dtype != MOE_IDX_I64) {
+    return fail(MOE_ERR_INVALID_ARG, "moe_map_extent: idx_dtype %d is not MOE_IDX_I32/I64", idx_dtype);
+  }
+  if (out == nullptr || (n > 0 && row_id_map == nullptr)) return fail(MOE_ERR_INVALID_ARG, "moe_map_extent: null map or out");
+  const size_t need = moe_map_extent_workspace_size(n);
+  if (workspace == nullptr || workspace_bytes < need || !is_aligned(workspace, 8)) {
+    return fail(MOE_ERR_WORKSPACE, "moe_map_extent: an 8-byte aligned workspace of %zu bytes is needed (got %zu)", need,
+                workspace == nullptr ? size_t(0) : workspace_bytes);
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t nb = map_extent_blocks(n);
+  int64_t *partials = static_cast<int64_t *>(workspace);
+  const bool vec = is_aligned(row_id_map, 16);
+  const bool i64 = idx_dtype == MOE_IDX_I64;
+  if (i64 && vec) map_extent_partial_kernel<true, true><<<dim3(nb), dim3(256), 0, s>>>(row_id_map, n, partials);
+  else if (i64) map_extent_partial_kernel<true, false><<<dim3(nb), dim3(256), 0, s>>>(row_id_map, n, partials);
+  else if (vec) map_extent_partial_kernel<false, true><<<dim3(nb), dim3(256), 0, s>>>(row_id_map, n, partials);
+  else map_extent_partial_kernel<false, false><<<dim3(nb), dim3(256), 0, s>>>(row_id_map, n, partials);
+  map_extent_final_kernel<<<dim3(1), dim3(64), 0, s>>>(partials, static_cast<int>(nb), out);
+  return check_launch("moe_map_extent");
 }
 
 int moe_permute_index(const void *row_id_map, int idx_dtype, int map_layout, int64_t T, int64_t E,

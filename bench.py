@@ -460,9 +460,27 @@ def config_lines(pkg, dev):
                             permuted_probs=pp), flush), 2 * T * H + 8 * T * E + 4 * T * E + 2 * R * H + 4 * R, "GB/s")
     res["unpermute (case15)"] = _rate(_median_ms(lambda: ops.unpermute(xp, em, layout=ops.EXPERT_MAJOR), flush),
                                       2 * R * H + 8 * T * E + 2 * T * H, "GB/s")
+    del xp, pp
+    # The expert-major scatter of case21/22/30 (their own (t + k) mod E routing, R = 8T) with the output row
+    # count known: the kernel alone, without the drop-ins' max/count read-back of the map.
+    c21 = pkg.cases.case21_permute_with_mask_map_trans
+    em21 = c21.make_row_id_map(device=dev)
+    R21 = 8 * T
+    x21 = inp.randn_bf16((T, H), seed=inp.SEED_CONFIG_BASE + 21, device=dev)
+    p21 = torch.rand(T, E, device=dev) * (em21 >= 0).t()
+    out21 = torch.empty(R21, H, dtype=torch.bfloat16, device=dev)
+    pp21 = torch.empty(R21, dtype=torch.float32, device=dev)
+    res["permute_expert_major (case21/30 map)"] = _rate(_median_ms(
+        lambda: ops.permute(x21, em21, num_out=R21, layout=ops.EXPERT_MAJOR, zero_tail=False, out=out21), flush),
+        2 * T * H + 8 * T * E + 2 * R21 * H, "GB/s")
+    res["permute_expert_major_with_probs (case22 map)"] = _rate(_median_ms(
+        lambda: ops.permute(x21, em21, p21, num_out=R21, layout=ops.EXPERT_MAJOR, zero_tail=False, out=out21,
+                            permuted_probs=pp21), flush), 2 * T * H + 8 * T * E + 4 * T * E + 2 * R21 * H + 4 * R21, "GB/s")
+    res["map_extent (case21 map: max and count)"] = _rate(_median_ms(lambda: ops.map_extent(em21), flush), 8 * T * E, "GB/s")
+    del x21, p21, out21, pp21, em21
     yield ({"config": "reference_shapes", "tokens": T, "hidden": H, "experts": E, "routed_rows": R,
                   "kernels": res})
-    del xr, probs, xp, pp, maps, mask
+    del xr, probs, maps, mask
     yield (reference_case_line(pkg, dev, flush))
 
 

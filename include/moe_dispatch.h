@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define MOE_DISPATCH_ABI_VERSION 9
+#define MOE_DISPATCH_ABI_VERSION 10
 
 typedef uint16_t moe_bf16_t;
 
@@ -180,6 +180,22 @@ int moe_permute(const moe_bf16_t *x, int64_t T, int64_t H, const void *row_id_ma
  * Feeds moe_grouped_gemm_gather, which then reads permuted rows straight from x. */
 int moe_permute_index(const void *row_id_map, int idx_dtype, int map_layout, int64_t T, int64_t E,
                       int32_t *src_token, int64_t num_out, int fill, void *stream);
+
+/* ---- a4'': extent of a row-id map --------------------------------------
+ * No kernel of its own in the reference: its scatter functions size their
+ * output as max(row_id_map) + 1, read back with torch
+ * (kernel_cases/case21_ref_permute_with_mask_map_trans.py:64, case22...:62,
+ * case30...:54; kernel_results/case17_moe_permute_with_mask_map/binding.cpp:24).
+ * One pass over the n entries of a map (any layout) computes both values the
+ * scatter drop-ins need:
+ *   out[0] = max(-1, largest entry)  (the output row count is out[0] + 1)
+ *   out[1] = number of entries >= 0  (== out[0] + 1 when they name every row)
+ * out: int64 [2] on the device, written by the last of two kernels (per-block
+ * partials, then their sum in block order). Workspace:
+ * moe_map_extent_workspace_size(n) bytes, 8-byte aligned. */
+size_t moe_map_extent_workspace_size(int64_t n);
+int moe_map_extent(const void *row_id_map, int idx_dtype, int64_t n, int64_t *out, void *workspace,
+                   size_t workspace_bytes, void *stream);
 
 /* ---- a8: unpermute (combine), optional probability-weighted merge ------
  * Replaces case15 kernel_function(pin, row_id_map) -> out

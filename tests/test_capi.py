@@ -17,7 +17,7 @@ L = pkg._lib
 def test_library_loads_and_exports_header_symbols():
     lib = L.lib()
     declared = L.header_functions()
-    assert len(declared) == len(L.SIGNATURES) == 27
+    assert len(declared) == len(L.SIGNATURES) == 29
     assert set(declared) == set(L.SIGNATURES)
     for name in declared:
         assert hasattr(lib, name), name
@@ -84,6 +84,10 @@ FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
     ("moe_permute_index", (FAKE, 1, 0, -4, 8, FAKE, 32, 1, None), L.MOE_ERR_SHAPE, "negative"),
     ("moe_permute_index", (FAKE, 1, 0, 1 << 31, 8, FAKE, 32, 1, None), L.MOE_ERR_CAPACITY, "int32"),
     # dgrad (dy, M, N, w, G, K, offsets, dx, ws, ws_bytes, stream)
+    ("moe_map_extent", (FAKE, L.MOE_IDX_I64, -1, FAKE, FAKE, 64, None), L.MOE_ERR_SHAPE, "negative"),
+    ("moe_map_extent", (FAKE, 7, 16, FAKE, FAKE, 64, None), L.MOE_ERR_INVALID_ARG, "idx_dtype"),
+    ("moe_map_extent", (FAKE, L.MOE_IDX_I64, 16, None, FAKE, 64, None), L.MOE_ERR_INVALID_ARG, "null"),
+    ("moe_map_extent", (FAKE, L.MOE_IDX_I64, 16, FAKE, FAKE, 8, None), L.MOE_ERR_WORKSPACE, "workspace"),
     ("moe_grouped_gemm_dgrad", (FAKE, -4, 16, FAKE, 1, 16, FAKE, FAKE, None, 0, None), L.MOE_ERR_SHAPE, "negative"),
     ("moe_grouped_gemm_dgrad", (FAKE, 4, 12, FAKE, 1, 16, FAKE, FAKE, None, 0, None), L.MOE_ERR_SHAPE, "multiples of 8"),
     ("moe_grouped_gemm_dgrad", (FAKE, 4, 16, FAKE, 1, 20, FAKE, FAKE, None, 0, None), L.MOE_ERR_SHAPE, "multiples of 8"),
@@ -157,6 +161,10 @@ def test_workspace_sizes():
     assert lib.moe_row_id_map_workspace_size(300001, 6) >= 62 * (6 + 1) * 4
     assert lib.moe_row_id_map_workspace_size(1 << 26, 32) <= 64 * 33 * 4 + 256
     assert lib.moe_permute_workspace_size(16384) >= 4096 * 4
+    # map extent: one (max, count) int64 pair per partial block, at most 1024 blocks
+    assert lib.moe_map_extent_workspace_size(0) == 16
+    assert lib.moe_map_extent_workspace_size(320 * 16384) == 1024 * 16
+    assert lib.moe_map_extent_workspace_size(-1) == 0
     assert lib.moe_row_id_map_workspace_size(-1, 4) == 0
     # router: one fp32 logits plane (used when the top-k call gets no logits output)
     assert lib.moe_router_workspace_size(16384, 8192, 320) == 16384 * 320 * 4

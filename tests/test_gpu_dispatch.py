@@ -179,6 +179,25 @@ def _padded_expert_major_map(T, E, k, pad, seed):
     return m
 
 
+@pytest.mark.parametrize("dtype", [torch.int64, torch.int32])
+def test_map_extent_matches_torch(pkg, dev, dtype):
+    # max(-1, largest entry) and the count of entries >= 0, in one pass: vector body and scalar tail,
+    # a misaligned view (scalar path), an all -1 map, an empty map, and the case21 map at full size.
+    g = torch.Generator().manual_seed(12)
+    maps = [torch.randint(-1, 1000, (37, 101), generator=g), torch.full((8, 8), -1), torch.empty(0, 5),
+            torch.randint(-1, 3, (1,), generator=g), torch.randint(-5, 70000, (300001,), generator=g)]
+    for m in maps:
+        m = m.to(dtype).to(dev)
+        mx, cnt = pkg.ops.map_extent(m)
+        ref_mx = max(int(m.max()), -1) if m.numel() else -1
+        assert (mx, cnt) == (ref_mx, int((m >= 0).sum())), (tuple(m.shape), mx, cnt)
+    base = torch.randint(-1, 50, (4097,), generator=g).to(dtype).to(dev)
+    view = base[1:]  # 4 or 8 bytes past a 16-byte boundary
+    assert pkg.ops.map_extent(view) == (int(view.max()), int((view >= 0).sum()))
+    em = pkg.cases.case21_permute_with_mask_map_trans.make_row_id_map(device=dev).to(dtype)
+    assert pkg.ops.map_extent(em) == (int(em.max()), int((em >= 0).sum()))
+
+
 @pytest.mark.parametrize("mod,fn,probs", [("case21_permute_with_mask_map_trans", "permute_with_mask_map_trans", False),
                                           ("case30_moe_permute_mask_kernel", "permute_mask", False),
                                           ("case22_moe_permute_mask_kernel_true", "permute_mask_with_probs", True)])
