@@ -515,5 +515,8 @@ def grouped_gemm_wgrad(dy: torch.Tensor, x: torch.Tensor, group_offsets: torch.T
     K = x.shape[1]
     dyc, xc, oc = dy.contiguous(), x.contiguous(), group_offsets.contiguous()
     out = _out(out, (G, N, K), torch.bfloat16, dy.device)
-    call("moe_grouped_gemm_wgrad", ptr(dyc), ptr(xc), M, N, K, G, ptr(oc), ptr(out), None, 0, stream_handle())
+    # The group order (largest first) that balances the tiles over the workgroups for skewed group sizes.
+    nbytes = _lib.lib().moe_grouped_gemm_wgrad_workspace_size(M, N, K, G)
+    ws = _ws(nbytes, dy.device)
+    call("moe_grouped_gemm_wgrad", ptr(dyc), ptr(xc), M, N, K, G, ptr(oc), ptr(out), ptr(ws), nbytes, stream_handle())
     return out

@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define MOE_DISPATCH_ABI_VERSION 10
+#define MOE_DISPATCH_ABI_VERSION 11
 
 typedef uint16_t moe_bf16_t;
 
@@ -303,7 +303,14 @@ int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, con
  *       (a group without rows gets zeros, like torch.mm over an empty K)
  * Limits: N % 8 == 0, K % 8 == 0, 1 <= G <= 4096, M_total * N, M_total * K and
  *   N * K < 2^30; dy, x, dw 16-byte aligned.
- * Workspace: none (pass NULL, 0). */
+ * Workspace: optional. With moe_grouped_gemm_wgrad_workspace_size bytes
+ *   (2-byte aligned; 2 G bytes rounded up), a first kernel lists the groups
+ *   largest first and the GEMM's tiles take them in that order, which evens
+ *   out the work per workgroup when the group sizes are skewed; each tile's
+ *   result is the same bit for bit either way. The size is 0 (no order) for
+ *   one group and where a group has more output tiles than the current
+ *   device has CUs. */
+size_t moe_grouped_gemm_wgrad_workspace_size(int64_t M_total, int64_t N, int64_t K, int64_t G);
 int moe_grouped_gemm_wgrad(const moe_bf16_t *dy, const moe_bf16_t *x, int64_t M_total, int64_t N,
                            int64_t K, int64_t G, const int32_t *group_offsets, moe_bf16_t *dw,
                            void *workspace, size_t workspace_bytes, void *stream);

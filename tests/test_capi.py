@@ -17,7 +17,7 @@ L = pkg._lib
 def test_library_loads_and_exports_header_symbols():
     lib = L.lib()
     declared = L.header_functions()
-    assert len(declared) == len(L.SIGNATURES) == 29
+    assert len(declared) == len(L.SIGNATURES) == 30
     assert set(declared) == set(L.SIGNATURES)
     for name in declared:
         assert hasattr(lib, name), name
@@ -177,6 +177,11 @@ def test_workspace_sizes():
     assert lib.moe_grouped_gemm_dgrad_workspace_size(160, 5120, 8192, 1) == 0    # 128-row tiles
     assert lib.moe_grouped_gemm_dgrad_workspace_size(288, 320, 8192, 1) == 0     # too short a reduction
     assert lib.moe_grouped_gemm_dgrad_workspace_size(288, 5128, 8192, 1) == 0    # N % 64 != 0
+    # wgrad group order: one int16 per group, only where a group has no more tiles than CUs (256 here)
+    assert lib.moe_grouped_gemm_wgrad_workspace_size(131072, 7168, 2048, 64) == 256    # c5 fc2: 28 x 8 tiles
+    assert lib.moe_grouped_gemm_wgrad_workspace_size(131072, 4096, 7168, 64) == 0      # c5 fc1: 16 x 28 tiles
+    assert lib.moe_grouped_gemm_wgrad_workspace_size(4096, 64, 64, 1) == 0
+    assert lib.moe_grouped_gemm_wgrad_workspace_size(4096, 64, 64, 4096) == 8192
     # router tf32 wgrad: [A_hi; A_hi; A_lo] and [B_hi; B_lo; B_hi] over 3M rows (+ fp32 planes when split)
     assert lib.moe_router_wgrad_tf32_workspace_size(4096, 64, 1000) >= 3 * 4096 * (64 + 1000) * 2
 

@@ -157,6 +157,28 @@ def test_wgrad_small(pkg, dev, sizes, N, K):
             assert torch.count_nonzero(out[gi]) == 0
 
 
+def test_wgrad_group_order_is_bit_identical(pkg, dev):
+    # With the workspace the tiles take the groups largest first; without it, by index. Each tile's
+    # accumulation is the same either way, so dw is bit for bit the same (skewed ragged groups,
+    # empty ones and ties included).
+    lib, ptr = pkg._lib.lib(), pkg._lib.ptr
+    sizes = [3, 0, 700, 41, 700, 0, 1500, 64, 129, 5]
+    N, K = 264, 520
+    g = torch.Generator().manual_seed(23)
+    dy = torch.randn(sum(sizes), N, generator=g).to(torch.bfloat16).to(dev)
+    x = torch.randn(sum(sizes), K, generator=g).to(torch.bfloat16).to(dev)
+    offs = _offsets(sizes, dev)
+    assert lib.moe_grouped_gemm_wgrad_workspace_size(sum(sizes), N, K, len(sizes)) > 0
+    ordered = pkg.ops.grouped_gemm_wgrad(dy, x, offs)
+    plain = torch.empty_like(ordered)
+    rc = lib.moe_grouped_gemm_wgrad(ptr(dy), ptr(x), sum(sizes), N, K, len(sizes), ptr(offs), ptr(plain), None, 0,
+                                    pkg._lib.stream_handle())
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert_bits_equal(ordered, plain, "wgrad ordered vs by index")
+    _check(ordered, ref_torch.grouped_gemm_wgrad_fp32(dy.cpu(), x.cpu(), sizes), "wgrad ordered")
+
+
 def test_wgrad_one_row_groups_exact(pkg, dev):
     # A group of one row is the outer product dy[r] x[r]^T: exact in fp32, one rounding.
     g = torch.Generator().manual_seed(91)
