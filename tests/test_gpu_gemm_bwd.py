@@ -42,6 +42,8 @@ def _offsets(sizes, dev):
     ([5, 7, 0, 100, 1], 136, 72),          # small groups (128-row tiles), tails
     ([90] * 6, 512, 1032),                 # 128-row tiles, several column tiles
     ([700, 3, 1200], 2048, 520),           # long reduction, 256-row tiles
+    ([400, 0, 333, 512], 192, 264),        # pipelined kernel at its shortest reduction (3 steps), column tail
+    ([600, 1], 6144, 72),                  # pipelined kernel, one column tile narrower than the tile
 ])
 def test_dgrad_small(pkg, dev, sizes, N, K):
     g = torch.Generator().manual_seed(sum(sizes) + 7 * N + K)
@@ -144,6 +146,7 @@ def test_dgrad_split_reduction(pkg, dev):
     ([300, 0, 17, 513], 200, 264),          # ragged, empty group, N and K tails
     ([102] * 5, 520, 1024),                 # case05/09 group size, K tail in the reduction
     ([2048, 5], 128, 264),                  # long reduction
+    ([1, 2, 0, 63, 64, 65, 127, 128, 129, 191, 192, 193] * 3, 136, 200),  # many small groups: 3-step minimum, zero steps
 ])
 def test_wgrad_small(pkg, dev, sizes, N, K):
     g = torch.Generator().manual_seed(3 * sum(sizes) + N + 5 * K)
