@@ -65,6 +65,9 @@ constexpr int kBM = 256, kBN = 256;
 #define MOE_GEMM_GROUP_M 8
 #endif
 constexpr int kGroupM = MOE_GEMM_GROUP_M;         // row tiles per tile-order group
+#ifndef MOE_GEMM_PINGPONG
+#define MOE_GEMM_PINGPONG 1
+#endif
 constexpr int kRowBytes = kBK * 2;                // 128: one tile row in LDS
 constexpr int kChunks = kBK / 8;                  // 8 chunks of 16 bytes per row
 constexpr int kOperandBytes = 256 * kRowBytes;    // 32 KiB: one 256-row operand tile
@@ -817,6 +820,405 @@ __global__ __launch_bounds__(256) void grouped_gemm_pipe_kernel(GemmArgs p) {
   }
   wait_dma();  // no LDS DMA outlives the workgroup
 }
+
+// ---------------------------------------------------------------------------
+// Ping-pong forward kernel (the default for K % 64 == 0, K >= 192, 16-byte
+// output rows): 8 wavefronts, two per SIMD, output tile 256 x 256, K step 64.
+//
+// With one wavefront per SIMD every LDS-DMA instruction (buffer_load ... lds,
+// about 40 cycles of issue each under load, 16 per wavefront per K step) and
+// every fragment read stalls that SIMD's MFMA stream. Here the two wavefronts
+// of a SIMD take turns: in each phase one of them issues its 64 MFMAs (one K
+// step of its 64 x 128 part of the tile, fragments in VGPRs) while the other
+// reads its fragments of the next stage from LDS and issues its share of the
+// stage DMAs; a workgroup barrier ends every phase and the roles swap.
+//
+// Groups: the two wavefronts of a SIMD (found from the hardware wave id at
+// start) form group 0 and group 1; wm = SIMD index selects the tile's rows
+// wm * 64 .. + 63, the group its columns grp * 128 .. + 127. Group 0 loads
+// stage s in phase 2s and multiplies it in phase 2s + 1; group 1 one phase
+// later.
+//
+// LDS (160 KiB): A ring of 3 slots (256 rows x 64 K), B ring of 2 slots (the
+// 128 B rows of group 0, then those of group 1). Stage s of A is read in
+// phases 2s and 2s + 1, group 0's B half in phase 2s, group 1's in phase
+// 2s + 1. In the load phase of stage s, group 0 DMAs its half of A stage
+// s + 2 and group 1's B half of stage s + 1, group 1 its half of A stage s + 2
+// and group 0's B half of stage s + 2: each slot is rewritten only after the
+// barrier that ends its last reader's phase, and every DMA has two phases to
+// land (its issuer waits for it at the end of its next load phase, before the
+// barrier that precedes its readers).
+//
+// The epilogue of a tile (same register layout as the pipelined kernel) runs
+// in the wavefront's next load phase; the stores are issued before that
+// phase's DMAs and are allowed to stay in flight across its barrier.
+template <bool kSwiglu, bool kGather>
+__global__ __launch_bounds__(512) void grouped_gemm_pp_kernel(GemmArgs p) {
+  constexpr int kAS = 3, kBS = 2;                   // ring slots
+  constexpr int kSlotBytes = 256 * kRowBytes;       // 32 KiB: 256 rows x 64 K
+  constexpr int kBBase = kAS * kSlotBytes;
+  constexpr int kEpiCols = kSwiglu ? kBN / 2 : kBN;  // output columns of a tile
+  constexpr int kMI = 4, kNI = 8;                    // 16 x 16 blocks of a wavefront
+  constexpr int kStores = kSwiglu ? 8 : 16;          // 16-byte stores per lane per tile
+  constexpr int kDmaA = 4, kDmaB = 4;                // DMA instructions per wavefront per load phase
+  static_assert(kDmaA + kDmaB + kStores <= 63, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) char smem[kAS * kSlotBytes + kBS * kSlotBytes];
+  lds_char *const sbase = (lds_char *)smem;
+  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sbase));
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // ---- roles from the SIMD each wavefront runs on (HW_ID bits 5:4): the two
+  // wavefronts of a SIMD must be in different groups. Exchanged through LDS
+  // before the ring is used.
+  int wm, grp;
+  {
+    const int simd = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_s_getreg((1 << 11) | (4 << 6) | 4)) & 3;
+    volatile int *sid = reinterpret_cast<volatile int *>(smem);
+    if (lane == 0) sid[wave] = simd;
+    __syncthreads();
+    int before = 0, per_simd[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      const int s = sid[w] & 3;
+      per_simd[s] += 1;
+      before += (s == simd) && (w < wave);
+    }
+    __syncthreads();
+    // Two wavefronts per SIMD (the register budget allows no more); if the
+    // hardware placed them otherwise, every wavefront falls back to
+    // wave-index roles (the test reads the same 8 values in every wavefront).
+    const bool ok = per_simd[0] == 2 && per_simd[1] == 2 && per_simd[2] == 2 && per_simd[3] == 2;
+    // Wave-uniform (scalar) roles: every DMA resource and offset derived from
+    // them stays in scalar registers.
+    wm = __builtin_amdgcn_readfirstlane(ok ? simd : (wave & 3));
+    grp = __builtin_amdgcn_readfirstlane(ok ? before : (wave >> 2));
+  }
+
+  const int64_t P = gridDim.x;
+  const int64_t b = blockIdx.x;
+  const int64_t K = p.K;
+  const int S = static_cast<int>(K / kBK);  // K steps per tile (>= 3, K % 64 == 0: host)
+
+  // ---- tile walker (group offsets read from memory: the ring fills the LDS)
+  auto group_rows = [&](int64_t g, int64_t &lo, int64_t &hi) {
+    lo = min(max(static_cast<int64_t>(p.offsets[g]), int64_t(0)), p.M);
+    hi = min(max(static_cast<int64_t>(p.offsets[g + 1]), lo), p.M);
+  };
+  int64_t g_cur = 0, tiles_before = 0, m_lo, m_hi;
+  group_rows(0, m_lo, m_hi);
+  int64_t mt_g = ceil_div(m_hi - m_lo, kBM);
+  struct Tile {
+    int64_t g, row0;
+    uint32_t nt;
+    int rows_valid;
+  };
+  auto find_tile = [&](int64_t round, Tile &t) -> bool {
+    const int64_t L = round * P + (b % 8) * (P / 8) + b / 8;
+    while (g_cur < p.G && L >= tiles_before + mt_g * p.ntiles) {
+      tiles_before += mt_g * p.ntiles;
+      ++g_cur;
+      if (g_cur < p.G) {
+        group_rows(g_cur, m_lo, m_hi);
+        mt_g = ceil_div(m_hi - m_lo, kBM);
+      }
+    }
+    if (g_cur >= p.G) return false;
+    const uint32_t q = static_cast<uint32_t>(L - tiles_before);
+    const uint32_t ntl = static_cast<uint32_t>(p.ntiles);
+    const uint32_t per_grp = kGroupM * ntl;
+    const uint32_t full = static_cast<uint32_t>(mt_g) / kGroupM;
+    uint32_t mt, nt;
+    if (q < full * per_grp) {
+      const uint32_t gq = q / per_grp, r = q - gq * per_grp;
+      nt = r / kGroupM;
+      mt = gq * kGroupM + r % kGroupM;
+    } else {
+      const uint32_t r = q - full * per_grp, gm = static_cast<uint32_t>(mt_g) - full * kGroupM;
+      nt = r / gm;
+      mt = full * kGroupM + (r - nt * gm);
+    }
+    t.g = g_cur;
+    t.row0 = m_lo + static_cast<int64_t>(mt) * kBM;
+    t.nt = nt;
+    t.rows_valid = static_cast<int>(min(m_hi - t.row0, int64_t(kBM)));
+    return true;
+  };
+
+  // ---- DMA sources. This wavefront's A rows: blocks (grp * 16 + j * 4 + wm),
+  // 8 rows each; its B rows: blocks ((1 - grp) * 16 + j * 4 + wm) (the other
+  // group's half, see above).
+  const uint32_t row_bytes = static_cast<uint32_t>(K) * 2u;
+  const int ncols32 = static_cast<int>(p.ncols);
+  const int src_rows32 = static_cast<int>(min(p.a_src_rows, int64_t(0x7fffffff)));
+  auto a_row = [&](int j, int ln) { return ((grp * 16 + j * 4 + wm) * kRowsPerKiB) + ln / kChunks; };
+  auto b_row = [&](int j, int ln) { return (((1 - grp) * 16 + j * 4 + wm) * kRowsPerKiB) + ln / kChunks; };
+  int32_t src_rows[kDmaA];
+  auto load_rows = [&](const Tile &t, bool valid) {
+    if constexpr (kGather) {
+      const __amdgpu_buffer_rsrc_t r_rows = make_rsrc(p.a_rows, valid ? static_cast<uint32_t>(p.M * 4) : 0u);
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const uint32_t row0 = static_cast<uint32_t>(t.row0);
+#pragma unroll
+      for (int j = 0; j < kDmaA; ++j) {
+        const uint32_t off = (row0 + static_cast<uint32_t>(min(a_row(j, ln), max(t.rows_valid - 1, 0)))) * 4u;
+#if defined(__HIP_DEVICE_COMPILE__)
+        src_rows[j] = __builtin_amdgcn_raw_buffer_load_b32(r_rows, static_cast<int>(off), 0, 0);
+#else
+        (void)off;
+        (void)r_rows;
+        src_rows[j] = 0;
+#endif
+      }
+    } else {
+      (void)t;
+      (void)valid;
+    }
+  };
+  __amdgpu_buffer_rsrc_t ra, rb;
+  // A: per-lane offsets (gather: data-dependent rows); B: one per-lane base,
+  // the rows of DMA j lie b_step(j) rows further (wave-uniform).
+  int a_off[kDmaA];
+  int b_base = 0;
+  uint32_t b_ncols = 0;  // SwiGLU: rows from a gate row to its up row (ncols), in bytes
+  auto setup_a = [&](const Tile &t, bool valid) {
+    ra = kGather ? make_rsrc(p.a, valid ? static_cast<uint32_t>(p.a_src_rows * K * 2) : 0u)
+                 : make_rsrc(p.a + t.row0 * K, valid ? static_cast<uint32_t>(t.rows_valid) * row_bytes : 0u);
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+#pragma unroll
+    for (int j = 0; j < kDmaA; ++j) {
+      const int r = a_row(j, ln);
+      const uint32_t lbytes = static_cast<uint32_t>((ln % kChunks) ^ swz(r)) * 16u;
+      if constexpr (kGather) {
+        const int32_t src = src_rows[j];
+        a_off[j] = (r < t.rows_valid && src >= 0 && src < src_rows32)
+                       ? static_cast<int>(static_cast<uint32_t>(src) * row_bytes + lbytes)
+                       : static_cast<int>(kNoAccess);
+      } else {
+        // Rows past the group's end lie past the resource: zeros.
+        a_off[j] = static_cast<int>(static_cast<uint32_t>(r) * row_bytes + lbytes);
+      }
+    }
+  };
+  // B row of tile row r: plain nt * 256 + r (rows past N lie past the
+  // resource: zeros); SwiGLU: half h = r / 128 holds 64 gate rows of output
+  // columns c = nt * 128 + h * 64 .., then the 64 up rows (ncols + c) of the
+  // same columns. A gate column past ncols reads an up row (in bounds, its
+  // output column is dropped); its up row lies past the resource.
+  // This wavefront's DMA j covers tile rows b_row(0) + 32 j; j = 0, 1 are gate
+  // rows and 2, 3 up rows (SwiGLU), so DMA j reads B row
+  // brow(0) + 32 (j % 2) (+ ncols for j >= 2): one base plus a uniform step.
+  auto setup_b = [&](const Tile &t, bool valid) {
+    rb = make_rsrc(p.w + t.g * p.N * K, valid ? static_cast<uint32_t>(p.N * K * 2) : 0u);
+    const int nt = static_cast<int>(t.nt);
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int r = b_row(0, ln);
+    const uint32_t lbytes = static_cast<uint32_t>((ln % kChunks) ^ swz(r)) * 16u;
+    int brow;
+    if constexpr (kSwiglu) {
+      brow = nt * (kBN / 2) + (r >> 7) * 64 + (r & 63);
+      b_ncols = static_cast<uint32_t>(ncols32) * row_bytes;
+    } else {
+      brow = nt * kBN + r;
+    }
+    b_base = static_cast<int>(static_cast<uint32_t>(brow) * row_bytes + lbytes);
+  };
+  auto b_off = [&](int j) -> int {
+    if constexpr (kSwiglu) {
+      return b_base + static_cast<int>((j & 1) * 32u * row_bytes + (j >= 2 ? b_ncols : 0u));
+    } else {
+      return b_base + static_cast<int>(static_cast<uint32_t>(j) * 32u * row_bytes);
+    }
+  };
+  // DMA of this wavefront's share of A stage kt into A slot sa and of its B
+  // rows of stage kt_b into B slot sb.
+  auto issue = [&](int kt_a, int sa, int kt_b, int sbs) {
+    const uint32_t a_dst = lds_base + sa * kSlotBytes;
+    const uint32_t b_dst = lds_base + kBBase + sbs * kSlotBytes;
+#pragma unroll
+    for (int j = 0; j < kDmaA; ++j) {
+      const uint32_t blk = grp * 16 + j * 4 + wm;
+      dma16b(ra, (lds_void *)(uintptr_t)(a_dst + blk * 1024), a_off[j], kt_a * kBK * 2);
+    }
+#pragma unroll
+    for (int j = 0; j < kDmaB; ++j) {
+      const uint32_t blk = (1 - grp) * 16 + j * 4 + wm;
+      dma16b(rb, (lds_void *)(uintptr_t)(b_dst + blk * 1024), b_off(j), kt_b * kBK * 2);
+    }
+  };
+
+  // ---- fragments (v_mfma_f32_16x16x32_bf16 layout as in the pipelined kernel)
+  const int fq = lane >> 4;
+  const int ra0 = wm * 64 + (lane & 15);
+  const int rb0 = grp * 128 + (lane & 15);
+  const uint32_t fa0 = ra0 * kRowBytes + ((fq ^ swz(ra0)) << 4);
+  const uint32_t fb0 = rb0 * kRowBytes + ((fq ^ swz(rb0)) << 4);
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  f32x4 acc[kMI][kNI];
+  bf16x8 fa[2][kMI], fb[2][kNI];
+  auto read_frags = [&](int sa, int sbs) {
+    const uint32_t a_base = lds_base + sa * kSlotBytes + fa0;
+    const uint32_t b_base = lds_base + kBBase + sbs * kSlotBytes + fb0;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int i = 0; i < kMI; ++i)
+        fa[ks][i] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)((a_base ^ (ks << 6)) + i * 16 * kRowBytes));
+#pragma unroll
+      for (int j = 0; j < kNI; ++j)
+        fb[ks][j] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)((b_base ^ (ks << 6)) + j * 16 * kRowBytes));
+    }
+  };
+  auto compute = [&](auto zero_c) {
+    constexpr bool zero = decltype(zero_c)::value;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int i = 0; i < kMI; ++i)
+#pragma unroll
+        for (int j = 0; j < kNI; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[ks][j], fa[ks][i],
+                                                             (zero && ks == 0) ? f32x4{} : acc[i][j], 0, 0, 0);
+  };
+  auto epilogue = [&](const Tile &t) {
+    const uint32_t ld = static_cast<uint32_t>(p.ncols) * 2u;
+    const __amdgpu_buffer_rsrc_t ro =
+        make_rsrc(p.out + t.row0 * p.ncols, static_cast<uint32_t>(t.rows_valid) * ld);
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int eq = ln >> 4;
+    const int wcol0 = static_cast<int>(t.nt) * kEpiCols + grp * (kEpiCols / 2) + (eq & 1) * 16 + (eq >> 1) * 8;
+    constexpr int kOut16 = kSwiglu ? kNI / 2 : kNI;
+#pragma unroll
+    for (int i = 0; i < kMI; ++i) {
+      const uint32_t orow = static_cast<uint32_t>(wm * 64 + i * 16 + (ln & 15));
+#pragma unroll
+      for (int jp = 0; jp < kOut16; jp += 2) {
+        uint32_t w[2][2];
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+          float h[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if constexpr (kSwiglu) {
+              const float gt = acc[i][jp + d][q];
+              h[q] = gt * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gt * -1.4426950408889634f)) *
+                     acc[i][jp + d + kNI / 2][q];
+            } else {
+              h[q] = acc[i][jp + d][q];
+            }
+          }
+          const bf16x2 lo = {(__bf16)h[0], (__bf16)h[1]};
+          const bf16x2 hi = {(__bf16)h[2], (__bf16)h[3]};
+          w[d][0] = __builtin_bit_cast(uint32_t, lo);
+          w[d][1] = __builtin_bit_cast(uint32_t, hi);
+        }
+        u32x4 o;
+#if defined(__HIP_DEVICE_COMPILE__)
+        const auto s0 = __builtin_amdgcn_permlane16_swap(w[0][0], w[1][0], false, false);
+        const auto s1 = __builtin_amdgcn_permlane16_swap(w[0][1], w[1][1], false, false);
+        o = u32x4{s0[0], s1[0], s0[1], s1[1]};
+#else
+        o = u32x4{0u, 0u, 0u, 0u};
+#endif
+        const int gcol = wcol0 + jp * 16;
+        const uint32_t off = gcol < ncols32 ? orow * ld + static_cast<uint32_t>(gcol) * 2u : kNoAccess;
+#if defined(__HIP_DEVICE_COMPILE__)
+        __builtin_amdgcn_raw_buffer_store_b128(o, ro, static_cast<int>(off), 0, 0);
+#else
+        (void)off;
+        (void)ro;
+        (void)o;
+#endif
+      }
+    }
+  };
+
+  // ---- prologue: A stages 0 and 1, group 0's B rows of stages 0 and 1 (by
+  // group 1), group 1's B rows of stage 0 (by group 0).
+  Tile cur{}, nxt{};
+  if (!find_tile(0, cur)) return;
+  load_rows(cur, true);
+  setup_a(cur, true);
+  setup_b(cur, true);
+  {
+    const uint32_t b_dst0 = lds_base + kBBase;
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+      for (int j = 0; j < kDmaA; ++j) {
+        const uint32_t blk = grp * 16 + j * 4 + wm;
+        dma16b(ra, (lds_void *)(uintptr_t)(lds_base + kt * kSlotBytes + blk * 1024), a_off[j], kt * kBK * 2);
+      }
+    }
+    const int nb = grp == 1 ? 2 : 1;
+    for (int kt = 0; kt < nb; ++kt) {
+#pragma unroll
+      for (int j = 0; j < kDmaB; ++j) {
+        const uint32_t blk = (1 - grp) * 16 + j * 4 + wm;
+        dma16b(rb, (lds_void *)(uintptr_t)(b_dst0 + kt * kSlotBytes + blk * 1024), b_off(j), kt * kBK * 2);
+      }
+    }
+  }
+  bool more = find_tile(1, nxt);
+  wait_dma();
+  barrier();
+  if (grp == 1) barrier();  // group 1 runs one phase behind
+
+  int slot_a = 0, slot_b = 0;  // ring slots of the stage being read
+  bool have_prev = false;
+  Tile prev{};
+  for (int64_t round = 0;; ++round) {
+    for (int s = 0; s < S; ++s) {
+      // ---------------- load phase of stage s
+      if (kGather && s == S - 3) load_rows(nxt, more);  // before this phase's other memory operations
+      const bool epi = s == 0 && have_prev;
+      if (epi) epilogue(prev);
+      __builtin_amdgcn_sched_barrier(0);
+      read_frags(slot_a, slot_b);
+      const int ta = s + 2, tb = s + 1 + grp;  // stages this phase DMAs (of this tile or the next)
+      if (ta == S) setup_a(nxt, more);
+      if (tb == S) setup_b(nxt, more);
+      int sa = slot_a + 2;
+      sa = sa >= kAS ? sa - kAS : sa;
+      const int sbs = (slot_b + 1 + grp) & 1;
+      issue(ta >= S ? ta - S : ta, sa, tb >= S ? tb - S : tb, sbs);
+      // The previous load phase's DMAs have landed (only this phase's DMAs,
+      // and the epilogue stores issued before them, may still be in flight).
+      if (epi) {
+        wait_vm_n<kDmaA + kDmaB + kStores>();
+      } else {
+        wait_vm_n<kDmaA + kDmaB>();
+      }
+      wait_lds();
+      barrier();
+      // ---------------- compute phase of stage s
+      if (s == 0) {
+        compute(std::true_type{});
+      } else {
+        compute(std::false_type{});
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      barrier();
+      slot_a = slot_a + 1 == kAS ? 0 : slot_a + 1;
+      slot_b ^= 1;
+    }
+    prev = cur;
+    have_prev = true;
+    if (!more) break;
+    cur = nxt;
+    more = find_tile(round + 2, nxt);
+  }
+  // Last tile's epilogue in a final load phase; group 0 passes one more
+  // barrier so that both groups pass the same number.
+  epilogue(prev);
+  if (grp == 0) barrier();
+  wait_dma();  // no LDS DMA outlives the workgroup
+}
 }  // namespace
 }  // namespace moe
 
@@ -874,7 +1276,17 @@ int launch_grouped_gemm(const char *fn, const moe_bf16_t *a, int64_t a_src_rows,
   // The pipelined kernel needs three K steps per tile, 16-byte output rows, a
   // 256-row output panel below 2 GiB and (gather) 32-bit offsets into a_rows.
   const bool pipe = K > 2 * kBK && p.vec_out && ncols < (int64_t(1) << 22) && (!gather || M_total < (int64_t(1) << 29));
-  if (pipe) {
+  // The ping-pong kernel: the same conditions and whole K steps.
+  const bool pingpong = MOE_GEMM_PINGPONG && pipe && K % kBK == 0;
+  if (pingpong) {
+    if (swiglu) {
+      if (gather) grouped_gemm_pp_kernel<true, true><<<dim3(grid), dim3(512), 0, s>>>(p);
+      else grouped_gemm_pp_kernel<true, false><<<dim3(grid), dim3(512), 0, s>>>(p);
+    } else {
+      if (gather) grouped_gemm_pp_kernel<false, true><<<dim3(grid), dim3(512), 0, s>>>(p);
+      else grouped_gemm_pp_kernel<false, false><<<dim3(grid), dim3(512), 0, s>>>(p);
+    }
+  } else if (pipe) {
     if (swiglu) {
       if (gather) grouped_gemm_pipe_kernel<true, true><<<dim3(grid), dim3(256), 0, s>>>(p);
       else grouped_gemm_pipe_kernel<true, false><<<dim3(grid), dim3(256), 0, s>>>(p);

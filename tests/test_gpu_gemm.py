@@ -120,6 +120,13 @@ def test_grouped_gemm_errors(pkg, dev):
 
 @pytest.mark.parametrize("sizes,K,N,swiglu,gather", [
     ([300, 0, 17, 513], 200, 264, False, False),      # ragged, empty group, K and N tails
+    # K % 64 == 0 runs the two-wavefronts-per-SIMD kernel:
+    ([300, 0, 17, 513], 192, 264, False, False),      # three K steps, N tail, ragged, empty group
+    ([1, 0, 2], 192, 8, False, False),                # tiny groups, one partial column tile
+    ([40] * 600, 256, 512, False, False),             # 600 groups: many tile changes per workgroup
+    ([100, 0, 333], 192, 272, True, True),            # SwiGLU with 136 output columns, gather
+    ([257, 255, 0, 513], 320, 1024, True, False),     # row tails of 1 and 255, SwiGLU
+    ([40] * 300, 384, 512, False, True),              # gather, many groups
     ([40] * 600, 200, 512, False, False),             # 600 groups: many tile changes per workgroup
     ([2000, 3, 1500], 2048, 7168, False, False),      # fc2 class, several tiles per workgroup
     ([64, 700, 0, 1500], 7168, 4096, True, False),    # fc1 class
