@@ -49,6 +49,7 @@
 // x all column tiles; workgroup b takes tile round * P + (b % 8) * (P / 8) + b / 8
 // so each XCD works on one patch per round.
 #include <algorithm>
+#include <type_traits>
 
 #include "gemm_device.h"
 
@@ -963,11 +964,405 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_pipe_kernel(BwdArgs p) {
   wait_dma();  // no LDS DMA outlives the workgroup
 }
 
+// Fragment of an RM operand whose LDS rows are kRow bytes apart: 8 consecutive
+// reduction values of one column per lane, from two transposing reads 4 rows apart.
+template <int kRow>
+__device__ __forceinline__ bf16x8 read_rm_frag_rows(uint32_t addr) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const v4bf16 lo = read_tr((lds_v4bf16 *)(uintptr_t)addr);
+  const v4bf16 hi = read_tr((lds_v4bf16 *)(uintptr_t)(addr + 4 * kRow));
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#else
+  (void)addr;
+  return bf16x8{};
+#endif
+}
+
+// Ping-pong backward kernel (bf16 output; dgrad with N % 64 == 0 and N >= 192,
+// and wgrad): the forward ping-pong kernel's schedule on the backward operands.
+// 8 wavefronts, two per SIMD taking turns: in each phase one issues its 64
+// MFMAs (a 64 x 128 part of the 256 x 256 tile: rows wm * 64 .., wm = its
+// SIMD; columns grp * 128 .., grp = its group) while the other reads its
+// fragments of the next stage and issues its share of the stage DMAs; a
+// workgroup barrier ends every phase.
+//
+// LDS (160 KiB): A in 3 slots of 32 KiB (read by both groups; dgrad's dy as
+// 256 rows x 128 bytes, wgrad's dy as 64 reduction rows x 512 bytes), B in 2
+// slots, each holding the two groups' column halves as separate 64 x 256-byte
+// RM tiles (a DMA block is 4 reduction rows of one half, so each group's half
+// is loaded by the other group on its own schedule). The 16-byte chunk swizzle
+// of the RM tiles (rm16_swz) stays within 256-byte segments, so the half tiles
+// keep the full-row tiles' conflict-free transposing reads.
+//
+// Stage schedule, waits and slot reuse as in grouped_gemm_pp_kernel: in its
+// load phase of stage s a wavefront DMAs its group's half of A stage s + 2 and
+// the other group's B half of stage s + 1 (group 0) or s + 2 (group 1); each
+// DMA is waited for at the end of its issuer's next load phase (vmcnt <= 8, or
+// 8 + 16 after an epilogue's stores). A tile's reduction step count varies
+// (wgrad: its group's rows), stages past a tile's end come from the next tile.
+template <bool kWgrad, bool kOrder>
+__global__ __launch_bounds__(512) void grouped_gemm_bwd_pp_kernel(BwdArgs p) {
+  static_assert(!kOrder || kWgrad, "the group order is a wgrad schedule");
+  constexpr int kBM = 256;
+  constexpr int kAS = 3, kBS = 2;
+  constexpr int kSlotBytes = 256 * kBK * 2;  // 32 KiB
+  constexpr int kHalfBytes = kSlotBytes / 2;  // one group's B columns
+  constexpr int kBBase = kAS * kSlotBytes;
+  constexpr int kHalfRow = 256;               // bytes per reduction row of a B half tile
+  constexpr int kMI = 4, kNI = 8;
+  constexpr int kStores = 16;                 // 16-byte stores per lane per tile
+  constexpr int kDmaA = 4, kDmaB = 4;
+  static_assert(kDmaA + kDmaB + kStores <= 63, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) char smem[kAS * kSlotBytes + kBS * kSlotBytes];
+  lds_char *const sbase = (lds_char *)smem;
+  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sbase));
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // ---- roles from the SIMD each wavefront runs on (as in grouped_gemm_pp_kernel)
+  int wm, grp;
+  {
+    const int simd = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_s_getreg((1 << 11) | (4 << 6) | 4)) & 3;
+    volatile int *sid = reinterpret_cast<volatile int *>(smem);
+    if (lane == 0) sid[wave] = simd;
+    __syncthreads();
+    int before = 0, per_simd[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      const int s = sid[w] & 3;
+      per_simd[s] += 1;
+      before += (s == simd) && (w < wave);
+    }
+    __syncthreads();
+    const bool ok = per_simd[0] == 2 && per_simd[1] == 2 && per_simd[2] == 2 && per_simd[3] == 2;
+    wm = __builtin_amdgcn_readfirstlane(ok ? simd : (wave & 3));
+    grp = __builtin_amdgcn_readfirstlane(ok ? before : (wave >> 2));
+  }
+
+  const int64_t P = gridDim.x;
+  const int64_t b = blockIdx.x;
+  const int64_t N = p.N, K = p.K;
+
+  // ---- tile walker (group offsets and order read from memory: the ring fills the LDS)
+  const int m32 = static_cast<int>(p.M);
+  const int g_count = static_cast<int>(p.G);
+  auto group_range = [&](int g, int &lo, int &hi) {
+    lo = min(max(__builtin_amdgcn_readfirstlane(p.offsets[g]), 0), m32);
+    hi = min(max(__builtin_amdgcn_readfirstlane(p.offsets[g + 1]), lo), m32);
+  };
+  const uint32_t ntl = static_cast<uint32_t>(p.ntiles);
+  const uint32_t wg_rows = static_cast<uint32_t>(ceil_div(N, kBM));
+  auto row_tiles = [&](int lo, int hi) -> uint32_t {
+    return kWgrad ? wg_rows : static_cast<uint32_t>(hi - lo + kBM - 1) / kBM;
+  };
+  auto group_at = [&](int i) -> int {
+    if constexpr (kOrder) {
+      return min(max(__builtin_amdgcn_readfirstlane(static_cast<int>(p.order[i])), 0), g_count - 1);
+    } else {
+      return i;
+    }
+  };
+  int g_cur = 0, g_act = group_at(0), g_lo, g_hi;
+  uint32_t tiles_before = 0;
+  group_range(g_act, g_lo, g_hi);
+  uint32_t mt_g = row_tiles(g_lo, g_hi);
+  struct Tile {
+    int g, lo, hi;
+    int i0;
+    uint32_t nt;
+    int rows_valid;
+    int ktiles;
+  };
+  const uint32_t P32 = static_cast<uint32_t>(P);
+  const uint32_t L0 = static_cast<uint32_t>((b % 8) * (P / 8) + b / 8);
+  auto find_tile = [&](uint32_t round, Tile &t) -> bool {
+    const uint32_t L = round * P32 + L0;
+    while (g_cur < g_count && L >= tiles_before + mt_g * ntl) {
+      tiles_before += mt_g * ntl;
+      ++g_cur;
+      if (g_cur < g_count) {
+        g_act = group_at(g_cur);
+        group_range(g_act, g_lo, g_hi);
+        mt_g = row_tiles(g_lo, g_hi);
+      }
+    }
+    if (g_cur >= g_count) return false;
+    const uint32_t q = L - tiles_before;
+    const uint32_t per_grp = kGroupM * ntl;
+    const uint32_t full = mt_g / kGroupM;
+    uint32_t mt, nt;
+    if (q < full * per_grp) {
+      const uint32_t gq = q / per_grp, r = q - gq * per_grp;
+      nt = r / kGroupM;
+      mt = gq * kGroupM + r % kGroupM;
+    } else {
+      const uint32_t r = q - full * per_grp, gm = mt_g - full * kGroupM;
+      nt = r / gm;
+      mt = full * kGroupM + (r - nt * gm);
+    }
+    t.g = g_act;
+    t.lo = g_lo;
+    t.hi = g_hi;
+    t.i0 = (kWgrad ? 0 : g_lo) + static_cast<int>(mt) * kBM;
+    t.nt = nt;
+    t.rows_valid = min((kWgrad ? static_cast<int>(N) : g_hi) - t.i0, kBM);
+    const int red = kWgrad ? g_hi - g_lo : static_cast<int>(N);
+    t.ktiles = max((red + kBK - 1) / kBK, 3);
+    return true;
+  };
+
+  // ---- DMA sources: A blocks (grp * 16 + j * 4 + wm) of a stage; B blocks
+  // (j * 4 + wm) of the other group's half.
+  const uint32_t n32 = static_cast<uint32_t>(N), k32 = static_cast<uint32_t>(K);
+  __amdgpu_buffer_rsrc_t ra, rb;
+  int a_off[kDmaA];
+  int b_base = 0;
+  const int a_step = kWgrad ? kBK * static_cast<int>(n32) * 2 : kBK * 2;  // bytes per reduction step
+  const int b_step = kBK * static_cast<int>(k32) * 2;
+  auto setup_a = [&](const Tile &t, bool valid) {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    if constexpr (kWgrad) {
+      const uint32_t rows = valid ? static_cast<uint32_t>(t.hi - t.lo) : 0u;
+      ra = make_rsrc(p.a + static_cast<int64_t>(t.lo) * N, rows * n32 * 2u);
+#pragma unroll
+      for (int j = 0; j < kDmaA; ++j) {
+        const int krow = (grp * 16 + j * 4 + wm) * 2 + (ln >> 5);
+        const uint32_t lchunk = static_cast<uint32_t>((ln & 31) ^ rm16_swz(krow));
+        a_off[j] = static_cast<int>(static_cast<uint32_t>(krow) * n32 * 2u + static_cast<uint32_t>(t.i0) * 2u + lchunk * 16u);
+      }
+    } else {
+      // Rows past the tile's valid rows lie past the resource: zeros.
+      ra = make_rsrc(p.a + static_cast<int64_t>(t.i0) * N, valid ? static_cast<uint32_t>(t.rows_valid) * n32 * 2u : 0u);
+#pragma unroll
+      for (int j = 0; j < kDmaA; ++j) {
+        const int r = (grp * 16 + j * 4 + wm) * 8 + (ln >> 3);
+        const uint32_t lchunk = static_cast<uint32_t>((ln & 7) ^ kc_swz(r));
+        a_off[j] = static_cast<int>(static_cast<uint32_t>(r) * n32 * 2u + lchunk * 16u);
+      }
+    }
+  };
+  // B half h = 1 - grp: reduction row krow = (j * 4 + wm) * 4 + ln / 16 of DMA j
+  // (its swizzle does not depend on j, so DMA j is the base + 16 j rows), 16
+  // chunks of columns nt * 256 + h * 128 ...
+  auto setup_b = [&](const Tile &t, bool valid) {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    if constexpr (kWgrad) {
+      const uint32_t rows = valid ? static_cast<uint32_t>(t.hi - t.lo) : 0u;
+      rb = make_rsrc(p.b + static_cast<int64_t>(t.lo) * K, rows * k32 * 2u);
+    } else {
+      rb = make_rsrc(p.b + static_cast<int64_t>(t.g) * N * K, valid ? static_cast<uint32_t>(N * K * 2) : 0u);
+    }
+    const int krow = wm * 4 + (ln >> 4);
+    const uint32_t lchunk = static_cast<uint32_t>((ln & 15) ^ rm16_swz(krow));
+    const uint32_t col0 = t.nt * static_cast<uint32_t>(kBN) + static_cast<uint32_t>(1 - grp) * 128u;
+    b_base = static_cast<int>(static_cast<uint32_t>(krow) * k32 * 2u + col0 * 2u + lchunk * 16u);
+  };
+  auto issue = [&](int kt_a, int sa, int kt_b, int sbs) {
+    const uint32_t a_dst = lds_base + sa * kSlotBytes;
+    const uint32_t b_dst = lds_base + kBBase + sbs * kSlotBytes + (1 - grp) * kHalfBytes;
+#pragma unroll
+    for (int j = 0; j < kDmaA; ++j) {
+      const uint32_t blk = grp * 16 + j * 4 + wm;
+      dma16b(ra, (lds_void *)(uintptr_t)(a_dst + blk * 1024), a_off[j], kt_a * a_step);
+    }
+#pragma unroll
+    for (int j = 0; j < kDmaB; ++j) {
+      const uint32_t blk = j * 4 + wm;
+      dma16b(rb, (lds_void *)(uintptr_t)(b_dst + blk * 1024), b_base + j * 16 * static_cast<int>(k32) * 2,
+             kt_b * b_step);
+    }
+  };
+
+  // ---- fragments
+  const int fq = lane >> 4;
+  const int ra0 = wm * 64 + (lane & 15);
+  const uint32_t fa0 = ra0 * kKCRow + ((fq ^ kc_swz(ra0)) << 4);  // dgrad A (KC)
+  const int rg = lane >> 4, rj = (lane >> 2) & 3, rq = lane & 3;
+  const uint32_t rm_in = ((rq >> 1) << 4) + (rq & 1) * 8;
+  const uint32_t rma0 = (8 * rg + rj) * kRMRow + rm_in;              // wgrad A: full 512-byte rows
+  const uint32_t rmb0 = (8 * rg + rj) * kHalfRow + rm_in;            // B: this group's half tile
+  const uint32_t rmx = static_cast<uint32_t>((rj << 1) | (rg & 1)) << 5;
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  f32x4 acc[kMI][kNI];
+  bf16x8 fa[2][kMI], fb[2][kNI];
+  auto read_frags = [&](int sa, int sbs) {
+    uint32_t x = rmx;
+    asm volatile("" : "+v"(x));
+    const uint32_t b_base_l = lds_base + kBBase + sbs * kSlotBytes + grp * kHalfBytes + rmb0;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      if constexpr (kWgrad) {
+        const uint32_t a_base_l = lds_base + sa * kSlotBytes + rma0 + ks * 32 * kRMRow;
+#pragma unroll
+        for (int i = 0; i < kMI; ++i)
+          fa[ks][i] = read_rm_frag_rows<kRMRow>(a_base_l + ((static_cast<uint32_t>(wm * kMI + i) * 32u) ^ x));
+      } else {
+        const uint32_t a_base_l = (lds_base + sa * kSlotBytes + fa0) ^ (ks << 6);
+#pragma unroll
+        for (int i = 0; i < kMI; ++i)
+          fa[ks][i] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)(a_base_l + i * 16 * kKCRow));
+      }
+#pragma unroll
+      for (int j = 0; j < kNI; ++j)
+        fb[ks][j] = read_rm_frag_rows<kHalfRow>(b_base_l + ks * 32 * kHalfRow + ((static_cast<uint32_t>(j) * 32u) ^ x));
+    }
+  };
+  auto compute = [&](auto zero_c) {
+    constexpr bool zero = decltype(zero_c)::value;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int i = 0; i < kMI; ++i)
+#pragma unroll
+        for (int j = 0; j < kNI; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[ks][j], fa[ks][i],
+                                                             (zero && ks == 0) ? f32x4{} : acc[i][j], 0, 0, 0);
+  };
+  // Epilogue: register r of lane l in block (i, j) holds output row
+  // wm * 64 + i * 16 + l % 16 and column grp * 128 + j * 16 + 4 (l / 16) + r of
+  // the tile; bf16 RNE, v_permlane16_swap pairs blocks j, j + 1 so each lane
+  // stores 8 consecutive columns (16 bytes) through a resource over the tile's
+  // valid rows; columns past K get an offset past it.
+  auto epilogue = [&](const Tile &t) {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int eq = ln >> 4;
+    const int64_t gbase = kWgrad ? static_cast<int64_t>(t.g) * N * K : 0;
+    const int kcols = static_cast<int>(k32);
+    const uint32_t ld = k32 * 2u;
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(static_cast<const uint16_t *>(p.out) + gbase + static_cast<int64_t>(t.i0) * K,
+                                                static_cast<uint32_t>(t.rows_valid) * ld);
+    const int wcol0 = static_cast<int>(t.nt) * kBN + grp * 128 + (eq & 1) * 16 + (eq >> 1) * 8;
+#pragma unroll
+    for (int i = 0; i < kMI; ++i) {
+      const uint32_t orow = static_cast<uint32_t>(wm * 64 + i * 16 + (ln & 15));
+#pragma unroll
+      for (int jp = 0; jp < kNI; jp += 2) {
+        uint32_t w[2][2];
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+          const bf16x2 lo = {(__bf16)acc[i][jp + d][0], (__bf16)acc[i][jp + d][1]};
+          const bf16x2 hi = {(__bf16)acc[i][jp + d][2], (__bf16)acc[i][jp + d][3]};
+          w[d][0] = __builtin_bit_cast(uint32_t, lo);
+          w[d][1] = __builtin_bit_cast(uint32_t, hi);
+        }
+        u32x4 o;
+#if defined(__HIP_DEVICE_COMPILE__)
+        const auto s0 = __builtin_amdgcn_permlane16_swap(w[0][0], w[1][0], false, false);
+        const auto s1 = __builtin_amdgcn_permlane16_swap(w[0][1], w[1][1], false, false);
+        o = u32x4{s0[0], s1[0], s0[1], s1[1]};
+#else
+        o = u32x4{0u, 0u, 0u, 0u};
+#endif
+        const int gcol = wcol0 + jp * 16;
+        const uint32_t off = gcol < kcols ? orow * ld + static_cast<uint32_t>(gcol) * 2u : kNoAccess;
+#if defined(__HIP_DEVICE_COMPILE__)
+        __builtin_amdgcn_raw_buffer_store_b128(o, ro, static_cast<int>(off), 0, 0);
+#else
+        (void)off;
+        (void)ro;
+        (void)o;
+#endif
+      }
+    }
+  };
+
+  // ---- prologue: A stages 0 and 1, group 0's B half of stages 0 and 1 (by
+  // group 1), group 1's B half of stage 0 (by group 0).
+  Tile cur{}, nxt{};
+  if (!find_tile(0, cur)) return;
+  setup_a(cur, true);
+  setup_b(cur, true);
+  {
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+      for (int j = 0; j < kDmaA; ++j) {
+        const uint32_t blk = grp * 16 + j * 4 + wm;
+        dma16b(ra, (lds_void *)(uintptr_t)(lds_base + kt * kSlotBytes + blk * 1024), a_off[j], kt * a_step);
+      }
+    }
+    const int nb = grp == 1 ? 2 : 1;
+    for (int kt = 0; kt < nb; ++kt) {
+      const uint32_t b_dst = lds_base + kBBase + kt * kSlotBytes + (1 - grp) * kHalfBytes;
+#pragma unroll
+      for (int j = 0; j < kDmaB; ++j) {
+        const uint32_t blk = j * 4 + wm;
+        dma16b(rb, (lds_void *)(uintptr_t)(b_dst + blk * 1024), b_base + j * 16 * static_cast<int>(k32) * 2,
+               kt * b_step);
+      }
+    }
+  }
+  bool more = find_tile(1, nxt);
+  wait_dma();
+  barrier();
+  if (grp == 1) barrier();  // group 1 runs one phase behind
+
+  int slot_a = 0, slot_b = 0;
+  bool have_prev = false;
+  Tile prev{};
+  for (uint32_t round = 0;; ++round) {
+    const int S = cur.ktiles;
+    for (int s = 0; s < S; ++s) {
+      // ---------------- load phase of stage s
+      const bool epi = s == 0 && have_prev;
+      if (epi) epilogue(prev);
+      __builtin_amdgcn_sched_barrier(0);
+      read_frags(slot_a, slot_b);
+      const int ta = s + 2, tb = s + 1 + grp;
+      if (ta == S) setup_a(nxt, more);
+      if (tb == S) setup_b(nxt, more);
+      int sa = slot_a + 2;
+      sa = sa >= kAS ? sa - kAS : sa;
+      const int sbs = (slot_b + 1 + grp) & 1;
+      issue(ta >= S ? ta - S : ta, sa, tb >= S ? tb - S : tb, sbs);
+      if (epi) {
+        wait_vm_n<kDmaA + kDmaB + kStores>();
+      } else {
+        wait_vm_n<kDmaA + kDmaB>();
+      }
+      wait_lds();
+      barrier();
+      // ---------------- compute phase of stage s
+      if (s == 0) {
+        compute(std::true_type{});
+      } else {
+        compute(std::false_type{});
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      barrier();
+      slot_a = slot_a + 1 == kAS ? 0 : slot_a + 1;
+      slot_b ^= 1;
+    }
+    prev = cur;
+    have_prev = true;
+    if (!more) break;
+    cur = nxt;
+    more = find_tile(round + 2, nxt);
+  }
+  epilogue(prev);
+  if (grp == 0) barrier();
+  wait_dma();  // no LDS DMA outlives the workgroup
+}
+
 template <bool kWgrad, int kOut = 0, bool kSplit = false, bool kOrder = false>
 void launch_pipe(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
   int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
   grid = std::max<int64_t>(8, (grid + 7) / 8 * 8);
   grouped_gemm_bwd_pipe_kernel<kWgrad, kOut, kSplit, kOrder><<<dim3(grid), dim3(256), 0, s>>>(p);
+}
+
+#ifndef MOE_GEMM_BWD_PINGPONG
+#define MOE_GEMM_BWD_PINGPONG 1
+#endif
+template <bool kWgrad, bool kOrder = false>
+void launch_pp(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
+  int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
+  grid = std::max<int64_t>(8, (grid + 7) / 8 * 8);
+  grouped_gemm_bwd_pp_kernel<kWgrad, kOrder><<<dim3(grid), dim3(512), 0, s>>>(p);
 }
 
 // order[rank] = group, rank = the number of groups with more rows (or as many
@@ -1210,6 +1605,8 @@ int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, con
   // of at least three (N % 64 != 0 or N < 192); the pipelined 256-row kernel otherwise.
   if (M_total <= 160 * G || N % kBK != 0 || N < 3 * kBK) {
     launch_dgrad128(p, (ceil_div(M_total, 128) + G) * p.ntiles, s);
+  } else if (MOE_GEMM_BWD_PINGPONG) {
+    launch_pp<false>(p, (ceil_div(M_total, 256) + G) * p.ntiles, s);
   } else {
     launch_pipe<false>(p, (ceil_div(M_total, 256) + G) * p.ntiles, s);
   }
@@ -1271,7 +1668,13 @@ int moe_grouped_gemm_wgrad(const moe_bf16_t *dy, const moe_bf16_t *x, int64_t M_
     int16_t *order = static_cast<int16_t *>(workspace);
     group_order_kernel<<<dim3(1), dim3(1024), 0, s>>>(group_offsets, static_cast<int>(G), M_total, order);
     p.order = order;
-    launch_pipe<true, 0, false, true>(p, tiles, s);
+    if (MOE_GEMM_BWD_PINGPONG) {
+      launch_pp<true, true>(p, tiles, s);
+    } else {
+      launch_pipe<true, 0, false, true>(p, tiles, s);
+    }
+  } else if (MOE_GEMM_BWD_PINGPONG) {
+    launch_pp<true>(p, tiles, s);
   } else {
     launch_pipe<true>(p, tiles, s);
   }

@@ -44,6 +44,7 @@ def _offsets(sizes, dev):
     ([700, 3, 1200], 2048, 520),           # long reduction, 256-row tiles
     ([400, 0, 333, 512], 192, 264),        # pipelined kernel at its shortest reduction (3 steps), column tail
     ([600, 1], 6144, 72),                  # pipelined kernel, one column tile narrower than the tile
+    ([300] * 20, 256, 200),                # 20 groups of 300 rows: many tile changes, K tail
 ])
 def test_dgrad_small(pkg, dev, sizes, N, K):
     g = torch.Generator().manual_seed(sum(sizes) + 7 * N + K)
@@ -147,6 +148,7 @@ def test_dgrad_split_reduction(pkg, dev):
     ([102] * 5, 520, 1024),                 # case05/09 group size, K tail in the reduction
     ([2048, 5], 128, 264),                  # long reduction
     ([1, 2, 0, 63, 64, 65, 127, 128, 129, 191, 192, 193] * 3, 136, 200),  # many small groups: 3-step minimum, zero steps
+    ([5000, 0, 3000], 264, 520),            # long reductions of different lengths, N and K tails
 ])
 def test_wgrad_small(pkg, dev, sizes, N, K):
     g = torch.Generator().manual_seed(3 * sum(sizes) + N + 5 * K)

@@ -1,9 +1,9 @@
 """CPU: the grouped GEMM kernels keep every value in registers (no scratch spills).
 
 The one-wavefront-per-SIMD GEMM kernels hold 128 or 256 fp32 accumulators in AGPRs and a K
-step of operand fragments in VGPRs; the ping-pong forward kernel (two wavefronts per SIMD)
-holds its 128 accumulators and fragments in the 256 registers a wavefront gets at that
-occupancy. A spill puts scratch loads (which wait on the vector-memory counter, and so on
+step of operand fragments in VGPRs; the ping-pong kernels (forward and backward, two
+wavefronts per SIMD) hold their 128 accumulators and fragments in the 256 registers a
+wavefront gets at that occupancy. A spill puts scratch loads (which wait on the vector-memory counter, and so on
 the LDS DMA in flight) inside the MFMA stream. The compiler's kernel-resource-usage remarks
 for the device code must report 0 scratch bytes per lane for every instantiation.
 """
@@ -33,8 +33,8 @@ def test_gemm_kernels_do_not_spill():
     assert len(rows) >= 15, rows
     spilled = [(name, v) for name, v in rows if v.get("scratch", 0) != 0]
     assert not spilled, spilled
-    pingpong = [(name, v) for name, v in rows if "grouped_gemm_pp_kernel" in name]
-    assert len(pingpong) == 4, pingpong
+    pingpong = [(name, v) for name, v in rows if "_pp_kernel" in name]
+    assert len(pingpong) == 7, pingpong  # forward: 4 epilogue/gather forms; backward: dgrad, wgrad, ordered wgrad
     assert all(v.get("occ") == 2 and v.get("vgpr", 0) + v.get("agpr", 0) <= 256 for _, v in pingpong), pingpong
     assert all(v.get("agpr") in (128, 256) for name, v in rows if "gemm" in name and "kernel" in name and "sum_planes" not in name
-               and "split" not in name and "grouped_gemm_pp_kernel" not in name)
+               and "split" not in name and "_pp_kernel" not in name)
