@@ -176,10 +176,10 @@ __global__ __launch_bounds__(PermShape<kExpertMajor>::kThreads) void permute_ker
   }
 }
 
-// Expert-major maps ([E, T], 0 < E <= kMaxStagedE, 16-byte rows): a workgroup of
-// 8 wavefronts takes kEmTok consecutive tokens. Their map entries are read once,
-// coalesced (8 lanes read one expert's entries of the 8 tokens: 64 contiguous
-// bytes of an int64 map), and staged transposed in LDS as int32 row ids (-1 for
+// Map tiles (expert-major maps, and token-major maps with 64 < E; E <= kMaxStagedE; 16-byte rows):
+// a workgroup of 8 wavefronts takes kTileTok consecutive tokens. Their map entries are read once,
+// coalesced (expert-major: 8 lanes read one expert's entries of the 8 tokens, 64 contiguous bytes
+// of an int64 map; token-major: a token's row), and staged in LDS as int32 row ids (-1 for
 // entries outside [0, num_out)); the padded LDS row (E rounded up to 64, + 1)
 // keeps the transposing writes off a single bank. Then one wavefront per token
 // builds the 64-bit ballots of its routed experts, writes the permuted probs,
@@ -187,33 +187,38 @@ __global__ __launch_bounds__(PermShape<kExpertMajor>::kThreads) void permute_ker
 // and stores it to each destination in ascending expert order.
 // 8 tokens, one wavefront each (case21 map, 1 GiB flush: 0.476-0.478 ms; 4 tokens 0.501, 16 tokens 0.486
 // (two per wavefront), 32 tokens 0.492; the per-token staged kernel below 0.500).
-constexpr int kEmTok = 8;
-constexpr int kEmThreads = kEmTok * kWave;
-__host__ __device__ inline int em_row_stride(int nchunks) { return nchunks * kWave + 1; }
-__host__ __device__ inline size_t em_lds_bytes(int nchunks) {
-  return static_cast<size_t>(kEmTok) * em_row_stride(nchunks) * 4 + static_cast<size_t>(kEmTok) * nchunks * 8 + 8;
+constexpr int kTileTok = 8;
+constexpr int kTileThreads = kTileTok * kWave;
+__host__ __device__ inline int tile_row_stride(int nchunks) { return nchunks * kWave + 1; }
+__host__ __device__ inline size_t tile_lds_bytes(int nchunks) {
+  return static_cast<size_t>(kTileTok) * tile_row_stride(nchunks) * 4 + static_cast<size_t>(kTileTok) * nchunks * 8 + 8;
 }
 
-template <bool kI64, bool kProbs>
-__global__ __launch_bounds__(kEmThreads) void permute_em_tile_kernel(PermuteArgs a) {
+template <bool kI64, bool kProbs, bool kExpertMajor>
+__global__ __launch_bounds__(kTileThreads) void permute_tile_kernel(PermuteArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int nch = static_cast<int>(ceil_div(a.E, kWave));
-  const int stride = em_row_stride(nch);
+  const int stride = tile_row_stride(nch);
   int32_t *s_dst = reinterpret_cast<int32_t *>(smem);
-  uint64_t *s_valid = reinterpret_cast<uint64_t *>(smem + ((static_cast<size_t>(kEmTok) * stride * 4 + 7) & ~size_t(7)));
+  uint64_t *s_valid = reinterpret_cast<uint64_t *>(smem + ((static_cast<size_t>(kTileTok) * stride * 4 + 7) & ~size_t(7)));
   const int tid = threadIdx.x, lane = lane_id(), wave = threadIdx.x / kWave;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kEmTok;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kTileTok;
   int routed = 0;
-  for (int i = tid; i < kEmTok * nch * kWave; i += kEmThreads) {
-    const int e = i / kEmTok, tk = i % kEmTok;
+  for (int i = tid; i < kTileTok * nch * kWave; i += kTileThreads) {
+    // Expert-major: consecutive threads take consecutive tokens of one expert;
+    // token-major: consecutive experts of one token (both coalesced).
+    const int e = kExpertMajor ? i / kTileTok : i % (nch * kWave);
+    const int tk = kExpertMajor ? i % kTileTok : i / (nch * kWave);
     const int64_t t = t0 + tk;
     int64_t v = -1;
-    if (e < a.E && t < a.T) v = load_idx<kI64>(a.map, static_cast<int64_t>(e) * a.T + t);
+    if (e < a.E && t < a.T) {
+      v = load_idx<kI64>(a.map, kExpertMajor ? static_cast<int64_t>(e) * a.T + t : t * a.E + e);
+    }
     routed += v >= 0;
     s_dst[tk * stride + e] = (v >= 0 && v < a.num_out) ? static_cast<int32_t>(v) : -1;
   }
   __syncthreads();
-  for (int pr = wave; pr < kEmTok * nch; pr += kEmThreads / kWave) {
+  for (int pr = wave; pr < kTileTok * nch; pr += kTileThreads / kWave) {
     const int tk = pr / nch, c = pr % nch;
     const int e = c * kWave + lane;
     const int32_t d = s_dst[tk * stride + e];
@@ -229,7 +234,7 @@ __global__ __launch_bounds__(kEmThreads) void permute_em_tile_kernel(PermuteArgs
   constexpr int kVecPerLane = 16 / kSplit;
   const int part = wave % kSplit;
   const int64_t nvec = a.H / 8;
-  for (int tk = wave / kSplit; tk < kEmTok; tk += kEmThreads / kWave / kSplit) {
+  for (int tk = wave / kSplit; tk < kTileTok; tk += kTileThreads / kWave / kSplit) {
     const int64_t t = t0 + tk;
     if (t >= a.T) break;
     const u32x4 *src = reinterpret_cast<const u32x4 *>(a.x + t * a.H);
@@ -257,14 +262,14 @@ __global__ __launch_bounds__(kEmThreads) void permute_em_tile_kernel(PermuteArgs
     }
   }
   if (a.block_counts != nullptr) {
-    __shared__ int wave_routed[kEmThreads / kWave];
+    __shared__ int wave_routed[kTileThreads / kWave];
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1) routed += __shfl_xor(routed, off);
     if (lane == 0) wave_routed[wave] = routed;
     __syncthreads();
     if (threadIdx.x == 0) {
       int sum = 0;
-      for (int w = 0; w < kEmThreads / kWave; ++w) sum += wave_routed[w];
+      for (int w = 0; w < kTileThreads / kWave; ++w) sum += wave_routed[w];
       a.block_counts[blockIdx.x] = sum;
     }
   }
@@ -460,9 +465,11 @@ int moe_permute(const moe_bf16_t *x, int64_t T, int64_t H, const void *row_id_ma
   }
   const bool em = map_layout == MOE_MAP_EXPERT_MAJOR;
   const bool vec = (H % 8 == 0) && is_aligned(x, 16) && is_aligned(out, 16);
-  // Expert-major maps with 16-byte rows: map tiles of kEmTok tokens (permute_em_tile_kernel).
-  const bool em_tile = em && vec && E > 0 && E <= kMaxStagedE;
-  const int64_t nblocks = ceil_div(T, em_tile ? kEmTok : em ? PermShape<true>::kTokensPerBlock
+  // Map tiles (permute_tile_kernel) for expert-major maps, and for token-major maps with more than 64
+  // experts (case17, E = 320, 1 GiB flush: 0.342 ms against 0.378 with 4 wavefronts per token; at c5, E = 64
+  // and 8 destinations per token, 4 wavefronts per token stay faster: 0.400 against 0.417 ms).
+  const bool map_tile = (em || E > kWave) && vec && E > 0 && E <= kMaxStagedE;
+  const int64_t nblocks = ceil_div(T, map_tile ? kTileTok : em ? PermShape<true>::kTokensPerBlock
                                                            : PermShape<false>::kTokensPerBlock);
   if (nblocks > 0x7fffffff) return fail(MOE_ERR_CAPACITY, "moe_permute: T=%lld too large", (long long)T);
   if (zero_tail && (workspace == nullptr || workspace_bytes < moe_permute_workspace_size(T))) {
@@ -481,14 +488,21 @@ int moe_permute(const moe_bf16_t *x, int64_t T, int64_t H, const void *row_id_ma
   a.pp = probs != nullptr ? permuted_probs : nullptr;
   a.num_out = num_out;
   a.block_counts = zero_tail ? static_cast<int32_t *>(workspace) : nullptr;
-  if (nblocks > 0 && em_tile) {
-    const size_t lds = em_lds_bytes(static_cast<int>(ceil_div(E, kWave)));
+  if (nblocks > 0 && map_tile) {
+    const size_t lds = tile_lds_bytes(static_cast<int>(ceil_div(E, kWave)));
     const bool i64 = idx_dtype == MOE_IDX_I64;
-    const dim3 grid(static_cast<uint32_t>(nblocks)), block(kEmThreads);
-    if (i64 && a.probs != nullptr) permute_em_tile_kernel<true, true><<<grid, block, lds, s>>>(a);
-    else if (i64) permute_em_tile_kernel<true, false><<<grid, block, lds, s>>>(a);
-    else if (a.probs != nullptr) permute_em_tile_kernel<false, true><<<grid, block, lds, s>>>(a);
-    else permute_em_tile_kernel<false, false><<<grid, block, lds, s>>>(a);
+    const dim3 grid(static_cast<uint32_t>(nblocks)), block(kTileThreads);
+    if (em) {
+      if (i64 && a.probs != nullptr) permute_tile_kernel<true, true, true><<<grid, block, lds, s>>>(a);
+      else if (i64) permute_tile_kernel<true, false, true><<<grid, block, lds, s>>>(a);
+      else if (a.probs != nullptr) permute_tile_kernel<false, true, true><<<grid, block, lds, s>>>(a);
+      else permute_tile_kernel<false, false, true><<<grid, block, lds, s>>>(a);
+    } else {
+      if (i64 && a.probs != nullptr) permute_tile_kernel<true, true, false><<<grid, block, lds, s>>>(a);
+      else if (i64) permute_tile_kernel<true, false, false><<<grid, block, lds, s>>>(a);
+      else if (a.probs != nullptr) permute_tile_kernel<false, true, false><<<grid, block, lds, s>>>(a);
+      else permute_tile_kernel<false, false, false><<<grid, block, lds, s>>>(a);
+    }
     int st = check_launch("moe_permute");
     if (st != MOE_OK) return st;
   } else if (nblocks > 0) {
