@@ -35,7 +35,7 @@ MOE_MAP_EXPERT_MAJOR = 1
 MOE_EPILOGUE_NONE = 0
 MOE_EPILOGUE_SWIGLU = 1
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -58,6 +58,7 @@ SIGNATURES = {
     "moe_unpermute": (_int, [_p, _i64, _i64, _p, _int, _int, _i64, _i64, _p, _p, _p, _p]),
     "moe_permute_bwd": (_int, [_p, _i64, _i64, _p, _p, _int, _int, _i64, _i64, _p, _p, _p, _p]),
     "moe_index_select": (_int, [_p, _i64, _i64, _p, _int, _i64, _p, _p]),
+    "moe_grouped_gemm_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
     "moe_grouped_gemm": (_int, [_p, _i64, _i64, _p, _i64, _i64, _p, _int, _p, _p, _sz, _p]),
     "moe_permute_index": (_int, [_p, _int, _int, _i64, _i64, _p, _i64, _int, _p]),
     "moe_grouped_gemm_gather": (_int, [_p, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _int, _p, _p, _sz, _p]),

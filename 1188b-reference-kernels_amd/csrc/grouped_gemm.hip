@@ -86,7 +86,63 @@ struct GemmArgs {
   int64_t ncols;   // output columns: N (NONE) or N / 2 (SWIGLU)
   int64_t ntiles;  // column tiles per expert
   int vec_out;     // output rows are 16-byte aligned (ncols % 8 == 0, aligned base)
+  int *tails;      // ping-pong kernel: tail list (kTail* layout) or nullptr (tails in 256-row tiles)
 };
+
+// Tails of the ping-pong kernel (workspace layout, ints): a group whose last
+// 256-row tile would have 1 to 128 rows leaves that tile to the 128-row form
+// of the kernel. tails_init_kernel lists those groups in order; after their
+// 256-row tiles the persistent workgroups take (group, column tile) units
+// u = 0, 1, ... of the list from the counter, unit u = list[u / ntiles],
+// column tile u % ntiles.
+constexpr int kTailCtr = 0;     // units handed out
+constexpr int kTailCount = 32;  // groups in the list (own 128-byte line)
+constexpr int kTailList = 64;   // the groups, ascending
+#ifndef MOE_GEMM_TAILS_MIN_K
+#define MOE_GEMM_TAILS_MIN_K 4096
+#endif
+constexpr int64_t kTailsMinK = MOE_GEMM_TAILS_MIN_K;  // shortest reduction that uses the 128-row tail tiles
+inline size_t tails_bytes(int64_t G) { return sizeof(int) * static_cast<size_t>(kTailList + G); }
+
+__device__ __forceinline__ bool has_tail(int64_t m) {
+  const int64_t r = m % 256;
+  return r >= 1 && r <= 128;
+}
+
+// One workgroup of 256 threads: each thread counts the tails of its chunk of
+// groups, an exclusive scan over the threads gives the chunk's first list
+// position, then each thread lists its chunk's tail groups.
+__global__ __launch_bounds__(256) void tails_init_kernel(GemmArgs p) {
+  __shared__ int part[256];
+  const int t = threadIdx.x;
+  const int64_t per = (p.G + 255) / 256;
+  const int64_t g0 = min(p.G, t * per), g1 = min(p.G, g0 + per);
+  auto tail_at = [&](int64_t g) {
+    const int64_t lo = min(max(static_cast<int64_t>(p.offsets[g]), int64_t(0)), p.M);
+    const int64_t hi = min(max(static_cast<int64_t>(p.offsets[g + 1]), lo), p.M);
+    return has_tail(hi - lo);
+  };
+  int n = 0;
+  for (int64_t g = g0; g < g1; ++g) n += tail_at(g) ? 1 : 0;
+  part[t] = n;
+  __syncthreads();
+  if (t == 0) {
+    int acc = 0;
+    for (int i = 0; i < 256; ++i) {
+      const int v = part[i];
+      part[i] = acc;
+      acc += v;
+    }
+    p.tails[kTailCount] = acc;
+    p.tails[kTailCtr] = 0;
+  }
+  __syncthreads();
+  int pos = part[t];
+  for (int64_t g = g0; g < g1; ++g) {
+    if (tail_at(g)) p.tails[kTailList + pos++] = static_cast<int>(g);
+  }
+}
+constexpr int kPpLdsBytes = 5 * 256 * 128;  // ping-pong kernel LDS: 160 KiB
 
 __device__ __forceinline__ int swz(int row) { return (row >> 1) & (kChunks - 1); }
 
@@ -852,21 +908,37 @@ __global__ __launch_bounds__(256) void grouped_gemm_pipe_kernel(GemmArgs p) {
 // The epilogue of a tile (same register layout as the pipelined kernel) runs
 // in the wavefront's next load phase; the stores are issued before that
 // phase's DMAs and are allowed to stay in flight across its barrier.
-template <bool kSwiglu, bool kGather>
-__global__ __launch_bounds__(512) void grouped_gemm_pp_kernel(GemmArgs p) {
+struct PpTile {  // rows and groups in 32 bits: the host runs the kernel for M < 2^31
+  int g, row0;
+  uint32_t nt;
+  int rows_valid;
+};
+
+// kTM = 256: the persistent workgroup b of P (the grid) takes its tiles in
+// the static order; kTM = 128: the one tile *one.
+template <bool kSwiglu, bool kGather, int kTM, bool kTails>
+__device__ __forceinline__ void pp_body(const GemmArgs &p, char *smem, const PpTile *one) {
+  static_assert(kTM == 256 || kTM == 128, "tile rows");
   constexpr int kAS = 3, kBS = 2;                   // ring slots
-  constexpr int kSlotBytes = 256 * kRowBytes;       // 32 KiB: 256 rows x 64 K
-  constexpr int kBBase = kAS * kSlotBytes;
+  constexpr int kASlotBytes = kTM * kRowBytes;      // A stage: kTM rows x 64 K
+  constexpr int kSlotBytes = 256 * kRowBytes;       // B stage: 32 KiB, 256 rows x 64 K
+  constexpr int kBBase = kAS * kASlotBytes;
   constexpr int kEpiCols = kSwiglu ? kBN / 2 : kBN;  // output columns of a tile
-  constexpr int kMI = 4, kNI = 8;                    // 16 x 16 blocks of a wavefront
-  constexpr int kStores = kSwiglu ? 8 : 16;          // 16-byte stores per lane per tile
-  constexpr int kDmaA = 4, kDmaB = 4;                // DMA instructions per wavefront per load phase
+  constexpr int kMI = kTM / 64, kNI = 8;             // 16 x 16 blocks of a wavefront
+  constexpr int kWR = kTM / 4;                       // tile rows of a wavefront
+  constexpr int kStores = kMI * (kSwiglu ? 2 : 4);   // 16-byte stores per lane per tile
+  constexpr int kDmaA = kTM / 64, kDmaB = 4;         // DMA instructions per wavefront per load phase
+  constexpr int kABlk = kTM / 16;                    // 8-row A blocks DMA'd by one group per stage
   static_assert(kDmaA + kDmaB + kStores <= 63, "vmcnt range");
-  __shared__ __attribute__((aligned(1024))) char smem[kAS * kSlotBytes + kBS * kSlotBytes];
+  static_assert(kAS * kASlotBytes + kBS * kSlotBytes <= kPpLdsBytes, "LDS");
   lds_char *const sbase = (lds_char *)smem;
   const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sbase));
 
-  const int tid = threadIdx.x;
+  // The thread index through an opaque copy: the lane-derived values of the
+  // 256-row and the 128-row form are computed separately, not kept live from
+  // one form to the other.
+  int tid = threadIdx.x;
+  if constexpr (kTails) asm volatile("" : "+v"(tid));
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
@@ -902,30 +974,38 @@ __global__ __launch_bounds__(512) void grouped_gemm_pp_kernel(GemmArgs p) {
   const int64_t K = p.K;
   const int S = static_cast<int>(K / kBK);  // K steps per tile (>= 3, K % 64 == 0: host)
 
-  // ---- tile walker (group offsets read from memory: the ring fills the LDS)
-  auto group_rows = [&](int64_t g, int64_t &lo, int64_t &hi) {
-    lo = min(max(static_cast<int64_t>(p.offsets[g]), int64_t(0)), p.M);
-    hi = min(max(static_cast<int64_t>(p.offsets[g + 1]), lo), p.M);
+  // ---- tile walker (group offsets read from memory: the ring fills the LDS;
+  // rows and groups in 32 bits)
+  const int M32 = static_cast<int>(p.M);
+  const int G32 = static_cast<int>(p.G);
+  auto group_rows = [&](int g, int &lo, int &hi) {
+    lo = min(max(p.offsets[g], 0), M32);
+    hi = min(max(p.offsets[g + 1], lo), M32);
   };
-  int64_t g_cur = 0, tiles_before = 0, m_lo, m_hi;
+  // 256-row tiles of a group (kTails: all but a last tile of at most 128
+  // rows, which the 128-row form takes).
+  auto main_tiles = [&](int m) -> int { return kTails ? (m + 127) / 256 : (m + 255) / 256; };
+  int g_cur = 0, m_lo, m_hi;
+  int64_t tiles_before = 0;
   group_rows(0, m_lo, m_hi);
-  int64_t mt_g = ceil_div(m_hi - m_lo, kBM);
-  struct Tile {
-    int64_t g, row0;
-    uint32_t nt;
-    int rows_valid;
-  };
+  int mt_g = main_tiles(m_hi - m_lo);
+  using Tile = PpTile;
   auto find_tile = [&](int64_t round, Tile &t) -> bool {
+    if constexpr (kTM == 128) {
+      if (round > 0) return false;
+      t = *one;
+      return true;
+    }
     const int64_t L = round * P + (b % 8) * (P / 8) + b / 8;
-    while (g_cur < p.G && L >= tiles_before + mt_g * p.ntiles) {
-      tiles_before += mt_g * p.ntiles;
+    while (g_cur < G32 && L >= tiles_before + static_cast<int64_t>(mt_g) * p.ntiles) {
+      tiles_before += static_cast<int64_t>(mt_g) * p.ntiles;
       ++g_cur;
-      if (g_cur < p.G) {
+      if (g_cur < G32) {
         group_rows(g_cur, m_lo, m_hi);
-        mt_g = ceil_div(m_hi - m_lo, kBM);
+        mt_g = main_tiles(m_hi - m_lo);
       }
     }
-    if (g_cur >= p.G) return false;
+    if (g_cur >= G32) return false;
     const uint32_t q = static_cast<uint32_t>(L - tiles_before);
     const uint32_t ntl = static_cast<uint32_t>(p.ntiles);
     const uint32_t per_grp = kGroupM * ntl;
@@ -941,9 +1021,9 @@ __global__ __launch_bounds__(512) void grouped_gemm_pp_kernel(GemmArgs p) {
       mt = full * kGroupM + (r - nt * gm);
     }
     t.g = g_cur;
-    t.row0 = m_lo + static_cast<int64_t>(mt) * kBM;
+    t.row0 = m_lo + static_cast<int>(mt) * kTM;
     t.nt = nt;
-    t.rows_valid = static_cast<int>(min(m_hi - t.row0, int64_t(kBM)));
+    t.rows_valid = min(m_hi - t.row0, kTM);
     return true;
   };
 
@@ -953,7 +1033,7 @@ __global__ __launch_bounds__(512) void grouped_gemm_pp_kernel(GemmArgs p) {
   const uint32_t row_bytes = static_cast<uint32_t>(K) * 2u;
   const int ncols32 = static_cast<int>(p.ncols);
   const int src_rows32 = static_cast<int>(min(p.a_src_rows, int64_t(0x7fffffff)));
-  auto a_row = [&](int j, int ln) { return ((grp * 16 + j * 4 + wm) * kRowsPerKiB) + ln / kChunks; };
+  auto a_row = [&](int j, int ln) { return ((grp * kABlk + j * 4 + wm) * kRowsPerKiB) + ln / kChunks; };
   auto b_row = [&](int j, int ln) { return (((1 - grp) * 16 + j * 4 + wm) * kRowsPerKiB) + ln / kChunks; };
   int32_t src_rows[kDmaA];
   auto load_rows = [&](const Tile &t, bool valid) {
@@ -1038,11 +1118,11 @@ __global__ __launch_bounds__(512) void grouped_gemm_pp_kernel(GemmArgs p) {
   // DMA of this wavefront's share of A stage kt into A slot sa and of its B
   // rows of stage kt_b into B slot sb.
   auto issue = [&](int kt_a, int sa, int kt_b, int sbs) {
-    const uint32_t a_dst = lds_base + sa * kSlotBytes;
+    const uint32_t a_dst = lds_base + sa * kASlotBytes;
     const uint32_t b_dst = lds_base + kBBase + sbs * kSlotBytes;
 #pragma unroll
     for (int j = 0; j < kDmaA; ++j) {
-      const uint32_t blk = grp * 16 + j * 4 + wm;
+      const uint32_t blk = grp * kABlk + j * 4 + wm;
       dma16b(ra, (lds_void *)(uintptr_t)(a_dst + blk * 1024), a_off[j], kt_a * kBK * 2);
     }
 #pragma unroll
@@ -1054,7 +1134,7 @@ __global__ __launch_bounds__(512) void grouped_gemm_pp_kernel(GemmArgs p) {
 
   // ---- fragments (v_mfma_f32_16x16x32_bf16 layout as in the pipelined kernel)
   const int fq = lane >> 4;
-  const int ra0 = wm * 64 + (lane & 15);
+  const int ra0 = wm * kWR + (lane & 15);
   const int rb0 = grp * 128 + (lane & 15);
   const uint32_t fa0 = ra0 * kRowBytes + ((fq ^ swz(ra0)) << 4);
   const uint32_t fb0 = rb0 * kRowBytes + ((fq ^ swz(rb0)) << 4);
@@ -1062,7 +1142,7 @@ __global__ __launch_bounds__(512) void grouped_gemm_pp_kernel(GemmArgs p) {
   f32x4 acc[kMI][kNI];
   bf16x8 fa[2][kMI], fb[2][kNI];
   auto read_frags = [&](int sa, int sbs) {
-    const uint32_t a_base = lds_base + sa * kSlotBytes + fa0;
+    const uint32_t a_base = lds_base + sa * kASlotBytes + fa0;
     const uint32_t b_base = lds_base + kBBase + sbs * kSlotBytes + fb0;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -1096,7 +1176,7 @@ __global__ __launch_bounds__(512) void grouped_gemm_pp_kernel(GemmArgs p) {
     constexpr int kOut16 = kSwiglu ? kNI / 2 : kNI;
 #pragma unroll
     for (int i = 0; i < kMI; ++i) {
-      const uint32_t orow = static_cast<uint32_t>(wm * 64 + i * 16 + (ln & 15));
+      const uint32_t orow = static_cast<uint32_t>(wm * kWR + i * 16 + (ln & 15));
 #pragma unroll
       for (int jp = 0; jp < kOut16; jp += 2) {
         uint32_t w[2][2];
@@ -1151,8 +1231,8 @@ __global__ __launch_bounds__(512) void grouped_gemm_pp_kernel(GemmArgs p) {
     for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
       for (int j = 0; j < kDmaA; ++j) {
-        const uint32_t blk = grp * 16 + j * 4 + wm;
-        dma16b(ra, (lds_void *)(uintptr_t)(lds_base + kt * kSlotBytes + blk * 1024), a_off[j], kt * kBK * 2);
+        const uint32_t blk = grp * kABlk + j * 4 + wm;
+        dma16b(ra, (lds_void *)(uintptr_t)(lds_base + kt * kASlotBytes + blk * 1024), a_off[j], kt * kBK * 2);
       }
     }
     const int nb = grp == 1 ? 2 : 1;
@@ -1176,6 +1256,7 @@ __global__ __launch_bounds__(512) void grouped_gemm_pp_kernel(GemmArgs p) {
     for (int s = 0; s < S; ++s) {
       // ---------------- load phase of stage s
       if (kGather && s == S - 3) load_rows(nxt, more);  // before this phase's other memory operations
+
       const bool epi = s == 0 && have_prev;
       if (epi) epilogue(prev);
       __builtin_amdgcn_sched_barrier(0);
@@ -1219,6 +1300,39 @@ __global__ __launch_bounds__(512) void grouped_gemm_pp_kernel(GemmArgs p) {
   if (grp == 0) barrier();
   wait_dma();  // no LDS DMA outlives the workgroup
 }
+
+// Ping-pong kernel: one persistent workgroup per CU takes its 256-row tiles
+// in the static order; with a tail list it then takes tail units from the
+// list's counter (wave 0 adds 1, the number reaches the other wavefronts
+// through the idle LDS ring) and computes each with the 128-row form of the
+// same pipeline, until the units run out. Workgroups whose static tiles end
+// early take more units, so the units also even out the last round.
+template <bool kSwiglu, bool kGather, bool kTails>
+__global__ __launch_bounds__(512) void grouped_gemm_pp_kernel(GemmArgs p) {
+  __shared__ __attribute__((aligned(1024))) char smem[kPpLdsBytes];
+  pp_body<kSwiglu, kGather, 256, kTails>(p, smem, nullptr);
+  if constexpr (!kTails) return;
+  volatile int *bcast = reinterpret_cast<volatile int *>(smem);
+  const int ntl = static_cast<int>(p.ntiles);
+  for (;;) {
+    __syncthreads();  // the ring is idle: every wavefront has left its last tile
+    if (threadIdx.x == 0) {
+      bcast[0] = __hip_atomic_fetch_add(p.tails + kTailCtr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    const int u = __builtin_amdgcn_readfirstlane(bcast[0]);
+    __syncthreads();  // every wavefront has read it before the ring is used again
+    if (u >= p.tails[kTailCount] * ntl) break;
+    const int g = p.tails[kTailList + u / ntl];
+    const int M32 = static_cast<int>(p.M);
+    const int lo = min(max(p.offsets[g], 0), M32);
+    const int hi = min(max(p.offsets[g + 1], lo), M32);
+    const int r = (hi - lo) % 256;
+    const PpTile t{g, hi - r, static_cast<uint32_t>(u % ntl), r};
+    pp_body<kSwiglu, kGather, 128, kTails>(p, smem, &t);
+  }
+}
+
 }  // namespace
 }  // namespace moe
 
@@ -1226,7 +1340,8 @@ namespace {
 
 int launch_grouped_gemm(const char *fn, const moe_bf16_t *a, int64_t a_src_rows, const int32_t *a_rows,
                         int64_t M_total, int64_t K, const moe_bf16_t *w, int64_t G, int64_t N,
-                        const int32_t *group_offsets, int epilogue, moe_bf16_t *out, void *stream) {
+                        const int32_t *group_offsets, int epilogue, moe_bf16_t *out, void *workspace,
+                        size_t workspace_bytes, void *stream) {
   using namespace moe;
   const bool gather = a_rows != nullptr;
   if (M_total < 0 || K < 0 || N < 0 || G < 0 || a_src_rows < 0) {
@@ -1276,15 +1391,33 @@ int launch_grouped_gemm(const char *fn, const moe_bf16_t *a, int64_t a_src_rows,
   // The pipelined kernel needs three K steps per tile, 16-byte output rows, a
   // 256-row output panel below 2 GiB and (gather) 32-bit offsets into a_rows.
   const bool pipe = K > 2 * kBK && p.vec_out && ncols < (int64_t(1) << 22) && (!gather || M_total < (int64_t(1) << 29));
-  // The ping-pong kernel: the same conditions and whole K steps.
-  const bool pingpong = MOE_GEMM_PINGPONG && pipe && K % kBK == 0;
-  if (pingpong) {
+  // The ping-pong kernel: the same conditions, whole K steps and row numbers in 31 bits.
+  const bool pingpong = MOE_GEMM_PINGPONG && pipe && K % kBK == 0 && M_total < (int64_t(1) << 31);
+  // With a workspace and a long reduction, group tails of at most 128 rows
+  // are listed first and computed as 128-row tiles after the 256-row ones
+  // (with short reductions the 128-row tiles' start and drain measured slower
+  // than the padding rows they save).
+  p.tails = nullptr;
+  if (pingpong && K >= kTailsMinK && workspace != nullptr && workspace_bytes >= tails_bytes(G) &&
+      is_aligned(workspace, 256)) {
+    p.tails = static_cast<int *>(workspace);
+    tails_init_kernel<<<dim3(1), dim3(256), 0, s>>>(p);
+  }
+  if (pingpong && p.tails != nullptr) {
     if (swiglu) {
-      if (gather) grouped_gemm_pp_kernel<true, true><<<dim3(grid), dim3(512), 0, s>>>(p);
-      else grouped_gemm_pp_kernel<true, false><<<dim3(grid), dim3(512), 0, s>>>(p);
+      if (gather) grouped_gemm_pp_kernel<true, true, true><<<dim3(grid), dim3(512), 0, s>>>(p);
+      else grouped_gemm_pp_kernel<true, false, true><<<dim3(grid), dim3(512), 0, s>>>(p);
     } else {
-      if (gather) grouped_gemm_pp_kernel<false, true><<<dim3(grid), dim3(512), 0, s>>>(p);
-      else grouped_gemm_pp_kernel<false, false><<<dim3(grid), dim3(512), 0, s>>>(p);
+      if (gather) grouped_gemm_pp_kernel<false, true, true><<<dim3(grid), dim3(512), 0, s>>>(p);
+      else grouped_gemm_pp_kernel<false, false, true><<<dim3(grid), dim3(512), 0, s>>>(p);
+    }
+  } else if (pingpong) {
+    if (swiglu) {
+      if (gather) grouped_gemm_pp_kernel<true, true, false><<<dim3(grid), dim3(512), 0, s>>>(p);
+      else grouped_gemm_pp_kernel<true, false, false><<<dim3(grid), dim3(512), 0, s>>>(p);
+    } else {
+      if (gather) grouped_gemm_pp_kernel<false, true, false><<<dim3(grid), dim3(512), 0, s>>>(p);
+      else grouped_gemm_pp_kernel<false, false, false><<<dim3(grid), dim3(512), 0, s>>>(p);
     }
   } else if (pipe) {
     if (swiglu) {
@@ -1308,25 +1441,28 @@ int launch_grouped_gemm(const char *fn, const moe_bf16_t *a, int64_t a_src_rows,
 
 extern "C" {
 
+size_t moe_grouped_gemm_workspace_size(int64_t M_total, int64_t K, int64_t N, int64_t G) {
+  (void)M_total;
+  (void)N;
+  if (G < 1 || G > 4096 || K % moe::gemm::kBK != 0 || K < moe::kTailsMinK) return 0;
+  return (moe::tails_bytes(G) + 255) / 256 * 256;
+}
+
 int moe_grouped_gemm(const moe_bf16_t *a, int64_t M_total, int64_t K, const moe_bf16_t *w, int64_t G,
                      int64_t N, const int32_t *group_offsets, int epilogue, moe_bf16_t *out,
                      void *workspace, size_t workspace_bytes, void *stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   return launch_grouped_gemm("moe_grouped_gemm", a, 0, nullptr, M_total, K, w, G, N, group_offsets, epilogue, out,
-                             stream);
+                             workspace, workspace_bytes, stream);
 }
 
 int moe_grouped_gemm_gather(const moe_bf16_t *x, int64_t x_rows, const int32_t *a_rows, int64_t M_total,
                             int64_t K, const moe_bf16_t *w, int64_t G, int64_t N, const int32_t *group_offsets,
                             int epilogue, moe_bf16_t *out, void *workspace, size_t workspace_bytes, void *stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   if (a_rows == nullptr && M_total > 0) {
     return moe::fail(MOE_ERR_INVALID_ARG, "moe_grouped_gemm_gather: null a_rows");
   }
   return launch_grouped_gemm("moe_grouped_gemm_gather", x, x_rows, a_rows, M_total, K, w, G, N, group_offsets,
-                             epilogue, out, stream);
+                             epilogue, out, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

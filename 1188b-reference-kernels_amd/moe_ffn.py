@@ -22,7 +22,7 @@ Data layout in HBM (T tokens, H hidden, F ffn, E experts, k top-k, R = T*k):
   out      bf16 [T, H]        sum_e probs[t, e] * z[row_map[t, e]]  (fp32, ascending e)
   W1       bf16 [E, 2F, H]    gate rows [0, F), up rows [F, 2F)  (out x in)
   W2       bf16 [E, H, F]
-The intermediates (src, h, z, the row-id-map workspace) are allocated once per
+The intermediates (src, h, z, the row-id-map and GEMM workspaces) are allocated once per
 token count and reused by later calls; the output is a new tensor on every call
 (or the caller's `out=`), so a result stays valid across later forward() calls.
 No host synchronisation happens inside forward() (R = T * k is known on the host).
@@ -61,6 +61,10 @@ class MoEFFN:
                 "z": torch.empty(R, self.H, **bf),
                 "ws": torch.empty(ops._lib.lib().moe_row_id_map_workspace_size(T, self.E), dtype=torch.uint8,
                                   device=device),
+                # the grouped GEMMs' tail list (fc1 and fc2 run one after the other)
+                "gemm_ws": torch.empty(max(ops._lib.lib().moe_grouped_gemm_workspace_size(R, self.H, 2 * self.F, self.E),
+                                           ops._lib.lib().moe_grouped_gemm_workspace_size(R, self.F, self.H, self.E), 1),
+                                       dtype=torch.uint8, device=device),
             }
         return self._bufs
 
@@ -84,11 +88,11 @@ class MoEFFN:
         mask, probs, row_map, offsets = self.route(logits)
         if self.fused_permute:
             # src holds the source token of every permuted row (R = T * k rows, all named by the map)
-            ops.grouped_gemm_gather(x, b["src"], self.w1, offsets, swiglu=True, out=b["h"])
+            ops.grouped_gemm_gather(x, b["src"], self.w1, offsets, swiglu=True, out=b["h"], workspace=b["gemm_ws"])
         else:
             ops.permute(x, row_map, num_out=T * self.k, layout=ops.TOKEN_MAJOR, zero_tail=False, out=b["xp"])
-            ops.grouped_gemm(b["xp"], self.w1, offsets, swiglu=True, out=b["h"])
-        ops.grouped_gemm(b["h"], self.w2, offsets, out=b["z"])
+            ops.grouped_gemm(b["xp"], self.w1, offsets, swiglu=True, out=b["h"], workspace=b["gemm_ws"])
+        ops.grouped_gemm(b["h"], self.w2, offsets, out=b["z"], workspace=b["gemm_ws"])
         ops.unpermute(b["z"], row_map, probs, layout=ops.TOKEN_MAJOR, out=out)
         self.last = {"mask": mask, "probs": probs, "row_map": row_map, "offsets": offsets}
         return out

@@ -392,12 +392,25 @@ def group_offsets_from_splits(m_splits: Sequence[int], device) -> torch.Tensor:
     return torch.tensor(offs, dtype=torch.int32).to(device, non_blocking=True)
 
 
+def _gemm_workspace(M: int, K: int, N: int, G: int, workspace: Optional[torch.Tensor], device):
+    """The grouped GEMM's workspace (the list of groups whose last row tile has at most 128 rows):
+    allocated when None; an empty tensor runs without one (every row tile 256 rows)."""
+    nbytes = _lib.lib().moe_grouped_gemm_workspace_size(M, K, N, G)
+    if nbytes == 0 or (workspace is not None and workspace.numel() == 0):
+        return None, 0
+    if workspace is None or workspace.numel() * workspace.element_size() < nbytes:
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    return workspace, workspace.numel() * workspace.element_size()
+
+
 def grouped_gemm(a: torch.Tensor, w: torch.Tensor, group_offsets: torch.Tensor, *, swiglu: bool = False,
-                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """out[rows of g] = a[rows of g] @ w[g]^T (bf16 in, fp32 accumulate, bf16 out).
 
     a bf16 [M, K]; w bf16 [G, N, K]; group_offsets int32 [G+1] on the device.
     With swiglu, out[:, j] = silu(y[:, j]) * y[:, N/2 + j] and out is [M, N/2].
+    workspace: uint8 device tensor (moe_grouped_gemm_workspace_size bytes; allocated when None,
+    an empty tensor: none).
     """
     _on_gpu("a", a)
     _on_gpu("w", w)
@@ -414,8 +427,9 @@ def grouped_gemm(a: torch.Tensor, w: torch.Tensor, group_offsets: torch.Tensor, 
     ac, wc, oc = a.contiguous(), w.contiguous(), group_offsets.contiguous()
     ncols = N // 2 if swiglu else N
     out = _out(out, (M, ncols), torch.bfloat16, a.device)
+    ws, ws_bytes = _gemm_workspace(M, K, N, G, workspace, a.device)
     call("moe_grouped_gemm", ptr(ac), M, K, ptr(wc), G, N, ptr(oc),
-         MOE_EPILOGUE_SWIGLU if swiglu else MOE_EPILOGUE_NONE, ptr(out), None, 0, stream_handle())
+         MOE_EPILOGUE_SWIGLU if swiglu else MOE_EPILOGUE_NONE, ptr(out), ptr(ws), ws_bytes, stream_handle())
     return out
 
 
@@ -441,7 +455,8 @@ def permute_index(row_id_map: torch.Tensor, num_out: int, *, layout: str = TOKEN
 
 
 def grouped_gemm_gather(x: torch.Tensor, a_rows: torch.Tensor, w: torch.Tensor, group_offsets: torch.Tensor, *,
-                        swiglu: bool = False, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                        swiglu: bool = False, out: Optional[torch.Tensor] = None,
+                        workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """grouped_gemm(x[a_rows], w, group_offsets) without materialising x[a_rows].
 
     x bf16 [X, K]; a_rows int32 [M] (an index outside [0, X) reads a zero row).
@@ -464,8 +479,9 @@ def grouped_gemm_gather(x: torch.Tensor, a_rows: torch.Tensor, w: torch.Tensor, 
     xc, rc, wc, oc = x.contiguous(), a_rows.contiguous(), w.contiguous(), group_offsets.contiguous()
     ncols = N // 2 if swiglu else N
     out = _out(out, (M, ncols), torch.bfloat16, x.device)
+    ws, ws_bytes = _gemm_workspace(M, K, N, G, workspace, x.device)
     call("moe_grouped_gemm_gather", ptr(xc), x.shape[0], ptr(rc), M, K, ptr(wc), G, N, ptr(oc),
-         MOE_EPILOGUE_SWIGLU if swiglu else MOE_EPILOGUE_NONE, ptr(out), None, 0, stream_handle())
+         MOE_EPILOGUE_SWIGLU if swiglu else MOE_EPILOGUE_NONE, ptr(out), ptr(ws), ws_bytes, stream_handle())
     return out
 
 

@@ -633,9 +633,9 @@ def main():
                               workspace=b["ws"])
         row_map, offs = maps["token_major"], maps["expert_offsets"]
         rec(2)
-        ops.grouped_gemm_gather(x, b["src"], w1, offs, swiglu=True, out=b["h"])
+        ops.grouped_gemm_gather(x, b["src"], w1, offs, swiglu=True, out=b["h"], workspace=b["gemm_ws"])
         rec(3)
-        ops.grouped_gemm(b["h"], w2, offs, out=b["z"])
+        ops.grouped_gemm(b["h"], w2, offs, out=b["z"], workspace=b["gemm_ws"])
         rec(4)
         ops.unpermute(b["z"], row_map, probs, layout=ops.TOKEN_MAJOR, out=out_buf)
         rec(5)

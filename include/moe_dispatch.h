@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define MOE_DISPATCH_ABI_VERSION 11
+#define MOE_DISPATCH_ABI_VERSION 12
 
 typedef uint16_t moe_bf16_t;
 
@@ -250,7 +250,16 @@ int moe_index_select(const moe_bf16_t *src, int64_t src_rows, int64_t row_elems,
  *       gate = columns [0, N/2), up = [N/2, N); silu(g) = g / (1 + exp(-g)),
  *       computed in fp32 on the fp32 accumulators, then one bf16 rounding).
  * Limits: K % 8 == 0, N % 2 == 0 (SWIGLU), 1 <= G <= 4096, K < 2^22, N * K < 2^30.
- * Workspace: none (pass NULL, 0). */
+ * Workspace: optional. With at least moe_grouped_gemm_workspace_size bytes
+ *   (256-byte aligned), a group whose last 256-row tile would hold 1 to 128
+ *   rows has that tile computed as a 128-row tile: a small kernel first lists
+ *   those groups, and the GEMM's workgroups take the 128-row tiles from the
+ *   list after their 256-row tiles (so the tiles also even out the last
+ *   round). Every output element is summed in the same order either way: the
+ *   result is the same bit for bit. NULL, 0 or a smaller size: every row tile
+ *   has 256 rows. The size is 0 where the 128-row form does not apply
+ *   (K % 64 != 0 or K <= 128). Calls that share a workspace must not overlap. */
+size_t moe_grouped_gemm_workspace_size(int64_t M_total, int64_t K, int64_t N, int64_t G);
 int moe_grouped_gemm(const moe_bf16_t *a, int64_t M_total, int64_t K, const moe_bf16_t *w,
                      int64_t G, int64_t N, const int32_t *group_offsets, int epilogue,
                      moe_bf16_t *out, void *workspace, size_t workspace_bytes, void *stream);

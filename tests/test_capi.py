@@ -17,7 +17,7 @@ L = pkg._lib
 def test_library_loads_and_exports_header_symbols():
     lib = L.lib()
     declared = L.header_functions()
-    assert len(declared) == len(L.SIGNATURES) == 30
+    assert len(declared) == len(L.SIGNATURES) == 31
     assert set(declared) == set(L.SIGNATURES)
     for name in declared:
         assert hasattr(lib, name), name
@@ -182,6 +182,13 @@ def test_workspace_sizes():
     assert lib.moe_grouped_gemm_wgrad_workspace_size(131072, 4096, 7168, 64) == 0      # c5 fc1: 16 x 28 tiles
     assert lib.moe_grouped_gemm_wgrad_workspace_size(4096, 64, 64, 1) == 0
     assert lib.moe_grouped_gemm_wgrad_workspace_size(4096, 64, 64, 4096) == 8192
+    # forward grouped GEMM: the tail list (counter, count, one int per group), for reductions of
+    # at least 4096 in whole 64-column steps
+    assert lib.moe_grouped_gemm_workspace_size(131072, 7168, 4096, 64) == 512     # c5 fc1: 4 * (64 + 64)
+    assert lib.moe_grouped_gemm_workspace_size(131072, 7168, 4096, 4096) == (4 * (64 + 4096) + 255) // 256 * 256
+    assert lib.moe_grouped_gemm_workspace_size(131072, 2048, 7168, 64) == 0       # c5 fc2: short reduction
+    assert lib.moe_grouped_gemm_workspace_size(4096, 4100, 256, 4) == 0           # K % 64 != 0
+    assert lib.moe_grouped_gemm_workspace_size(4096, 4096, 256, 0) == 0
     # router tf32 wgrad: [A_hi; A_hi; A_lo] and [B_hi; B_lo; B_hi] over 3M rows (+ fp32 planes when split)
     assert lib.moe_router_wgrad_tf32_workspace_size(4096, 64, 1000) >= 3 * 4096 * (64 + 1000) * 2
 

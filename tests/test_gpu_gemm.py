@@ -161,3 +161,40 @@ def test_pipelined_kernel_matches_drained_kernel(pkg, dev, sizes, K, N, swiglu, 
     # and both against the fp32 golden on sampled rows of every group
     a = x[rows.long()] if gather else x
     _sampled_check(a, w, offs.cpu(), piped, swiglu, rows_per_group=8)
+
+
+@pytest.mark.parametrize("sizes,K,N,swiglu,gather", [
+    # tails of 1, 127, 128 (128-row tiles), 129, 255 (256-row tiles), whole tiles, empty groups
+    ([1, 127, 128, 129, 255, 256, 512, 0, 385, 640], 4096, 512, False, False),
+    ([1, 127, 128, 129, 255, 256, 512, 0, 385, 640], 4096, 1024, True, True),
+    ([3, 0, 70, 2000, 128, 4097], 7168, 4096, True, False),       # fc1 class, K of the benchmark
+    ([40] * 200 + [300] * 20, 4096, 256, False, True),            # many 128-row tiles: several per workgroup
+    ([1] * 64, 4096, 8, False, False),                            # tails only, one partial column tile
+])
+def test_tail_tiles_match_full_tiles(pkg, dev, sizes, K, N, swiglu, gather):
+    """With its workspace the forward GEMM computes a group's last row tile of 1 to 128 rows as a
+    128-row tile, taken from a list after the 256-row tiles; without it every row tile has 256
+    rows. The per-element K order and rounding are the same: equal bit for bit."""
+    g = torch.Generator().manual_seed(sum(sizes) + K + N + 7)
+    M = sum(sizes)
+    w = (torch.randn(len(sizes), N, K, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    offs = pkg.ops.group_offsets_from_splits(sizes, dev)
+    assert pkg.ops._lib.lib().moe_grouped_gemm_workspace_size(M, K, N, len(sizes)) > 0
+    none = torch.empty(0, dtype=torch.uint8, device=dev)
+    if gather:
+        X = 501
+        x = torch.randn(X, K, generator=g).to(torch.bfloat16).to(dev)
+        rows = torch.randint(0, X, (M,), generator=g, dtype=torch.int32).to(dev)
+        tails = pkg.ops.grouped_gemm_gather(x, rows, w, offs, swiglu=swiglu)
+        full = pkg.ops.grouped_gemm_gather(x, rows, w, offs, swiglu=swiglu, workspace=none)
+    else:
+        x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+        ws = torch.full((4096,), 0xAB, dtype=torch.uint8, device=dev)  # stale contents: the list kernel rewrites it
+        tails = pkg.ops.grouped_gemm(x, w, offs, swiglu=swiglu, workspace=ws)
+        tails2 = pkg.ops.grouped_gemm(x, w, offs, swiglu=swiglu, workspace=ws)  # the same workspace again
+        full = pkg.ops.grouped_gemm(x, w, offs, swiglu=swiglu, workspace=none)
+        assert torch.equal(tails.view(torch.int16), tails2.view(torch.int16))
+    torch.cuda.synchronize()
+    assert torch.equal(tails.view(torch.int16), full.view(torch.int16)), f"sizes={sizes[:6]} K={K} N={N}"
+    a = x[rows.long()] if gather else x
+    _sampled_check(a, w, offs.cpu(), tails, swiglu, rows_per_group=8)
