@@ -681,7 +681,7 @@ def main():
     del xp
 
     fc1 = stages["fc1_swiglu"]
-    roofline = {"kernel": "grouped_gemm_pp_kernel<swiglu, gather> (fc1 + SwiGLU)", "bound": "mfma",
+    roofline = {"kernel": "grouped_gemm_pp_kernel<swiglu, gather, tails> (fc1 + SwiGLU)", "bound": "mfma",
                 "achieved": fc1["TFLOP/s"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(fc1["TFLOP/s"] / BF16_PEAK_TFLOPS, 4), "traffic": None,
                 "flops_per_launch": fc1["flops"], "avg_launch_ms": fc1["ms"]}
