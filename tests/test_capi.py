@@ -177,9 +177,9 @@ def test_workspace_sizes():
     assert lib.moe_grouped_gemm_dgrad_workspace_size(160, 5120, 8192, 1) == 0    # 128-row tiles
     assert lib.moe_grouped_gemm_dgrad_workspace_size(288, 320, 8192, 1) == 0     # too short a reduction
     assert lib.moe_grouped_gemm_dgrad_workspace_size(288, 5128, 8192, 1) == 0    # N % 64 != 0
-    # wgrad group order: one int16 per group, only where a group has no more tiles than CUs (256 here)
+    # wgrad group order: one int16 per group, for two or more groups
     assert lib.moe_grouped_gemm_wgrad_workspace_size(131072, 7168, 2048, 64) == 256    # c5 fc2: 28 x 8 tiles
-    assert lib.moe_grouped_gemm_wgrad_workspace_size(131072, 4096, 7168, 64) == 0      # c5 fc1: 16 x 28 tiles
+    assert lib.moe_grouped_gemm_wgrad_workspace_size(131072, 4096, 7168, 64) == 256    # c5 fc1: 16 x 28 tiles
     assert lib.moe_grouped_gemm_wgrad_workspace_size(4096, 64, 64, 1) == 0
     assert lib.moe_grouped_gemm_wgrad_workspace_size(4096, 64, 64, 4096) == 8192
     # forward grouped GEMM: the tail list (counter, count, one int per group), for reductions of

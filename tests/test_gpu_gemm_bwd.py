@@ -162,13 +162,16 @@ def test_wgrad_small(pkg, dev, sizes, N, K):
             assert torch.count_nonzero(out[gi]) == 0
 
 
-def test_wgrad_group_order_is_bit_identical(pkg, dev):
-    # With the workspace the tiles take the groups largest first; without it, by index. Each tile's
-    # accumulation is the same either way, so dw is bit for bit the same (skewed ragged groups,
-    # empty ones and ties included).
+@pytest.mark.parametrize("sizes,N,K", [
+    ([3, 0, 700, 41, 700, 0, 1500, 64, 129, 5], 264, 520),
+    # 80 skewed groups x 8 tiles = 640 tiles: three rounds on 256 CUs, the second dealt in reverse
+    ([(37 * i * i) % 1500 for i in range(80)], 512, 1024),
+])
+def test_wgrad_group_order_is_bit_identical(pkg, dev, sizes, N, K):
+    # With the workspace the tiles take the groups largest first (dealt in reverse on odd rounds);
+    # without it, by index. Each tile's accumulation is the same either way, so dw is bit for bit
+    # the same (skewed ragged groups, empty ones and ties included).
     lib, ptr = pkg._lib.lib(), pkg._lib.ptr
-    sizes = [3, 0, 700, 41, 700, 0, 1500, 64, 129, 5]
-    N, K = 264, 520
     g = torch.Generator().manual_seed(23)
     dy = torch.randn(sum(sizes), N, generator=g).to(torch.bfloat16).to(dev)
     x = torch.randn(sum(sizes), K, generator=g).to(torch.bfloat16).to(dev)
