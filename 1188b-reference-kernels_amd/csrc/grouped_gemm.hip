@@ -8,10 +8,13 @@
 // SwiGLU (fused, no reference function): h = silu(y[:, :F]) * y[:, F:] on the
 // fp32 accumulators, F = N / 2, rounded once to bf16.
 //
-// Two kernels: grouped_gemm_pipe_kernel (further down; K > 128 and 16-byte
-// output rows, i.e. every MoE shape) and grouped_gemm_kernel, the drained
-// form for the rest (K <= 128, unaligned outputs). Both are bit-identical on
-// the shapes both take. Shared shape (gfx950), as the drained kernel has it:
+// Three kernels: grouped_gemm_pp_kernel (last; two wavefronts per SIMD, for
+// K % 64 == 0 and K >= 192 with 16-byte output rows, i.e. every MoE shape, with
+// an optional 128-row form for group tails), grouped_gemm_pipe_kernel (one
+// wavefront per SIMD; the same shapes with a K tail) and grouped_gemm_kernel,
+// the drained form for the rest (K <= 128, unaligned outputs). They are
+// bit-identical on the shapes they share. Shared shape (gfx950), as the
+// drained kernel has it:
 //   * one persistent workgroup of 4 wavefronts (one per SIMD) per CU; output
 //     tile 256 x 256, K step 64; each wavefront owns 128 x 128 of the tile as
 //     4 x 4 blocks of v_mfma_f32_32x32x16_bf16 (256 accumulator registers);
