@@ -1030,9 +1030,9 @@ __device__ __forceinline__ void pp_body(const GemmArgs &p, char *smem, const PpT
     return true;
   };
 
-  // ---- DMA sources. This wavefront's A rows: blocks (grp * 16 + j * 4 + wm),
-  // 8 rows each; its B rows: blocks ((1 - grp) * 16 + j * 4 + wm) (the other
-  // group's half, see above).
+  // ---- DMA sources. This wavefront's A rows: blocks (grp * kTM / 16 + j * 4 +
+  // wm), 8 rows each; its B rows: blocks ((1 - grp) * 16 + j * 4 + wm) (the
+  // other group's half, see above).
   const uint32_t row_bytes = static_cast<uint32_t>(K) * 2u;
   const int ncols32 = static_cast<int>(p.ncols);
   const int src_rows32 = static_cast<int>(min(p.a_src_rows, int64_t(0x7fffffff)));
