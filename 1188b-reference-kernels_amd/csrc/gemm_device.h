@@ -103,5 +103,64 @@ inline int num_cus() {
   return cache[dev];
 }
 
+// Tail list of the ping-pong kernels (workspace layout, ints): a group whose
+// last 256-row tile would have 1 to 128 rows leaves that tile to the 128-row
+// form of the kernel. tails_init_kernel lists those groups in order; after
+// their 256-row tiles the persistent workgroups take (group, column tile)
+// units u = 0, 1, ... of the list from the counter, unit u = list[u / ntiles],
+// column tile u % ntiles.
+constexpr int kTailCtr = 0;     // units handed out
+constexpr int kTailCount = 32;  // groups in the list (own 128-byte line)
+constexpr int kTailList = 64;   // the groups, ascending
+#ifndef MOE_GEMM_TAILS_MIN_K
+#define MOE_GEMM_TAILS_MIN_K 4096
+#endif
+constexpr int64_t kTailsMinK = MOE_GEMM_TAILS_MIN_K;  // shortest reduction that uses the 128-row tail tiles
+inline size_t tails_bytes(int64_t G) { return sizeof(int) * static_cast<size_t>(kTailList + G); }
+
+__device__ __forceinline__ bool has_tail(int64_t m) {
+  const int64_t r = m % 256;
+  return r >= 1 && r <= 128;
+}
+
+namespace {
+
+// One workgroup of 256 threads: each thread counts the tails of its chunk of
+// groups, an exclusive scan over the threads gives the chunk's first list
+// position, then each thread lists its chunk's tail groups. Group g is rows
+// offsets[g] .. offsets[g + 1] - 1, clamped to [0, M].
+__global__ __launch_bounds__(256) void tails_init_kernel(const int32_t *offsets, int64_t G, int64_t M, int *tails) {
+  __shared__ int part[256];
+  const int t = threadIdx.x;
+  const int64_t per = (G + 255) / 256;
+  const int64_t g0 = min(G, t * per), g1 = min(G, g0 + per);
+  auto tail_at = [&](int64_t g) {
+    const int64_t lo = min(max(static_cast<int64_t>(offsets[g]), int64_t(0)), M);
+    const int64_t hi = min(max(static_cast<int64_t>(offsets[g + 1]), lo), M);
+    return has_tail(hi - lo);
+  };
+  int n = 0;
+  for (int64_t g = g0; g < g1; ++g) n += tail_at(g) ? 1 : 0;
+  part[t] = n;
+  __syncthreads();
+  if (t == 0) {
+    int acc = 0;
+    for (int i = 0; i < 256; ++i) {
+      const int v = part[i];
+      part[i] = acc;
+      acc += v;
+    }
+    tails[kTailCount] = acc;
+    tails[kTailCtr] = 0;
+  }
+  __syncthreads();
+  int pos = part[t];
+  for (int64_t g = g0; g < g1; ++g) {
+    if (tail_at(g)) tails[kTailList + pos++] = static_cast<int>(g);
+  }
+}
+
+}  // namespace
+
 }  // namespace gemm
 }  // namespace moe

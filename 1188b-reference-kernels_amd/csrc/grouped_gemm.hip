@@ -92,59 +92,6 @@ struct GemmArgs {
   int *tails;      // ping-pong kernel: tail list (kTail* layout) or nullptr (tails in 256-row tiles)
 };
 
-// Tails of the ping-pong kernel (workspace layout, ints): a group whose last
-// 256-row tile would have 1 to 128 rows leaves that tile to the 128-row form
-// of the kernel. tails_init_kernel lists those groups in order; after their
-// 256-row tiles the persistent workgroups take (group, column tile) units
-// u = 0, 1, ... of the list from the counter, unit u = list[u / ntiles],
-// column tile u % ntiles.
-constexpr int kTailCtr = 0;     // units handed out
-constexpr int kTailCount = 32;  // groups in the list (own 128-byte line)
-constexpr int kTailList = 64;   // the groups, ascending
-#ifndef MOE_GEMM_TAILS_MIN_K
-#define MOE_GEMM_TAILS_MIN_K 4096
-#endif
-constexpr int64_t kTailsMinK = MOE_GEMM_TAILS_MIN_K;  // shortest reduction that uses the 128-row tail tiles
-inline size_t tails_bytes(int64_t G) { return sizeof(int) * static_cast<size_t>(kTailList + G); }
-
-__device__ __forceinline__ bool has_tail(int64_t m) {
-  const int64_t r = m % 256;
-  return r >= 1 && r <= 128;
-}
-
-// One workgroup of 256 threads: each thread counts the tails of its chunk of
-// groups, an exclusive scan over the threads gives the chunk's first list
-// position, then each thread lists its chunk's tail groups.
-__global__ __launch_bounds__(256) void tails_init_kernel(GemmArgs p) {
-  __shared__ int part[256];
-  const int t = threadIdx.x;
-  const int64_t per = (p.G + 255) / 256;
-  const int64_t g0 = min(p.G, t * per), g1 = min(p.G, g0 + per);
-  auto tail_at = [&](int64_t g) {
-    const int64_t lo = min(max(static_cast<int64_t>(p.offsets[g]), int64_t(0)), p.M);
-    const int64_t hi = min(max(static_cast<int64_t>(p.offsets[g + 1]), lo), p.M);
-    return has_tail(hi - lo);
-  };
-  int n = 0;
-  for (int64_t g = g0; g < g1; ++g) n += tail_at(g) ? 1 : 0;
-  part[t] = n;
-  __syncthreads();
-  if (t == 0) {
-    int acc = 0;
-    for (int i = 0; i < 256; ++i) {
-      const int v = part[i];
-      part[i] = acc;
-      acc += v;
-    }
-    p.tails[kTailCount] = acc;
-    p.tails[kTailCtr] = 0;
-  }
-  __syncthreads();
-  int pos = part[t];
-  for (int64_t g = g0; g < g1; ++g) {
-    if (tail_at(g)) p.tails[kTailList + pos++] = static_cast<int>(g);
-  }
-}
 constexpr int kPpLdsBytes = 5 * 256 * 128;  // ping-pong kernel LDS: 160 KiB
 
 __device__ __forceinline__ int swz(int row) { return (row >> 1) & (kChunks - 1); }
@@ -1404,7 +1351,7 @@ int launch_grouped_gemm(const char *fn, const moe_bf16_t *a, int64_t a_src_rows,
   if (pingpong && K >= kTailsMinK && workspace != nullptr && workspace_bytes >= tails_bytes(G) &&
       is_aligned(workspace, 256)) {
     p.tails = static_cast<int *>(workspace);
-    tails_init_kernel<<<dim3(1), dim3(256), 0, s>>>(p);
+    tails_init_kernel<<<dim3(1), dim3(256), 0, s>>>(p.offsets, p.G, p.M, p.tails);
   }
   if (pingpong && p.tails != nullptr) {
     if (swiglu) {
@@ -1447,8 +1394,8 @@ extern "C" {
 size_t moe_grouped_gemm_workspace_size(int64_t M_total, int64_t K, int64_t N, int64_t G) {
   (void)M_total;
   (void)N;
-  if (G < 1 || G > 4096 || K % moe::gemm::kBK != 0 || K < moe::kTailsMinK) return 0;
-  return (moe::tails_bytes(G) + 255) / 256 * 256;
+  if (G < 1 || G > 4096 || K % moe::gemm::kBK != 0 || K < moe::gemm::kTailsMinK) return 0;
+  return (moe::gemm::tails_bytes(G) + 255) / 256 * 256;
 }
 
 int moe_grouped_gemm(const moe_bf16_t *a, int64_t M_total, int64_t K, const moe_bf16_t *w, int64_t G,

@@ -77,6 +77,7 @@ struct BwdArgs {
   int64_t chunk;            // rows per group when offsets is nullptr
   int64_t kchunk;           // split dgrad: reduction columns of split g = [g kchunk, (g + 1) kchunk), the last to N
   const int16_t *order;     // wgrad (kOrder): the groups in the order the tiles take them
+  int *tails;               // dgrad ping-pong kernel: tail list (kTail* layout) or nullptr
 };
 
 __device__ __forceinline__ int kc_swz(int row) { return (row >> 1) & 7; }
@@ -1003,24 +1004,47 @@ __device__ __forceinline__ bf16x8 read_rm_frag_rows(uint32_t addr) {
 // DMA is waited for at the end of its issuer's next load phase (vmcnt <= 8, or
 // 8 + 16 after an epilogue's stores). A tile's reduction step count varies
 // (wgrad: its group's rows), stages past a tile's end come from the next tile.
-template <bool kWgrad, bool kOrder>
-__global__ __launch_bounds__(512) void grouped_gemm_bwd_pp_kernel(BwdArgs p) {
+//
+// dgrad with a tail list: tiles of kTM = 128 rows (a wavefront's 32 rows,
+// half the A blocks per stage, the first half of each A slot) for group tails
+// of 1 to 128 rows, taken after the 256-row tiles (grouped_gemm_bwd_pp_kernel).
+struct BwdTile {
+  int g, lo, hi;
+  int i0;
+  uint32_t nt;
+  int rows_valid;
+  int ktiles;
+};
+constexpr int kBwdPpLdsBytes = 5 * 256 * kBK * 2;  // 160 KiB
+
+// kTM = 256: the persistent workgroup b of P (the grid) takes its tiles in
+// the static order; kTM = 128: the one tile *one.
+template <bool kWgrad, bool kOrder, int kTM, bool kTails>
+__device__ __forceinline__ void bwd_pp_body(const BwdArgs &p, char *smem, const BwdTile *one) {
   static_assert(!kOrder || kWgrad, "the group order is a wgrad schedule");
-  constexpr int kBM = 256;
+  static_assert(kTM == 256 || (kTM == 128 && !kWgrad), "tile rows");
+  static_assert(!kTails || !kWgrad, "tail tiles are a dgrad form");
+  constexpr int kBM = kTM;
   constexpr int kAS = 3, kBS = 2;
   constexpr int kSlotBytes = 256 * kBK * 2;  // 32 KiB
   constexpr int kHalfBytes = kSlotBytes / 2;  // one group's B columns
   constexpr int kBBase = kAS * kSlotBytes;
   constexpr int kHalfRow = 256;               // bytes per reduction row of a B half tile
-  constexpr int kMI = 4, kNI = 8;
-  constexpr int kStores = 16;                 // 16-byte stores per lane per tile
-  constexpr int kDmaA = 4, kDmaB = 4;
+  constexpr int kMI = kTM / 64, kNI = 8;
+  constexpr int kWR = kTM / 4;                // dgrad: tile rows of a wavefront
+  constexpr int kStores = kMI * 4;            // 16-byte stores per lane per tile
+  constexpr int kDmaA = kTM / 64, kDmaB = 4;
+  constexpr int kABlk = kTM / 16;             // 1 KiB A blocks DMA'd by one group per stage
   static_assert(kDmaA + kDmaB + kStores <= 63, "vmcnt range");
-  __shared__ __attribute__((aligned(1024))) char smem[kAS * kSlotBytes + kBS * kSlotBytes];
+  static_assert(kAS * kSlotBytes + kBS * kSlotBytes <= kBwdPpLdsBytes, "LDS");
   lds_char *const sbase = (lds_char *)smem;
   const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sbase));
 
-  const int tid = threadIdx.x;
+  // The thread index through an opaque copy: the lane-derived values of the
+  // 256-row and the 128-row form are computed separately, not kept live from
+  // one form to the other.
+  int tid = threadIdx.x;
+  if constexpr (kTails) asm volatile("" : "+v"(tid));
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
@@ -1057,8 +1081,10 @@ __global__ __launch_bounds__(512) void grouped_gemm_bwd_pp_kernel(BwdArgs p) {
   };
   const uint32_t ntl = static_cast<uint32_t>(p.ntiles);
   const uint32_t wg_rows = static_cast<uint32_t>(ceil_div(N, kBM));
+  // dgrad row tiles of a group (kTails: all but a last tile of at most 128
+  // rows, which the 128-row form takes).
   auto row_tiles = [&](int lo, int hi) -> uint32_t {
-    return kWgrad ? wg_rows : static_cast<uint32_t>(hi - lo + kBM - 1) / kBM;
+    return kWgrad ? wg_rows : static_cast<uint32_t>(hi - lo + (kTails ? 127 : kBM - 1)) / kBM;
   };
   auto group_at = [&](int i) -> int {
     if constexpr (kOrder) {
@@ -1071,16 +1097,15 @@ __global__ __launch_bounds__(512) void grouped_gemm_bwd_pp_kernel(BwdArgs p) {
   uint32_t tiles_before = 0;
   group_range(g_act, g_lo, g_hi);
   uint32_t mt_g = row_tiles(g_lo, g_hi);
-  struct Tile {
-    int g, lo, hi;
-    int i0;
-    uint32_t nt;
-    int rows_valid;
-    int ktiles;
-  };
+  using Tile = BwdTile;
   const uint32_t P32 = static_cast<uint32_t>(P);
   const uint32_t L0 = static_cast<uint32_t>((b % 8) * (P / 8) + b / 8);
   auto find_tile = [&](uint32_t round, Tile &t) -> bool {
+    if constexpr (kTM == 128) {
+      if (round > 0) return false;
+      t = *one;
+      return true;
+    }
     // With the group order (largest first) odd rounds deal the tiles in
     // reverse, so a workgroup that took one of the larger tiles of a round
     // takes one of the smaller ones of the next (the patches stay whole).
@@ -1119,7 +1144,7 @@ __global__ __launch_bounds__(512) void grouped_gemm_bwd_pp_kernel(BwdArgs p) {
     return true;
   };
 
-  // ---- DMA sources: A blocks (grp * 16 + j * 4 + wm) of a stage; B blocks
+  // ---- DMA sources: A blocks (grp * kABlk + j * 4 + wm) of a stage; B blocks
   // (j * 4 + wm) of the other group's half.
   const uint32_t n32 = static_cast<uint32_t>(N), k32 = static_cast<uint32_t>(K);
   __amdgpu_buffer_rsrc_t ra, rb;
@@ -1135,7 +1160,7 @@ __global__ __launch_bounds__(512) void grouped_gemm_bwd_pp_kernel(BwdArgs p) {
       ra = make_rsrc(p.a + static_cast<int64_t>(t.lo) * N, rows * n32 * 2u);
 #pragma unroll
       for (int j = 0; j < kDmaA; ++j) {
-        const int krow = (grp * 16 + j * 4 + wm) * 2 + (ln >> 5);
+        const int krow = (grp * kABlk + j * 4 + wm) * 2 + (ln >> 5);
         const uint32_t lchunk = static_cast<uint32_t>((ln & 31) ^ rm16_swz(krow));
         a_off[j] = static_cast<int>(static_cast<uint32_t>(krow) * n32 * 2u + static_cast<uint32_t>(t.i0) * 2u + lchunk * 16u);
       }
@@ -1144,7 +1169,7 @@ __global__ __launch_bounds__(512) void grouped_gemm_bwd_pp_kernel(BwdArgs p) {
       ra = make_rsrc(p.a + static_cast<int64_t>(t.i0) * N, valid ? static_cast<uint32_t>(t.rows_valid) * n32 * 2u : 0u);
 #pragma unroll
       for (int j = 0; j < kDmaA; ++j) {
-        const int r = (grp * 16 + j * 4 + wm) * 8 + (ln >> 3);
+        const int r = (grp * kABlk + j * 4 + wm) * 8 + (ln >> 3);
         const uint32_t lchunk = static_cast<uint32_t>((ln & 7) ^ kc_swz(r));
         a_off[j] = static_cast<int>(static_cast<uint32_t>(r) * n32 * 2u + lchunk * 16u);
       }
@@ -1172,7 +1197,7 @@ __global__ __launch_bounds__(512) void grouped_gemm_bwd_pp_kernel(BwdArgs p) {
     const uint32_t b_dst = lds_base + kBBase + sbs * kSlotBytes + (1 - grp) * kHalfBytes;
 #pragma unroll
     for (int j = 0; j < kDmaA; ++j) {
-      const uint32_t blk = grp * 16 + j * 4 + wm;
+      const uint32_t blk = grp * kABlk + j * 4 + wm;
       dma16b(ra, (lds_void *)(uintptr_t)(a_dst + blk * 1024), a_off[j], kt_a * a_step);
     }
 #pragma unroll
@@ -1185,7 +1210,7 @@ __global__ __launch_bounds__(512) void grouped_gemm_bwd_pp_kernel(BwdArgs p) {
 
   // ---- fragments
   const int fq = lane >> 4;
-  const int ra0 = wm * 64 + (lane & 15);
+  const int ra0 = wm * kWR + (lane & 15);
   const uint32_t fa0 = ra0 * kKCRow + ((fq ^ kc_swz(ra0)) << 4);  // dgrad A (KC)
   const int rg = lane >> 4, rj = (lane >> 2) & 3, rq = lane & 3;
   const uint32_t rm_in = ((rq >> 1) << 4) + (rq & 1) * 8;
@@ -1229,7 +1254,7 @@ __global__ __launch_bounds__(512) void grouped_gemm_bwd_pp_kernel(BwdArgs p) {
                                                              (zero && ks == 0) ? f32x4{} : acc[i][j], 0, 0, 0);
   };
   // Epilogue: register r of lane l in block (i, j) holds output row
-  // wm * 64 + i * 16 + l % 16 and column grp * 128 + j * 16 + 4 (l / 16) + r of
+  // wm * kWR + i * 16 + l % 16 and column grp * 128 + j * 16 + 4 (l / 16) + r of
   // the tile; bf16 RNE, v_permlane16_swap pairs blocks j, j + 1 so each lane
   // stores 8 consecutive columns (16 bytes) through a resource over the tile's
   // valid rows; columns past K get an offset past it.
@@ -1245,7 +1270,7 @@ __global__ __launch_bounds__(512) void grouped_gemm_bwd_pp_kernel(BwdArgs p) {
     const int wcol0 = static_cast<int>(t.nt) * kBN + grp * 128 + (eq & 1) * 16 + (eq >> 1) * 8;
 #pragma unroll
     for (int i = 0; i < kMI; ++i) {
-      const uint32_t orow = static_cast<uint32_t>(wm * 64 + i * 16 + (ln & 15));
+      const uint32_t orow = static_cast<uint32_t>(wm * kWR + i * 16 + (ln & 15));
 #pragma unroll
       for (int jp = 0; jp < kNI; jp += 2) {
         uint32_t w[2][2];
@@ -1287,7 +1312,7 @@ __global__ __launch_bounds__(512) void grouped_gemm_bwd_pp_kernel(BwdArgs p) {
     for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
       for (int j = 0; j < kDmaA; ++j) {
-        const uint32_t blk = grp * 16 + j * 4 + wm;
+        const uint32_t blk = grp * kABlk + j * 4 + wm;
         dma16b(ra, (lds_void *)(uintptr_t)(lds_base + kt * kSlotBytes + blk * 1024), a_off[j], kt * a_step);
       }
     }
@@ -1354,6 +1379,39 @@ __global__ __launch_bounds__(512) void grouped_gemm_bwd_pp_kernel(BwdArgs p) {
   wait_dma();  // no LDS DMA outlives the workgroup
 }
 
+// One persistent workgroup per CU takes its 256-row tiles in the static
+// order; with a tail list (dgrad) it then takes tail units from the list's
+// counter (thread 0 adds 1, the number reaches the other wavefronts through
+// the idle LDS ring) and computes each with the 128-row form, until the units
+// run out.
+template <bool kWgrad, bool kOrder, bool kTails>
+__global__ __launch_bounds__(512) void grouped_gemm_bwd_pp_kernel(BwdArgs p) {
+  __shared__ __attribute__((aligned(1024))) char smem[kBwdPpLdsBytes];
+  bwd_pp_body<kWgrad, kOrder, 256, kTails>(p, smem, nullptr);
+  if constexpr (kTails) {
+    volatile int *bcast = reinterpret_cast<volatile int *>(smem);
+    const int ntl = static_cast<int>(p.ntiles);
+    const int ktiles = max((static_cast<int>(p.N) + kBK - 1) / kBK, 3);
+    for (;;) {
+      __syncthreads();  // the ring is idle: every wavefront has left its last tile
+      if (threadIdx.x == 0) {
+        bcast[0] = __hip_atomic_fetch_add(p.tails + kTailCtr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+      const int u = __builtin_amdgcn_readfirstlane(bcast[0]);
+      __syncthreads();  // every wavefront has read it before the ring is used again
+      if (u >= p.tails[kTailCount] * ntl) break;
+      const int g = p.tails[kTailList + u / ntl];
+      const int M32 = static_cast<int>(p.M);
+      const int lo = min(max(p.offsets[g], 0), M32);
+      const int hi = min(max(p.offsets[g + 1], lo), M32);
+      const int r = (hi - lo) % 256;
+      const BwdTile t{g, lo, hi, hi - r, static_cast<uint32_t>(u % ntl), r, ktiles};
+      bwd_pp_body<kWgrad, kOrder, 128, kTails>(p, smem, &t);
+    }
+  }
+}
+
 template <bool kWgrad, int kOut = 0, bool kSplit = false, bool kOrder = false>
 void launch_pipe(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
   int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
@@ -1364,11 +1422,11 @@ void launch_pipe(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
 #ifndef MOE_GEMM_BWD_PINGPONG
 #define MOE_GEMM_BWD_PINGPONG 1
 #endif
-template <bool kWgrad, bool kOrder = false>
+template <bool kWgrad, bool kOrder = false, bool kTails = false>
 void launch_pp(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
   int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
   grid = std::max<int64_t>(8, (grid + 7) / 8 * 8);
-  grouped_gemm_bwd_pp_kernel<kWgrad, kOrder><<<dim3(grid), dim3(512), 0, s>>>(p);
+  grouped_gemm_bwd_pp_kernel<kWgrad, kOrder, kTails><<<dim3(grid), dim3(512), 0, s>>>(p);
 }
 
 // order[rank] = group, rank = the number of groups with more rows (or as many
@@ -1548,6 +1606,16 @@ DgradSplit dgrad_split_plan(int64_t M, int64_t N, int64_t K, int64_t G) {
   return pl;
 }
 
+// dgrad runs the 256-row ping-pong kernel (no split; groups of more than 160
+// rows on average; whole reduction steps) with a reduction long enough for the
+// 128-row tail tiles: group tails of 1 to 128 rows then take 128-row tiles
+// after the 256-row ones, listed in a workspace of tails_bytes(G).
+bool dgrad_pp_tails(int64_t M, int64_t N, int64_t G) {
+  using namespace moe;
+  return MOE_GEMM_BWD_PINGPONG && G >= 1 && G <= 4096 && M > 160 * G && M < (int64_t(1) << 31) && N % kBK == 0 &&
+         N >= std::max<int64_t>(3 * kBK, gemm::kTailsMinK);
+}
+
 }  // namespace
 
 extern "C" {
@@ -1555,7 +1623,8 @@ extern "C" {
 size_t moe_grouped_gemm_dgrad_workspace_size(int64_t M_total, int64_t N, int64_t K, int64_t G) {
   if (M_total < 0 || N < 0 || K < 0 || G < 1) return 0;
   const DgradSplit sp = dgrad_split_plan(M_total, N, K, G);
-  return sp.s > 1 ? moe::align_up(static_cast<size_t>(sp.s) * M_total * K * 4) : 0;
+  if (sp.s > 1) return moe::align_up(static_cast<size_t>(sp.s) * M_total * K * 4);
+  return dgrad_pp_tails(M_total, N, G) ? moe::align_up(moe::gemm::tails_bytes(G)) : 0;
 }
 
 int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, const moe_bf16_t *w, int64_t G,
@@ -1589,6 +1658,7 @@ int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, con
   p.chunk = 0;
   p.kchunk = 0;
   p.order = nullptr;
+  p.tails = nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
   // One group with few output tiles (fewer than half the CUs) and a workspace
   // for the fp32 partials: the reduction is split over the idle CUs.
@@ -1612,7 +1682,16 @@ int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, con
   if (M_total <= 160 * G || N % kBK != 0 || N < 3 * kBK) {
     launch_dgrad128(p, (ceil_div(M_total, 128) + G) * p.ntiles, s);
   } else if (MOE_GEMM_BWD_PINGPONG) {
-    launch_pp<false>(p, (ceil_div(M_total, 256) + G) * p.ntiles, s);
+    // With a workspace and a long reduction, group tails of at most 128 rows
+    // are listed first and computed as 128-row tiles after the 256-row ones.
+    if (dgrad_pp_tails(M_total, N, G) && workspace != nullptr && workspace_bytes >= gemm::tails_bytes(G) &&
+        is_aligned(workspace, kWsAlign)) {
+      p.tails = static_cast<int *>(workspace);
+      gemm::tails_init_kernel<<<dim3(1), dim3(256), 0, s>>>(group_offsets, G, M_total, p.tails);
+      launch_pp<false, false, true>(p, (ceil_div(M_total, 256) + G) * p.ntiles, s);
+    } else {
+      launch_pp<false>(p, (ceil_div(M_total, 256) + G) * p.ntiles, s);
+    }
   } else {
     launch_pipe<false>(p, (ceil_div(M_total, 256) + G) * p.ntiles, s);
   }
@@ -1662,6 +1741,7 @@ int moe_grouped_gemm_wgrad(const moe_bf16_t *dy, const moe_bf16_t *x, int64_t M_
   p.chunk = 0;
   p.kchunk = 0;
   p.order = nullptr;
+  p.tails = nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t tiles = G * ceil_div(N, 256) * p.ntiles;
   // Every group has the same tile count and a tile costs in proportion to its
@@ -1737,6 +1817,7 @@ int moe_router_dgrad_tf32(const float *grad_output, int64_t M, int64_t K, const 
   p.chunk = M;
   p.kchunk = 0;
   p.order = nullptr;
+  p.tails = nullptr;
   if (M <= 160 || (3 * K) % kBK != 0 || 3 * K < 3 * kBK) launch_dgrad128<1>(p, (ceil_div(M, 128) + 1) * p.ntiles, s);
   else launch_pipe<false, 1>(p, (ceil_div(M, 256) + 1) * p.ntiles, s);
   return check_launch(fn);
@@ -1837,6 +1918,7 @@ int moe_router_wgrad_tf32(const float *grad_output, int64_t M, int64_t N, const 
   p.chunk = pl.c;
   p.kchunk = 0;
   p.order = nullptr;
+  p.tails = nullptr;
   launch_pipe<true, 1>(p, ceil_div(N, 256) * p.ntiles * p.G, s);
   if (split) {
     const int64_t q = N * K / 4;

@@ -486,10 +486,13 @@ def grouped_gemm_gather(x: torch.Tensor, a_rows: torch.Tensor, w: torch.Tensor, 
 
 
 def grouped_gemm_dgrad(dy: torch.Tensor, w: torch.Tensor, group_offsets: torch.Tensor, *,
-                       out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                       out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """dx[rows of g] = dy[rows of g] @ w[g] (bf16 in, fp32 accumulate, bf16 out).
 
     dy bf16 [M, N]; w bf16 [G, N, K] (the forward's weights); group_offsets int32 [G+1] on the device.
+    workspace: uint8 device tensor of moe_grouped_gemm_dgrad_workspace_size bytes (a one-group split's
+    fp32 partials, or the list of groups whose last row tile has at most 128 rows); allocated when
+    None; an empty tensor runs without one.
     """
     _on_gpu("dy", dy)
     _on_gpu("w", w)
@@ -505,9 +508,15 @@ def grouped_gemm_dgrad(dy: torch.Tensor, w: torch.Tensor, group_offsets: torch.T
     M = dy.shape[0]
     dyc, wc, oc = dy.contiguous(), w.contiguous(), group_offsets.contiguous()
     out = _out(out, (M, K), torch.bfloat16, dy.device)
-    # A one-group dgrad with few output tiles splits its reduction into fp32 partials in a workspace.
+    # A one-group dgrad with few output tiles splits its reduction into fp32 partials in a workspace;
+    # with long reductions the workspace lists the group tails of at most 128 rows.
     nbytes = _lib.lib().moe_grouped_gemm_dgrad_workspace_size(M, N, K, G)
-    ws = _ws(nbytes, dy.device)
+    if workspace is not None and workspace.numel() == 0:
+        nbytes = 0
+    if workspace is None or workspace.numel() * workspace.element_size() < nbytes:
+        ws = _ws(nbytes, dy.device)
+    else:
+        ws, nbytes = workspace, workspace.numel() * workspace.element_size()
     call("moe_grouped_gemm_dgrad", ptr(dyc), M, N, ptr(wc), G, K, ptr(oc), ptr(out), ptr(ws), nbytes, stream_handle())
     return out
 

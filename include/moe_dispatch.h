@@ -295,7 +295,13 @@ int moe_grouped_gemm_gather(const moe_bf16_t *x, int64_t x_rows, const int32_t *
  *   than half the CUs (case37) splits its reduction over the idle CUs into
  *   fp32 partial planes in the workspace, summed in split order (deterministic)
  *   and rounded once; otherwise (NULL, 0, or a smaller size) one pass as above.
- *   The size is 0 where no split applies; it depends on the current device's
+ *   Without a split, groups of more than 160 rows on average and a reduction
+ *   N >= 4096 (N % 64 == 0), the workspace (4 * (64 + G) bytes, rounded up to
+ *   256) lists the groups whose last 256-row tile would hold 1 to 128 rows;
+ *   those tiles then run as 128-row tiles after the 256-row ones (the same
+ *   results bit for bit, less padding). The list is rebuilt on the stream by
+ *   every call: calls that share one workspace must not overlap.
+ *   The size is 0 where neither applies; it depends on the current device's
  *   CU count. */
 size_t moe_grouped_gemm_dgrad_workspace_size(int64_t M_total, int64_t N, int64_t K, int64_t G);
 int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, const moe_bf16_t *w,

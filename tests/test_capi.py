@@ -172,7 +172,13 @@ def test_workspace_sizes():
     # one-group dgrad reduction split (no GPU here: the CU count reads as 256): case37
     # [288 x 5120] @ [5120 x 8192] has 2 x 32 output tiles -> 4 splits of 20 steps, fp32 planes
     assert lib.moe_grouped_gemm_dgrad_workspace_size(288, 5120, 8192, 1) == 4 * 288 * 8192 * 4
-    assert lib.moe_grouped_gemm_dgrad_workspace_size(4096, 5120, 8192, 1) == 0   # 512 tiles: no split
+    # no split (512 tiles), a reduction of at least 4096: the tail list, 4 * (64 + G) bytes rounded to 256
+    assert lib.moe_grouped_gemm_dgrad_workspace_size(4096, 5120, 8192, 1) == 512
+    assert lib.moe_grouped_gemm_dgrad_workspace_size(131072, 4096, 7168, 64) == 512    # c5 fc1 dgrad
+    assert lib.moe_grouped_gemm_dgrad_workspace_size(131072, 7168, 2048, 64) == 512    # c5 fc2 dgrad
+    assert lib.moe_grouped_gemm_dgrad_workspace_size(131072, 4096, 7168, 4096) == 0    # 128-row tiles (32 rows a group)
+    assert lib.moe_grouped_gemm_dgrad_workspace_size(131072, 2048, 7168, 64) == 0      # reduction below 4096
+    assert lib.moe_grouped_gemm_dgrad_workspace_size(4096, 4160, 8192, 1) == 512       # 4160 = 65 steps
     assert lib.moe_grouped_gemm_dgrad_workspace_size(288, 5120, 8192, 2) == 0    # several groups
     assert lib.moe_grouped_gemm_dgrad_workspace_size(160, 5120, 8192, 1) == 0    # 128-row tiles
     assert lib.moe_grouped_gemm_dgrad_workspace_size(288, 320, 8192, 1) == 0     # too short a reduction

@@ -140,6 +140,36 @@ def test_dgrad_split_reduction(pkg, dev):
     assert_bits_equal(outs[0], outs[1], "split dgrad repeat")
 
 
+@pytest.mark.parametrize("sizes,N,K", [
+    # tails of 1, 127, 128 (128-row tiles), 129, 255 (256-row tiles), whole tiles, an empty group; K tail
+    ([1, 127, 128, 129, 255, 256, 512, 0, 385, 640], 4096, 520),
+    ([3, 0, 70, 2000, 128, 4097], 7168, 2048),       # fc2 dgrad class: the benchmark's reduction and width
+    ([100] * 100 + [2000] * 10, 4096, 512),          # 200 tail units over the persistent grid
+    ([257] * 16, 4160, 8),                           # one-row tails, one narrow column tile, 65 steps
+])
+def test_dgrad_tail_tiles_match_full_tiles(pkg, dev, sizes, N, K):
+    """With its workspace dgrad computes a group's last row tile of 1 to 128 rows as a 128-row
+    tile, taken from a list after the 256-row tiles; without it every row tile has 256 rows. The
+    per-element reduction order and rounding are the same: equal bit for bit."""
+    lib = pkg._lib.lib()
+    M, G = sum(sizes), len(sizes)
+    assert lib.moe_grouped_gemm_dgrad_workspace_size(M, N, K, G) == (4 * (64 + G) + 255) // 256 * 256
+    g = torch.Generator().manual_seed(M + N + K + 11)
+    dy = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    w = (torch.randn(G, N, K, generator=g) * 0.05).to(torch.bfloat16)
+    offs = _offsets(sizes, dev)
+    dyd, wd = dy.to(dev), w.to(dev)
+    ws = torch.full((8192,), 0xAB, dtype=torch.uint8, device=dev)  # stale contents: the list kernel rewrites it
+    tails = pkg.ops.grouped_gemm_dgrad(dyd, wd, offs, workspace=ws)
+    tails2 = pkg.ops.grouped_gemm_dgrad(dyd, wd, offs, workspace=ws)  # the same workspace again
+    full = pkg.ops.grouped_gemm_dgrad(dyd, wd, offs, workspace=torch.empty(0, dtype=torch.uint8, device=dev))
+    torch.cuda.synchronize()
+    what = f"sizes={sizes[:6]} N={N} K={K}"
+    assert_bits_equal(tails.cpu(), tails2.cpu(), "tail dgrad repeat " + what)
+    assert_bits_equal(tails.cpu(), full.cpu(), "tail vs full tiles " + what)
+    _check(tails, ref_torch.grouped_gemm_dgrad_fp32(dy, w, sizes), "tail dgrad " + what)
+
+
 # ------------------------------------------------------------------ wgrad
 @pytest.mark.parametrize("sizes,N,K", [
     ([64], 256, 256),                       # one tile, one step
