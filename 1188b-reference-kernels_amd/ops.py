@@ -492,7 +492,7 @@ def grouped_gemm_dgrad(dy: torch.Tensor, w: torch.Tensor, group_offsets: torch.T
     dy bf16 [M, N]; w bf16 [G, N, K] (the forward's weights); group_offsets int32 [G+1] on the device.
     workspace: uint8 device tensor of moe_grouped_gemm_dgrad_workspace_size bytes (a one-group split's
     fp32 partials, or the list of groups whose last row tile has at most 128 rows); allocated when
-    None; an empty tensor runs without one.
+    None or smaller than that size; an empty tensor runs without one.
     """
     _on_gpu("dy", dy)
     _on_gpu("w", w)
