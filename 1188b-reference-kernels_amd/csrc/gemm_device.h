@@ -117,11 +117,14 @@ constexpr int kTailList = 64;   // the groups, ascending
 #endif
 constexpr int64_t kTailsMinK = MOE_GEMM_TAILS_MIN_K;  // shortest reduction that uses the 128-row tail tiles
 inline size_t tails_bytes(int64_t G) { return sizeof(int) * static_cast<size_t>(kTailList + G); }
+constexpr int kTailMaxRows = 128;  // longest tail of the list (the 128-row form's height)
 
 __device__ __forceinline__ bool has_tail(int64_t m) {
   const int64_t r = m % 256;
-  return r >= 1 && r <= 128;
+  return r >= 1 && r <= kTailMaxRows;
 }
+// 256-row tiles of a group of m rows when its tail (if has_tail) is left to the list.
+__device__ __forceinline__ int main_row_tiles(int m) { return (m + 255 - kTailMaxRows) / 256; }
 
 namespace {
 

@@ -934,7 +934,7 @@ __device__ __forceinline__ void pp_body(const GemmArgs &p, char *smem, const PpT
   };
   // 256-row tiles of a group (kTails: all but a last tile of at most 128
   // rows, which the 128-row form takes).
-  auto main_tiles = [&](int m) -> int { return kTails ? (m + 127) / 256 : (m + 255) / 256; };
+  auto main_tiles = [&](int m) -> int { return kTails ? main_row_tiles(m) : (m + 255) / 256; };
   int g_cur = 0, m_lo, m_hi;
   int64_t tiles_before = 0;
   group_rows(0, m_lo, m_hi);

@@ -1084,7 +1084,7 @@ __device__ __forceinline__ void bwd_pp_body(const BwdArgs &p, char *smem, const 
   // dgrad row tiles of a group (kTails: all but a last tile of at most 128
   // rows, which the 128-row form takes).
   auto row_tiles = [&](int lo, int hi) -> uint32_t {
-    return kWgrad ? wg_rows : static_cast<uint32_t>(hi - lo + (kTails ? 127 : kBM - 1)) / kBM;
+    return kWgrad ? wg_rows : static_cast<uint32_t>(kTails ? main_row_tiles(hi - lo) : (hi - lo + kBM - 1) / kBM);
   };
   auto group_at = [&](int i) -> int {
     if constexpr (kOrder) {
