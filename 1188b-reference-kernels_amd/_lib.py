@@ -35,7 +35,7 @@ MOE_MAP_EXPERT_MAJOR = 1
 MOE_EPILOGUE_NONE = 0
 MOE_EPILOGUE_SWIGLU = 1
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64

@@ -10,6 +10,7 @@ this package.  Generated inputs are returned on `device` (default "cuda").
 from . import (case03_moe_grouped_gemm_fc1_fwd, case04_moe_grouped_gemm_fc2_fwd,  # noqa: F401
                case05_moe_grouped_gemm_fc2_wgrad, case07_moe_grouped_gemm_fc1_dgrad,
                case08_moe_grouped_gemm_fc2_dgrad, case09_moe_grouped_gemm_fc1_wgrad,
+               case10_grouped_gemm_single_group_fc1_fwd, case14_grouped_gemm_single_group_fc2_fwd,
                case13_grouped_gemm_single_group_fc1_dgrad, case19_grouped_gemm_single_group_fc2_dgrad,
                case37_ref_musa_asm_bf16_gemm_nn_256x384, case38_ref_musa_asm_bf16_ssgemm_nt_320x256,
                case11_router_bwd_cast_bf16_to_fp32, case25_ref_unary_cast_fp32_to_bf16,
@@ -23,6 +24,7 @@ from . import (case03_moe_grouped_gemm_fc1_fwd, case04_moe_grouped_gemm_fc2_fwd,
 
 ALL = [case03_moe_grouped_gemm_fc1_fwd, case04_moe_grouped_gemm_fc2_fwd, case05_moe_grouped_gemm_fc2_wgrad,
        case07_moe_grouped_gemm_fc1_dgrad, case08_moe_grouped_gemm_fc2_dgrad, case09_moe_grouped_gemm_fc1_wgrad,
+       case10_grouped_gemm_single_group_fc1_fwd, case14_grouped_gemm_single_group_fc2_fwd,
        case13_grouped_gemm_single_group_fc1_dgrad, case19_grouped_gemm_single_group_fc2_dgrad,
        case37_ref_musa_asm_bf16_gemm_nn_256x384, case38_ref_musa_asm_bf16_ssgemm_nt_320x256,
        case11_router_bwd_cast_bf16_to_fp32, case25_ref_unary_cast_fp32_to_bf16,

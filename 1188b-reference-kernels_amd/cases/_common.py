@@ -10,18 +10,18 @@ from .. import inputs, ops
 
 def scatter_rows(row_id_map: torch.Tensor) -> tuple[int, bool]:
     """(num_out, dense): num_out = max(row_id_map) + 1 (0 if no entry is >= 0), the reference
-    functions' output row count, and whether the entries >= 0 are as many as num_out -- for a map
-    whose entries are distinct, as a row-id map's are, that they name every output row.
+    functions' output row count, and whether the entries >= 0 name every output row exactly once
+    (as a row-id map's do), so that a scatter writes every row. A map with repeated entries is
+    never dense, whatever its count.
 
-    One pass over the map (moe_map_extent) and one read-back of the pair, where the reference reads its max
+    One pass over the map (moe_map_extent) and one read-back, where the reference reads its max
     (kernel_cases/case21_ref_permute_with_mask_map_trans.py:64,
     kernel_results/case17_moe_permute_with_mask_map/binding.cpp:24).
     """
     if row_id_map.numel() == 0:
         return 0, True
-    mx, cnt = ops.map_extent(row_id_map)
-    num_out = mx + 1
-    return num_out, cnt == num_out
+    mx, _, bijective = ops.map_extent(row_id_map)
+    return mx + 1, bijective
 
 
 def permute_from_map(inp: torch.Tensor, row_id_map: torch.Tensor, probs, layout: str):

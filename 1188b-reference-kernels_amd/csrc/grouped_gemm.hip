@@ -90,6 +90,12 @@ struct GemmArgs {
   int64_t ntiles;  // column tiles per expert
   int vec_out;     // output rows are 16-byte aligned (ncols % 8 == 0, aligned base)
   int *tails;      // ping-pong kernel: tail list (kTail* layout) or nullptr (tails in 256-row tiles)
+  // Reduction split of the last tiles (ping-pong kernel, 0: none): the last split_tiles tiles of the
+  // static order are left to grouped_gemm_split_kernel, which computes each as split_ways ranges of
+  // split_steps K steps (the last range takes the rest) into fp32 planes of 256 x 256 (planes), and
+  // split_sum_kernel adds each tile's planes in range order and rounds once.
+  int split_tiles, split_ways, split_steps;
+  float *planes;
 };
 
 constexpr int kPpLdsBytes = 5 * 256 * 128;  // ping-pong kernel LDS: 160 KiB
@@ -862,13 +868,70 @@ struct PpTile {  // rows and groups in 32 bits: the host runs the kernel for M <
   int g, row0;
   uint32_t nt;
   int rows_valid;
+  int unit;  // split kernel: the unit (range * split_tiles + tile); otherwise 0
 };
 
+// Tiles of the static order (256-row tiles, no tail list) over all groups.
+__device__ __forceinline__ int64_t static_tile_count(const GemmArgs &p) {
+  const int M32 = static_cast<int>(p.M);
+  int64_t total = 0;
+  for (int g = 0; g < static_cast<int>(p.G); ++g) {
+    const int lo = min(max(p.offsets[g], 0), M32);
+    const int hi = min(max(p.offsets[g + 1], lo), M32);
+    total += static_cast<int64_t>((hi - lo + 255) / 256) * p.ntiles;
+  }
+  return total;
+}
+
+// Row tile and column tile of position q inside a group of mt_g row tiles: groups of kGroupM row
+// tiles x all column tiles, row tile fastest.
+__device__ __forceinline__ void patch_pos(uint32_t q, uint32_t ntl, uint32_t mt_g, uint32_t &mt, uint32_t &nt) {
+  const uint32_t per_grp = kGroupM * ntl;
+  const uint32_t full = mt_g / kGroupM;
+  if (q < full * per_grp) {
+    const uint32_t gq = q / per_grp, r = q - gq * per_grp;
+    nt = r / kGroupM;
+    mt = gq * kGroupM + r % kGroupM;
+  } else {
+    const uint32_t r = q - full * per_grp, gm = mt_g - full * kGroupM;
+    nt = r / gm;
+    mt = full * kGroupM + (r - nt * gm);
+  }
+}
+
+// Tile L of the static order (256-row tiles); false past the last tile.
+__device__ __forceinline__ bool static_tile(const GemmArgs &p, int64_t L, PpTile &t) {
+  const int M32 = static_cast<int>(p.M);
+  int64_t before = 0;
+  for (int g = 0; g < static_cast<int>(p.G); ++g) {
+    const int lo = min(max(p.offsets[g], 0), M32);
+    const int hi = min(max(p.offsets[g + 1], lo), M32);
+    const int mt_g = (hi - lo + 255) / 256;
+    const int64_t n = static_cast<int64_t>(mt_g) * p.ntiles;
+    if (L < before + n) {
+      uint32_t mt, nt;
+      patch_pos(static_cast<uint32_t>(L - before), static_cast<uint32_t>(p.ntiles), static_cast<uint32_t>(mt_g), mt,
+                nt);
+      t.g = g;
+      t.row0 = lo + static_cast<int>(mt) * 256;
+      t.nt = nt;
+      t.rows_valid = min(hi - t.row0, 256);
+      t.unit = 0;
+      return true;
+    }
+    before += n;
+  }
+  return false;
+}
+
 // kTM = 256: the persistent workgroup b of P (the grid) takes its tiles in
-// the static order; kTM = 128: the one tile *one.
-template <bool kSwiglu, bool kGather, int kTM, bool kTails>
+// the static order (those before the split tiles, if any); kTM = 128: the one
+// tile *one; kSplit: workgroup b computes split unit b (one K range of one of
+// the last split_tiles tiles) into its fp32 plane.
+template <bool kSwiglu, bool kGather, int kTM, bool kTails, bool kSplit = false>
 __device__ __forceinline__ void pp_body(const GemmArgs &p, char *smem, const PpTile *one) {
   static_assert(kTM == 256 || kTM == 128, "tile rows");
+  static_assert(!kSplit || (kTM == 256 && !kTails), "split units are 256-row tiles");
   constexpr int kAS = 3, kBS = 2;                   // ring slots
   constexpr int kASlotBytes = kTM * kRowBytes;      // A stage: kTM rows x 64 K
   constexpr int kSlotBytes = 256 * kRowBytes;       // B stage: 32 KiB, 256 rows x 64 K
@@ -922,7 +985,7 @@ __device__ __forceinline__ void pp_body(const GemmArgs &p, char *smem, const PpT
   const int64_t P = gridDim.x;
   const int64_t b = blockIdx.x;
   const int64_t K = p.K;
-  const int S = static_cast<int>(K / kBK);  // K steps per tile (>= 3, K % 64 == 0: host)
+  int S = static_cast<int>(K / kBK);  // K steps per tile (>= 3, K % 64 == 0: host; split units: their range's)
 
   // ---- tile walker (group offsets read from memory: the ring fills the LDS;
   // rows and groups in 32 bits)
@@ -940,13 +1003,27 @@ __device__ __forceinline__ void pp_body(const GemmArgs &p, char *smem, const PpT
   group_rows(0, m_lo, m_hi);
   int mt_g = main_tiles(m_hi - m_lo);
   using Tile = PpTile;
+  // With a reduction split the static order ends where the split tiles begin.
+  int64_t split_base = INT64_MAX;
+  if (!kTails && p.split_tiles > 0) split_base = max(static_tile_count(p) - p.split_tiles, int64_t(0));
   auto find_tile = [&](int64_t round, Tile &t) -> bool {
     if constexpr (kTM == 128) {
       if (round > 0) return false;
       t = *one;
       return true;
     }
-    const int64_t L = round * P + (b % 8) * (P / 8) + b / 8;
+    int64_t L;
+    int unit = 0;
+    if constexpr (kSplit) {
+      // unit u = range * split_tiles + tile: an XCD's workgroups take neighbouring tiles of one range
+      if (round > 0) return false;
+      unit = static_cast<int>((b % 8) * (P / 8) + b / 8);
+      if (unit >= p.split_tiles * p.split_ways) return false;
+      L = split_base + unit % p.split_tiles;
+    } else {
+      L = round * P + (b % 8) * (P / 8) + b / 8;
+      if (L >= split_base) return false;
+    }
     while (g_cur < G32 && L >= tiles_before + static_cast<int64_t>(mt_g) * p.ntiles) {
       tiles_before += static_cast<int64_t>(mt_g) * p.ntiles;
       ++g_cur;
@@ -956,25 +1033,26 @@ __device__ __forceinline__ void pp_body(const GemmArgs &p, char *smem, const PpT
       }
     }
     if (g_cur >= G32) return false;
-    const uint32_t q = static_cast<uint32_t>(L - tiles_before);
-    const uint32_t ntl = static_cast<uint32_t>(p.ntiles);
-    const uint32_t per_grp = kGroupM * ntl;
-    const uint32_t full = static_cast<uint32_t>(mt_g) / kGroupM;
     uint32_t mt, nt;
-    if (q < full * per_grp) {
-      const uint32_t gq = q / per_grp, r = q - gq * per_grp;
-      nt = r / kGroupM;
-      mt = gq * kGroupM + r % kGroupM;
-    } else {
-      const uint32_t r = q - full * per_grp, gm = static_cast<uint32_t>(mt_g) - full * kGroupM;
-      nt = r / gm;
-      mt = full * kGroupM + (r - nt * gm);
-    }
+    patch_pos(static_cast<uint32_t>(L - tiles_before), static_cast<uint32_t>(p.ntiles), static_cast<uint32_t>(mt_g),
+              mt, nt);
     t.g = g_cur;
     t.row0 = m_lo + static_cast<int>(mt) * kTM;
     t.nt = nt;
     t.rows_valid = min(m_hi - t.row0, kTM);
+    t.unit = unit;
     return true;
+  };
+  // Split units: the K range [k0, k0 + 64 S) of the unit's tile (buffer bases move by k0 columns).
+  int64_t k0 = 0;
+  auto split_range = [&](const Tile &t) {
+    if constexpr (kSplit) {
+      const int r = t.unit / p.split_tiles;
+      k0 = static_cast<int64_t>(r) * p.split_steps * kBK;
+      S = r == p.split_ways - 1 ? static_cast<int>(K / kBK) - r * p.split_steps : p.split_steps;
+    } else {
+      (void)t;
+    }
   };
 
   // ---- DMA sources. This wavefront's A rows: blocks (grp * kTM / 16 + j * 4 +
@@ -1015,8 +1093,9 @@ __device__ __forceinline__ void pp_body(const GemmArgs &p, char *smem, const PpT
   int b_base = 0;
   uint32_t b_ncols = 0;  // SwiGLU: rows from a gate row to its up row (ncols), in bytes
   auto setup_a = [&](const Tile &t, bool valid) {
-    ra = kGather ? make_rsrc(p.a, valid ? static_cast<uint32_t>(p.a_src_rows * K * 2) : 0u)
-                 : make_rsrc(p.a + t.row0 * K, valid ? static_cast<uint32_t>(t.rows_valid) * row_bytes : 0u);
+    const uint32_t kb = static_cast<uint32_t>(k0) * 2u;  // split units: columns before the range
+    ra = kGather ? make_rsrc(p.a + k0, valid ? static_cast<uint32_t>(p.a_src_rows * K * 2) - kb : 0u)
+                 : make_rsrc(p.a + t.row0 * K + k0, valid ? static_cast<uint32_t>(t.rows_valid) * row_bytes - kb : 0u);
     int ln = lane;
     asm volatile("" : "+v"(ln));
 #pragma unroll
@@ -1043,7 +1122,7 @@ __device__ __forceinline__ void pp_body(const GemmArgs &p, char *smem, const PpT
   // rows and 2, 3 up rows (SwiGLU), so DMA j reads B row
   // brow(0) + 32 (j % 2) (+ ncols for j >= 2): one base plus a uniform step.
   auto setup_b = [&](const Tile &t, bool valid) {
-    rb = make_rsrc(p.w + t.g * p.N * K, valid ? static_cast<uint32_t>(p.N * K * 2) : 0u);
+    rb = make_rsrc(p.w + t.g * p.N * K + k0, valid ? static_cast<uint32_t>(p.N * K * 2) - static_cast<uint32_t>(k0) * 2u : 0u);
     const int nt = static_cast<int>(t.nt);
     int ln = lane;
     asm volatile("" : "+v"(ln));
@@ -1115,7 +1194,35 @@ __device__ __forceinline__ void pp_body(const GemmArgs &p, char *smem, const PpT
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[ks][j], fa[ks][i],
                                                              (zero && ks == 0) ? f32x4{} : acc[i][j], 0, 0, 0);
   };
+  // Split units: the fp32 accumulators to the unit's 256 x 256 plane (row-major). Plane column of a
+  // wave's block j: plain j * 16 + its 16 columns of the group's 128; SwiGLU gate blocks 0-3 at
+  // columns [0, 128), their up blocks 4-7 at the same columns + 128.
+  auto split_store = [&](const Tile &t) {
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.planes + static_cast<int64_t>(t.unit) * 65536, 65536u * 4u);
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+#pragma unroll
+    for (int i = 0; i < kMI; ++i) {
+      const uint32_t prow = static_cast<uint32_t>(wm * kWR + i * 16 + (ln & 15));
+#pragma unroll
+      for (int j = 0; j < kNI; ++j) {
+        const int pcol = kSwiglu ? (j >= kNI / 2 ? 128 : 0) + grp * 64 + (j % (kNI / 2)) * 16 + (ln >> 4) * 4
+                                 : grp * 128 + j * 16 + (ln >> 4) * 4;
+        const uint32_t off = (prow * 256u + static_cast<uint32_t>(pcol)) * 4u;
+#if defined(__HIP_DEVICE_COMPILE__)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), rp, static_cast<int>(off), 0, 0);
+#else
+        (void)off;
+        (void)rp;
+#endif
+      }
+    }
+  };
   auto epilogue = [&](const Tile &t) {
+    if constexpr (kSplit) {
+      split_store(t);
+      return;
+    }
     const uint32_t ld = static_cast<uint32_t>(p.ncols) * 2u;
     const __amdgpu_buffer_rsrc_t ro =
         make_rsrc(p.out + t.row0 * p.ncols, static_cast<uint32_t>(t.rows_valid) * ld);
@@ -1173,6 +1280,7 @@ __device__ __forceinline__ void pp_body(const GemmArgs &p, char *smem, const PpT
   // group 1), group 1's B rows of stage 0 (by group 0).
   Tile cur{}, nxt{};
   if (!find_tile(0, cur)) return;
+  split_range(cur);
   load_rows(cur, true);
   setup_a(cur, true);
   setup_b(cur, true);
@@ -1283,10 +1391,101 @@ __global__ __launch_bounds__(512) void grouped_gemm_pp_kernel(GemmArgs p) {
   }
 }
 
+// Reduction split of the last tiles (see GemmArgs): workgroup b computes unit
+// b into its fp32 plane, then split_sum_kernel adds the planes.
+template <bool kSwiglu, bool kGather>
+__global__ __launch_bounds__(512) void grouped_gemm_split_kernel(GemmArgs p) {
+  __shared__ __attribute__((aligned(1024))) char smem[kPpLdsBytes];
+  pp_body<kSwiglu, kGather, 256, false, true>(p, smem, nullptr);
+}
+
+// Block (tile, 16-row slab): each thread adds the split_ways planes of one row
+// and 16 plane columns (SwiGLU: 8 gate and the 8 matching up columns) in
+// range order, applies the epilogue (SwiGLU on the fp32 sums as the GEMM
+// epilogue does) and stores its 16 (8) bf16 outputs of the valid rows and
+// columns.
+template <bool kSwiglu>
+__global__ __launch_bounds__(256) void split_sum_kernel(GemmArgs p) {
+  PpTile t;
+  const int64_t base = max(static_tile_count(p) - p.split_tiles, int64_t(0));
+  const int tile = blockIdx.x;
+  if (!static_tile(p, base + tile, t)) return;
+  const int r = blockIdx.y * 16 + threadIdx.x / 16;
+  if (r >= t.rows_valid) return;
+  constexpr int kCols = kSwiglu ? 8 : 16;  // output columns of a thread
+  constexpr int kEpiCols = kSwiglu ? kBN / 2 : kBN;
+  const int c = (threadIdx.x % 16) * kCols;
+  const int64_t col = static_cast<int64_t>(t.nt) * kEpiCols + c;
+  if (col >= p.ncols) return;  // ncols % 8 == 0: a thread's columns are all valid or all past the end
+  float v[kCols], up[kCols];
+#pragma unroll
+  for (int q = 0; q < kCols; ++q) v[q] = up[q] = 0.0f;
+  for (int w = 0; w < p.split_ways; ++w) {
+    const float *pl = p.planes + (static_cast<int64_t>(w) * p.split_tiles + tile) * 65536 + r * 256;
+#pragma unroll
+    for (int q = 0; q < kCols; q += 4) {
+      const float4 a = *reinterpret_cast<const float4 *>(pl + c + q);
+      v[q] += a.x;
+      v[q + 1] += a.y;
+      v[q + 2] += a.z;
+      v[q + 3] += a.w;
+      if constexpr (kSwiglu) {
+        const float4 u = *reinterpret_cast<const float4 *>(pl + 128 + c + q);
+        up[q] += u.x;
+        up[q + 1] += u.y;
+        up[q + 2] += u.z;
+        up[q + 3] += u.w;
+      }
+    }
+  }
+  uint32_t o[kCols / 2];
+#pragma unroll
+  for (int q = 0; q < kCols; q += 2) {
+    float h0 = v[q], h1 = v[q + 1];
+    if constexpr (kSwiglu) {
+      h0 = h0 * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(h0 * -1.4426950408889634f)) * up[q];
+      h1 = h1 * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(h1 * -1.4426950408889634f)) * up[q + 1];
+    }
+    const bf16x2 pr = {(__bf16)h0, (__bf16)h1};
+    o[q / 2] = __builtin_bit_cast(uint32_t, pr);
+  }
+  u32x4 *dst = reinterpret_cast<u32x4 *>(p.out + static_cast<int64_t>(t.row0 + r) * p.ncols + col);
+  dst[0] = u32x4{o[0], o[1], o[2], o[3]};
+  if constexpr (!kSwiglu) {
+    if (col + 8 < p.ncols) dst[1] = u32x4{o[4], o[5], o[6], o[7]};
+  }
+}
+
 }  // namespace
 }  // namespace moe
 
 namespace {
+
+// Reduction split plan of a one-group GEMM whose 256-row tiles leave the last
+// round at most half full (e.g. 320 tiles on 256 CUs): the last `tiles` tiles
+// run as `ways` K ranges each, one unit per CU, after the other tiles.
+struct SplitPlan {
+  int tiles = 0, ways = 0, steps = 0;
+  size_t bytes = 0;  // fp32 planes
+};
+
+SplitPlan split_plan(int64_t M_total, int64_t K, int64_t N, int64_t G, int64_t cus) {
+  using namespace moe;
+  SplitPlan sp;
+  if (G != 1 || K % kBK != 0 || M_total <= 0 || N <= 0) return sp;
+  const int64_t S = K / kBK;
+  const int64_t total = ceil_div(M_total, 256) * ceil_div(N, 256);  // SwiGLU: ceil(N/2 / 128), the same
+  const int64_t P = std::max<int64_t>(8, cus / 8 * 8);
+  const int64_t L = total % P;  // tiles of the last round (all of them when total < P)
+  if (L == 0 || 2 * L > P) return sp;
+  const int64_t ways = std::min<int64_t>({P / L, S / 3, 8});
+  if (ways < 2) return sp;
+  sp.tiles = static_cast<int>(L);
+  sp.ways = static_cast<int>(ways);
+  sp.steps = static_cast<int>(S / ways);
+  sp.bytes = static_cast<size_t>(L * ways) * 65536 * sizeof(float);
+  return sp;
+}
 
 int launch_grouped_gemm(const char *fn, const moe_bf16_t *a, int64_t a_src_rows, const int32_t *a_rows,
                         int64_t M_total, int64_t K, const moe_bf16_t *w, int64_t G, int64_t N,
@@ -1348,6 +1547,40 @@ int launch_grouped_gemm(const char *fn, const moe_bf16_t *a, int64_t a_src_rows,
   // (with short reductions the 128-row tiles' start and drain measured slower
   // than the padding rows they save).
   p.tails = nullptr;
+  p.split_tiles = p.split_ways = p.split_steps = 0;
+  p.planes = nullptr;
+  // One group whose last round of tiles is sparse: with a large enough workspace, a reduction split of
+  // those tiles (the results differ from the unsplit ones only in the order of their fp32 partial sums).
+  const SplitPlan sp = pingpong ? split_plan(M_total, K, N, G, num_cus()) : SplitPlan{};
+  if (sp.tiles > 0 && workspace != nullptr && workspace_bytes >= sp.bytes && is_aligned(workspace, 256)) {
+    p.split_tiles = sp.tiles;
+    p.split_ways = sp.ways;
+    p.split_steps = sp.steps;
+    p.planes = static_cast<float *>(workspace);
+    const int64_t units = static_cast<int64_t>(sp.tiles) * sp.ways;
+    const int64_t total = ceil_div(M_total, 256) * p.ntiles;
+    if (total > sp.tiles) {
+      const int64_t g0 = std::max<int64_t>(8, std::min<int64_t>(grid, total - sp.tiles) / 8 * 8);
+      if (swiglu) {
+        if (gather) grouped_gemm_pp_kernel<true, true, false><<<dim3(g0), dim3(512), 0, s>>>(p);
+        else grouped_gemm_pp_kernel<true, false, false><<<dim3(g0), dim3(512), 0, s>>>(p);
+      } else {
+        if (gather) grouped_gemm_pp_kernel<false, true, false><<<dim3(g0), dim3(512), 0, s>>>(p);
+        else grouped_gemm_pp_kernel<false, false, false><<<dim3(g0), dim3(512), 0, s>>>(p);
+      }
+    }
+    const dim3 gu(static_cast<uint32_t>((units + 7) / 8 * 8));
+    if (swiglu) {
+      if (gather) grouped_gemm_split_kernel<true, true><<<gu, dim3(512), 0, s>>>(p);
+      else grouped_gemm_split_kernel<true, false><<<gu, dim3(512), 0, s>>>(p);
+      split_sum_kernel<true><<<dim3(sp.tiles, 16), dim3(256), 0, s>>>(p);
+    } else {
+      if (gather) grouped_gemm_split_kernel<false, true><<<gu, dim3(512), 0, s>>>(p);
+      else grouped_gemm_split_kernel<false, false><<<gu, dim3(512), 0, s>>>(p);
+      split_sum_kernel<false><<<dim3(sp.tiles, 16), dim3(256), 0, s>>>(p);
+    }
+    return check_launch(fn);
+  }
   if (pingpong && K >= kTailsMinK && workspace != nullptr && workspace_bytes >= tails_bytes(G) &&
       is_aligned(workspace, 256)) {
     p.tails = static_cast<int *>(workspace);
@@ -1392,9 +1625,10 @@ int launch_grouped_gemm(const char *fn, const moe_bf16_t *a, int64_t a_src_rows,
 extern "C" {
 
 size_t moe_grouped_gemm_workspace_size(int64_t M_total, int64_t K, int64_t N, int64_t G) {
-  (void)M_total;
-  (void)N;
-  if (G < 1 || G > 4096 || K % moe::gemm::kBK != 0 || K < moe::gemm::kTailsMinK) return 0;
+  if (G < 1 || G > 4096 || K % moe::gemm::kBK != 0 || K < 0 || N < 0 || M_total < 0) return 0;
+  const SplitPlan sp = split_plan(M_total, K, N, G, moe::gemm::num_cus());
+  if (sp.tiles > 0) return sp.bytes;
+  if (K < moe::gemm::kTailsMinK) return 0;
   return (moe::gemm::tails_bytes(G) + 255) / 256 * 256;
 }
 

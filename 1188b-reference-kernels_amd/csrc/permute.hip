@@ -352,17 +352,24 @@ __global__ __launch_bounds__(256) void permute_index_kernel(const void *map, int
   }
 }
 
-// Extent of a row-id map: max(-1, max entry) and the number of entries >= 0,
-// in one pass. Each block reduces a grid-stride share of the entries (16-byte
-// loads when kVec) into partials [2 * gridDim.x]; map_extent_final_kernel adds
-// them up in block order.
+// Extent of a row-id map: max(-1, max entry), the number of entries >= 0 and
+// whether those entries are distinct, in one pass. Each block reduces a
+// grid-stride share of the entries (16-byte loads when kVec) into partials
+// [2 * gridDim.x] and sets bit v of `bits` (zeroed by the caller, n bits) for
+// every entry v in [0, n); map_extent_final_kernel adds the partials up in
+// block order and counts the bits of [0, max]: the map names every row of
+// [0, max] exactly once iff count == max + 1 == that bit count.
 constexpr int kExtentMaxBlocks = 1024;
 template <bool kI64, bool kVec>
-__global__ __launch_bounds__(256) void map_extent_partial_kernel(const void *map, int64_t n, int64_t *partials) {
+__global__ __launch_bounds__(256) void map_extent_partial_kernel(const void *map, int64_t n, int64_t *partials,
+                                                                 uint32_t *bits) {
   int64_t mx = -1, cnt = 0;
   auto take = [&](int64_t e) {
     mx = e > mx ? e : mx;
     cnt += e >= 0;
+    if (e >= 0 && e < n) {
+      __hip_atomic_fetch_or(bits + (e >> 5), 1u << (e & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   };
   const int64_t gtid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   const int64_t gstride = static_cast<int64_t>(gridDim.x) * 256;
@@ -404,9 +411,12 @@ __global__ __launch_bounds__(256) void map_extent_partial_kernel(const void *map
   }
 }
 
-__global__ __launch_bounds__(64) void map_extent_final_kernel(const int64_t *partials, int nblocks, int64_t *out) {
+__global__ __launch_bounds__(256) void map_extent_final_kernel(const int64_t *partials, int nblocks,
+                                                               const uint32_t *bits, int64_t *out) {
+  __shared__ int64_t s_a[256 / kWave], s_b[256 / kWave];
+  const int wave = threadIdx.x / kWave;
   int64_t mx = -1, cnt = 0;
-  for (int b = threadIdx.x; b < nblocks; b += 64) {
+  for (int b = threadIdx.x; b < nblocks; b += 256) {
     mx = partials[2 * b] > mx ? partials[2 * b] : mx;
     cnt += partials[2 * b + 1];
   }
@@ -416,13 +426,45 @@ __global__ __launch_bounds__(64) void map_extent_final_kernel(const int64_t *par
     mx = omx > mx ? omx : mx;
     cnt += __shfl_xor(cnt, off);
   }
+  if (lane_id() == 0) {
+    s_a[wave] = mx;
+    s_b[wave] = cnt;
+  }
+  __syncthreads();
+  mx = s_a[0];
+  cnt = s_b[0];
+  for (int w = 1; w < 256 / kWave; ++w) {
+    mx = s_a[w] > mx ? s_a[w] : mx;
+    cnt += s_b[w];
+  }
+  __syncthreads();
+  // Distinct entries of [0, max]: only needed when the count matches.
+  int64_t pop = 0;
+  if (cnt == mx + 1 && mx >= 0) {
+    const int64_t rows = mx + 1, words = (rows + 31) / 32;
+    for (int64_t w = threadIdx.x; w < words; w += 256) {
+      uint32_t v = bits[w];
+      if (w == words - 1 && (rows & 31) != 0) v &= (1u << (rows & 31)) - 1u;
+      pop += __builtin_popcount(v);
+    }
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) pop += __shfl_xor(pop, off);
+  if (lane_id() == 0) s_a[wave] = pop;
+  __syncthreads();
   if (threadIdx.x == 0) {
+    for (int w = 1; w < 256 / kWave; ++w) pop += s_a[w];
     out[0] = mx;
     out[1] = cnt;
+    out[2] = (cnt == mx + 1 && pop == cnt) ? 1 : 0;
   }
 }
 
 int64_t map_extent_blocks(int64_t n) { return std::max<int64_t>(1, std::min<int64_t>(kExtentMaxBlocks, ceil_div(n, 256 * 16))); }
+// Workspace of moe_map_extent: the partials, then (256-byte aligned) the n-bit bitmap.
+size_t map_extent_bits_offset(int64_t n) {
+  return static_cast<size_t>((map_extent_blocks(n) * 2 * sizeof(int64_t) + 255) / 256 * 256);
+}
 
 __global__ __launch_bounds__(256) void fill_i32_kernel(int32_t *p, int64_t n, int32_t v) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
@@ -531,7 +573,7 @@ int moe_permute(const moe_bf16_t *x, int64_t T, int64_t H, const void *row_id_ma
 
 size_t moe_map_extent_workspace_size(int64_t n) {
   if (n < 0) return 0;
-  return static_cast<size_t>(moe::map_extent_blocks(n)) * 2 * sizeof(int64_t);
+  return moe::map_extent_bits_offset(n) + static_cast<size_t>(moe::ceil_div(n, 32)) * sizeof(uint32_t);
 }
 
 int moe_map_extent(const void *row_id_map, int idx_dtype, int64_t n, int64_t *out, void *workspace,
@@ -550,13 +592,19 @@ int moe_map_extent(const void *row_id_map, int idx_dtype, int64_t n, int64_t *ou
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t nb = map_extent_blocks(n);
   int64_t *partials = static_cast<int64_t *>(workspace);
+  uint32_t *bits = reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) + map_extent_bits_offset(n));
+  const int64_t words = ceil_div(n, 32);
+  if (words > 0) {
+    fill_i32_kernel<<<dim3(std::min<int64_t>(1024, ceil_div(words, 256))), dim3(256), 0, s>>>(
+        reinterpret_cast<int32_t *>(bits), words, 0);
+  }
   const bool vec = is_aligned(row_id_map, 16);
   const bool i64 = idx_dtype == MOE_IDX_I64;
-  if (i64 && vec) map_extent_partial_kernel<true, true><<<dim3(nb), dim3(256), 0, s>>>(row_id_map, n, partials);
-  else if (i64) map_extent_partial_kernel<true, false><<<dim3(nb), dim3(256), 0, s>>>(row_id_map, n, partials);
-  else if (vec) map_extent_partial_kernel<false, true><<<dim3(nb), dim3(256), 0, s>>>(row_id_map, n, partials);
-  else map_extent_partial_kernel<false, false><<<dim3(nb), dim3(256), 0, s>>>(row_id_map, n, partials);
-  map_extent_final_kernel<<<dim3(1), dim3(64), 0, s>>>(partials, static_cast<int>(nb), out);
+  if (i64 && vec) map_extent_partial_kernel<true, true><<<dim3(nb), dim3(256), 0, s>>>(row_id_map, n, partials, bits);
+  else if (i64) map_extent_partial_kernel<true, false><<<dim3(nb), dim3(256), 0, s>>>(row_id_map, n, partials, bits);
+  else if (vec) map_extent_partial_kernel<false, true><<<dim3(nb), dim3(256), 0, s>>>(row_id_map, n, partials, bits);
+  else map_extent_partial_kernel<false, false><<<dim3(nb), dim3(256), 0, s>>>(row_id_map, n, partials, bits);
+  map_extent_final_kernel<<<dim3(1), dim3(256), 0, s>>>(partials, static_cast<int>(nb), bits, out);
   return check_launch("moe_map_extent");
 }
 

@@ -194,21 +194,22 @@ def router_wgrad_tf32(grad_output: torch.Tensor, inp: torch.Tensor) -> torch.Ten
     return out
 
 
-def map_extent(row_id_map: torch.Tensor) -> tuple[int, int]:
-    """(max(-1, largest entry), number of entries >= 0) of a row-id map (any layout, int32 or int64), read back
-    to the host in one pass over the map; the scatter functions' output row count is the first + 1."""
+def map_extent(row_id_map: torch.Tensor) -> tuple[int, int, bool]:
+    """(max(-1, largest entry), number of entries >= 0, whether those entries name every row of [0, max] exactly
+    once) of a row-id map (any layout, int32 or int64), read back to the host after one pass over the map; the
+    scatter functions' output row count is the first + 1."""
     _on_gpu("row_id_map", row_id_map)
     if row_id_map.dtype not in (torch.int32, torch.int64):
         raise ValueError(f"row_id_map dtype {row_id_map.dtype}: int32 or int64 expected")
     m = row_id_map.contiguous()
     n = m.numel()
-    res = torch.empty(2, dtype=torch.int64, device=m.device)
+    res = torch.empty(3, dtype=torch.int64, device=m.device)
     nbytes = _lib.lib().moe_map_extent_workspace_size(n)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=m.device)
     call("moe_map_extent", ptr(m), MOE_IDX_I64 if m.dtype == torch.int64 else MOE_IDX_I32, n, ptr(res), ptr(ws), nbytes,
          stream_handle())
-    mx, cnt = res.tolist()
-    return int(mx), int(cnt)
+    mx, cnt, bijective = res.tolist()
+    return int(mx), int(cnt), bool(bijective)
 
 
 # ---------------------------------------------------------------- row-id map

@@ -14,8 +14,9 @@ kernels of this repository on torch's current stream:
 The stand-alone permute kernel (x -> permuted rows) is timed separately on the
 same map, after the timed steps, and reported under "standalone"; the four
 grouped GEMMs of the layer's backward (dgrad and wgrad of fc1 and fc2, on the
-same routing) and the reference backward cases at their own shapes are timed
-after that and reported under "backward", the router front end and backward
+same routing) and the reference grouped-GEMM cases (forward and backward) at
+their own shapes are timed after that and reported under "backward", the
+router front end and backward
 (router GEMM, its top-k, the reference router cases) under "router" (none of
 them is part of `value`).
 
@@ -268,7 +269,8 @@ def backward_gemms(pkg, x, row_map, offs, h, w1, w2, dev, library=False):
 
     dz [R, H] and dy1 [R, 2F] are synthetic N(0,1) gradients; xp = the permuted x.  fc2 dgrad
     dh = dz @ W2[e]; fc2 wgrad dW2[e] = dz^T h; fc1 dgrad dxp = dy1 @ W1[e]; fc1 wgrad dW1[e] = dy1^T xp.
-    Also the reference backward cases at their own shapes (uniform groups, T=4096).
+    Also the reference grouped-GEMM cases at their own shapes (uniform groups, T=4096): the backward ones,
+    and the forward ones with hipBLASLt's single torch.mm beside the one-group cases.
     """
     ops, inp = pkg.ops, pkg.inputs
     R, H = h.shape[0], x.shape[1]
@@ -309,6 +311,31 @@ def backward_gemms(pkg, x, row_map, offs, h, w1, w2, dev, library=False):
         hbm = 2 * (T * N + (G * N * K if kind == "dgrad" else T * K) + (T * K if kind == "dgrad" else G * N * K))
         cases[name.split("_")[0]] = {"ms": round(ms, 4), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2),
                                      "GB/s": round(hbm / (ms * 1e-3) / 1e9, 2), "bytes": hbm}
+        del a, b
+    # The forward reference cases at their own shapes (GB/s: x, w and out once each; with 40 groups of 102
+    # rows every weight element serves 102 rows, so one pass over w bounds case03/04). Beside the one-group
+    # cases, hipBLASLt's single torch.mm of the same product (x @ w[0].T), timed in alternation with ours
+    # (three pairs, medians: the clock drifts between consecutive measurements).
+    for name in ["case03_moe_grouped_gemm_fc1_fwd", "case04_moe_grouped_gemm_fc2_fwd",
+                 "case10_grouped_gemm_single_group_fc1_fwd", "case14_grouped_gemm_single_group_fc2_fwd"]:
+        case = getattr(pkg.cases, name)
+        a, b = case.get_inputs(dev)
+        model = case.Model()
+        T, N, K, G = case.TOKENS, case.N, case.K, case.NUM_GROUPS
+        flops, hbm = 2 * T * N * K, 2 * (T * K + G * N * K + T * N)
+        if G == 1:
+            bt = b[0].t()
+            pairs = [(_time_ms(lambda: model(a, b)), _time_ms(lambda: torch.mm(a, bt))) for _ in range(3)]
+            ms = statistics.median(p[0] for p in pairs)
+            lib_ms = statistics.median(p[1] for p in pairs)
+        else:
+            ms = _time_ms(lambda: model(a, b))
+        r = {"ms": round(ms, 4), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2),
+             "frac_of_peak": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+             "GB/s": round(hbm / (ms * 1e-3) / 1e9, 2), "bytes": hbm}
+        if G == 1:
+            r["library_mm_ms"] = round(lib_ms, 4)
+        cases[name.split("_")[0]] = r
         del a, b
     case = pkg.cases.case37_ref_musa_asm_bf16_gemm_nn_256x384
     g, w = case.make_inputs(seed=0, device=dev)

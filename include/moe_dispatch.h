@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define MOE_DISPATCH_ABI_VERSION 12
+#define MOE_DISPATCH_ABI_VERSION 13
 
 typedef uint16_t moe_bf16_t;
 
@@ -186,13 +186,19 @@ int moe_permute_index(const void *row_id_map, int idx_dtype, int map_layout, int
  * output as max(row_id_map) + 1, read back with torch
  * (kernel_cases/case21_ref_permute_with_mask_map_trans.py:64, case22...:62,
  * case30...:54; kernel_results/case17_moe_permute_with_mask_map/binding.cpp:24).
- * One pass over the n entries of a map (any layout) computes both values the
+ * One pass over the n entries of a map (any layout) computes the values the
  * scatter drop-ins need:
  *   out[0] = max(-1, largest entry)  (the output row count is out[0] + 1)
- *   out[1] = number of entries >= 0  (== out[0] + 1 when they name every row)
- * out: int64 [2] on the device, written by the last of two kernels (per-block
- * partials, then their sum in block order). Workspace:
- * moe_map_extent_workspace_size(n) bytes, 8-byte aligned. */
+ *   out[1] = number of entries >= 0
+ *   out[2] = 1 if the entries >= 0 name every row of [0, out[0]] exactly once
+ *            (out[1] == out[0] + 1 and no entry repeats), else 0: only then
+ *            does a scatter write every output row, so that the reference's
+ *            zero-initialised output (new_zeros) needs no clearing.
+ * out: int64 [3] on the device, written by the last of three kernels (a
+ * bitmap clear; per-block partials that also set one bit per entry; their
+ * sum in block order with the bit count). Workspace:
+ * moe_map_extent_workspace_size(n) bytes (the partials and an n-bit bitmap),
+ * 8-byte aligned. */
 size_t moe_map_extent_workspace_size(int64_t n);
 int moe_map_extent(const void *row_id_map, int idx_dtype, int64_t n, int64_t *out, void *workspace,
                    size_t workspace_bytes, void *stream);
@@ -250,15 +256,29 @@ int moe_index_select(const moe_bf16_t *src, int64_t src_rows, int64_t row_elems,
  *       gate = columns [0, N/2), up = [N/2, N); silu(g) = g / (1 + exp(-g)),
  *       computed in fp32 on the fp32 accumulators, then one bf16 rounding).
  * Limits: K % 8 == 0, N % 2 == 0 (SWIGLU), 1 <= G <= 4096, K < 2^22, N * K < 2^30.
- * Workspace: optional. With at least moe_grouped_gemm_workspace_size bytes
- *   (256-byte aligned), a group whose last 256-row tile would hold 1 to 128
- *   rows has that tile computed as a 128-row tile: a small kernel first lists
- *   those groups, and the GEMM's workgroups take the 128-row tiles from the
- *   list after their 256-row tiles (so the tiles also even out the last
- *   round). Every output element is summed in the same order either way: the
- *   result is the same bit for bit. NULL, 0 or a smaller size: every row tile
- *   has 256 rows. The size is 0 where the 128-row form does not apply
- *   (K % 64 != 0 or K <= 128). Calls that share a workspace must not overlap. */
+ * Workspace: optional; moe_grouped_gemm_workspace_size bytes, 256-byte
+ *   aligned. What it holds depends on the shape:
+ *   - G == 1 whose 256 x 256 output tiles leave the last round on the GPU's
+ *     CUs at most half full (e.g. case10: 320 tiles on 256 CUs), K % 64 == 0,
+ *     K >= 384: fp32 planes for a reduction split of that round's tiles. The
+ *     other tiles run as usual; each of the last ones is computed as 2 to 8
+ *     K ranges (one per CU) into its own fp32 plane, and a last kernel adds
+ *     a tile's planes in range order and rounds once. The result is
+ *     deterministic; it differs from the unsplit one only in the order of
+ *     the fp32 partial sums (both are within the fp32-accumulation bound).
+ *   - otherwise, K % 64 == 0 and K >= 4096: a group whose last 256-row tile
+ *     would hold 1 to 128 rows has that tile computed as a 128-row tile: a
+ *     small kernel first lists those groups, and the GEMM's workgroups take
+ *     the 128-row tiles from the list after their 256-row tiles (so the tiles
+ *     also even out the last round). Every output element is summed in the
+ *     same order either way: the result is the same bit for bit. With shorter
+ *     reductions a 128-row tile's start and drain cost more than the padding
+ *     rows it saves, and the size is 0.
+ *   Either is used only where the two-wavefronts-per-SIMD kernel runs (output
+ *   rows of a multiple of 16 bytes on a 16-byte aligned out, fewer than 2^22
+ *   output columns, M_total < 2^31, and M_total < 2^29 for the gather form);
+ *   a workspace is ignored elsewhere, and NULL, 0 or a smaller size runs every
+ *   tile whole with 256 rows. Calls that share a workspace must not overlap. */
 size_t moe_grouped_gemm_workspace_size(int64_t M_total, int64_t K, int64_t N, int64_t G);
 int moe_grouped_gemm(const moe_bf16_t *a, int64_t M_total, int64_t K, const moe_bf16_t *w,
                      int64_t G, int64_t N, const int32_t *group_offsets, int epilogue,

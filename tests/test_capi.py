@@ -162,8 +162,9 @@ def test_workspace_sizes():
     assert lib.moe_row_id_map_workspace_size(1 << 26, 32) <= 64 * 33 * 4 + 256
     assert lib.moe_permute_workspace_size(16384) >= 4096 * 4
     # map extent: one (max, count) int64 pair per partial block, at most 1024 blocks
-    assert lib.moe_map_extent_workspace_size(0) == 16
-    assert lib.moe_map_extent_workspace_size(320 * 16384) == 1024 * 16
+    assert lib.moe_map_extent_workspace_size(0) == 256  # partials (256-byte aligned), then the n-bit bitmap
+    assert lib.moe_map_extent_workspace_size(320 * 16384) == 1024 * 16 + 320 * 16384 // 8
+    assert lib.moe_map_extent_workspace_size(33) == 256 + 8
     assert lib.moe_map_extent_workspace_size(-1) == 0
     assert lib.moe_row_id_map_workspace_size(-1, 4) == 0
     # router: one fp32 logits plane (used when the top-k call gets no logits output)
@@ -195,6 +196,12 @@ def test_workspace_sizes():
     assert lib.moe_grouped_gemm_workspace_size(131072, 2048, 7168, 64) == 0       # c5 fc2: short reduction
     assert lib.moe_grouped_gemm_workspace_size(4096, 4100, 256, 4) == 0           # K % 64 != 0
     assert lib.moe_grouped_gemm_workspace_size(4096, 4096, 256, 0) == 0
+    # one group whose last round of 256 x 256 tiles is at most half full (256 CUs; no GPU here: the default):
+    # fp32 planes of 256 x 256 for the reduction split of those tiles
+    assert lib.moe_grouped_gemm_workspace_size(4096, 8192, 5120, 1) == 64 * 4 * 65536 * 4  # case10: 320 tiles
+    assert lib.moe_grouped_gemm_workspace_size(1000, 1024, 1000, 1) == 16 * 5 * 65536 * 4  # 16 tiles, 5 ranges
+    assert lib.moe_grouped_gemm_workspace_size(4096, 2560, 8192, 1) == 0   # case14: 512 tiles, two full rounds
+    assert lib.moe_grouped_gemm_workspace_size(4096, 8192, 5120, 2) == (4 * (64 + 2) + 255) // 256 * 256
     # router tf32 wgrad: [A_hi; A_hi; A_lo] and [B_hi; B_lo; B_hi] over 3M rows (+ fp32 planes when split)
     assert lib.moe_router_wgrad_tf32_workspace_size(4096, 64, 1000) >= 3 * 4096 * (64 + 1000) * 2
 

@@ -188,14 +188,40 @@ def test_map_extent_matches_torch(pkg, dev, dtype):
             torch.randint(-1, 3, (1,), generator=g), torch.randint(-5, 70000, (300001,), generator=g)]
     for m in maps:
         m = m.to(dtype).to(dev)
-        mx, cnt = pkg.ops.map_extent(m)
-        ref_mx = max(int(m.max()), -1) if m.numel() else -1
-        assert (mx, cnt) == (ref_mx, int((m >= 0).sum())), (tuple(m.shape), mx, cnt)
+        assert pkg.ops.map_extent(m) == _extent_ref(m), tuple(m.shape)
     base = torch.randint(-1, 50, (4097,), generator=g).to(dtype).to(dev)
     view = base[1:]  # 4 or 8 bytes past a 16-byte boundary
-    assert pkg.ops.map_extent(view) == (int(view.max()), int((view >= 0).sum()))
+    assert pkg.ops.map_extent(view) == _extent_ref(view)
     em = pkg.cases.case21_permute_with_mask_map_trans.make_row_id_map(device=dev).to(dtype)
-    assert pkg.ops.map_extent(em) == (int(em.max()), int((em >= 0).sum()))
+    assert pkg.ops.map_extent(em) == _extent_ref(em)
+    assert pkg.ops.map_extent(em)[2], "a row-id map names every row once"
+
+
+def _extent_ref(m: torch.Tensor) -> tuple[int, int, bool]:
+    """(max(-1, largest entry), count of entries >= 0, whether those entries are exactly 0 .. max)."""
+    v = m[m >= 0].cpu().long()
+    mx = int(v.max()) if v.numel() else -1
+    return mx, int(v.numel()), bool(v.numel() == mx + 1 and torch.unique(v).numel() == v.numel())
+
+
+@pytest.mark.parametrize("dtype", [torch.int64, torch.int32])
+def test_map_extent_bijective_flag(pkg, dev, dtype):
+    # The third value is set only for maps whose entries >= 0 are 0 .. max, each once: a permutation of
+    # a row-id map (any layout), but not a map whose count matches max + 1 through a repeat and a hole
+    # ({0, 0, 2}), nor one with a hole alone or a repeat alone; bits past the first 32 and in the last
+    # partial word of the bitmap are exercised by the larger maps.
+    g = torch.Generator().manual_seed(13)
+    perm = torch.randperm(5000, generator=g)
+    holed = perm.clone()
+    holed[holed == 4099] = 17  # 17 twice, 4099 missing: count still == max + 1
+    cases = [(torch.tensor([0, 0, 2, -1]), False), (torch.tensor([[0, -1], [-1, 2]]), False),
+             (torch.tensor([1, 0, 1]), False), (torch.tensor([2, -1, 0, 1]), True), (torch.full((3, 3), -1), True),
+             (perm.reshape(50, 100), True), (holed.reshape(100, 50), False), (perm[:4097], False)]
+    for m, want in cases:
+        m = m.to(dtype).to(dev)
+        got = pkg.ops.map_extent(m)
+        assert got == _extent_ref(m), (tuple(m.shape), got)
+        assert got[2] is want, (tuple(m.shape), got)
 
 
 @pytest.mark.parametrize("mod,fn,probs", [("case21_permute_with_mask_map_trans", "permute_with_mask_map_trans", False),
@@ -232,6 +258,24 @@ def test_permute_sparse_maps_zero_the_unnamed_rows(pkg, dev, mod, fn, probs):
     ref_out, ref_pp = ref_torch.permute_token_major(x, tm, pr * (tm >= 0), int(m.max()) + 1)
     assert_bits_equal(out, ref_out, "case17 sparse out")
     assert_bits_equal(pp, ref_pp, "case17 sparse pp")
+
+
+@pytest.mark.parametrize("mod,fn", [("case21_permute_with_mask_map_trans", "permute_with_mask_map_trans"),
+                                    ("case30_moe_permute_mask_kernel", "permute_mask")])
+def test_scatter_map_with_repeat_and_hole_zeroes_the_hole(pkg, dev, mod, fn):
+    # Entries {0, 0, 2}: as many as max + 1, yet row 1 is named by no entry and row 0 twice. The hole
+    # is zero, as the reference's new_zeros leaves it; row 2 is its token's row; row 0 is one of its two
+    # tokens' rows (the reference writes them in turn, kernel_cases/case21_ref_permute_with_mask_map_trans.py:60-68).
+    case = getattr(pkg.cases, mod)
+    g = torch.Generator().manual_seed(10)
+    m = torch.tensor([[0, -1, -1], [-1, 0, 2]], dtype=torch.int64)
+    inp = torch.randn(3, 72, generator=g).to(torch.bfloat16)
+    torch.empty(4 << 20, dtype=torch.uint8, device=dev).fill_(0x7F)  # stale memory would show in row 1
+    out = getattr(case, fn)(inp.to(dev), m.to(dev)).cpu()
+    assert out.shape == (3, 72)
+    assert torch.equal(out[1], torch.zeros(72, dtype=torch.bfloat16)), "the unnamed row is not zero"
+    assert torch.equal(out[2], inp[2])
+    assert torch.equal(out[0], inp[0]) or torch.equal(out[0], inp[1])
 
 
 def test_permute_known_answer_on_gpu(pkg, dev):

@@ -67,6 +67,64 @@ def test_grouped_gemm_uniform_model(pkg, dev):
     _check(out, ref_torch.grouped_gemm_fp32(x.cpu(), w.cpu(), case.group_sizes(1000, 8)), "uniform model")
 
 
+@pytest.mark.parametrize("case_name", ["case10_grouped_gemm_single_group_fc1_fwd",
+                                       "case14_grouped_gemm_single_group_fc2_fwd"])
+def test_single_group_reference_cases_full(pkg, dev, case_name):
+    # The reference's one-group forward cases at their own shapes (4096 x 8192 -> 5120 and 4096 x 2560 -> 8192,
+    # kernel_cases/case10_grouped_gemm_single_group_fc1_fwd.py:25-28, case14...:25-28), every output element
+    # against the CPU oracle, through the Model with the case's uniform sizes and through kernel_function.
+    case = getattr(pkg.cases, case_name)
+    x, w = case.get_inputs(dev)
+    assert x.shape == (case.TOKENS, case.K) and w.shape == (1, case.N, case.K)
+    out = case.Model()(x, w)
+    assert out.shape == (case.TOKENS, case.N)
+    _check(out, ref_torch.grouped_gemm_fp32(x.cpu(), w.cpu(), case.group_sizes(case.TOKENS, 1)), case_name)
+    again = case.kernel_function(x, w)
+    assert torch.equal(again.cpu(), out.cpu()), "two calls differ"
+
+
+@pytest.mark.parametrize("M,K,N,swiglu,gather,rows", [
+    (1000, 1024, 1000, False, False, 1000),   # 16 tiles: every tile split (5 ranges of 3 K steps)
+    (1000, 1024, 1040, True, False, 1000),    # SwiGLU: the sums of gate and up, then silu(g) * u
+    (1000, 1024, 1040, True, True, 1000),     # gathered A rows (fc1 of a one-expert layer)
+    (1000, 1024, 1000, False, False, 700),    # the group ends before M: rows past it untouched
+    (4100, 8192, 5120, False, False, 4100),   # 340 tiles: 256 unsplit, the last 84 in 3 ranges (a 4-row tail)
+    (300, 640, 264, False, False, 300),       # output columns not a multiple of 16
+])
+def test_single_group_reduction_split(pkg, dev, M, K, N, swiglu, gather, rows):
+    # One group whose last round of 256 x 256 tiles is at most half full: with the workspace those tiles run
+    # as K ranges into fp32 planes, added in range order. Against the CPU oracle at the task tolerance, and
+    # against the same GEMM without a workspace (no split) at the same tolerance.
+    ops = pkg.ops
+    assert pkg._lib.lib().moe_grouped_gemm_workspace_size(M, K, N, 1) >= 65536 * 4 * 2, "no split planned"
+    g = torch.Generator().manual_seed(M + K + N + rows)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(1, N, K, generator=g) * 0.05).to(torch.bfloat16)
+    offs = torch.tensor([0, rows], dtype=torch.int32, device=dev)
+    ncols = N // 2 if swiglu else N
+    out = torch.full((M + 2, ncols), 3.0, dtype=torch.bfloat16, device=dev)  # guard rows around the output
+    if gather:
+        src = torch.randperm(M, generator=g)[:M].to(torch.int32)
+        ops.grouped_gemm_gather(x.to(dev), src.to(dev), w.to(dev), offs, swiglu=swiglu, out=out[1:M + 1])
+        a = x[src.long()]
+    else:
+        ops.grouped_gemm(x.to(dev), w.to(dev), offs, swiglu=swiglu, out=out[1:M + 1])
+        a = x
+    got = out.cpu()
+    assert torch.all(got[0] == 3.0) and torch.all(got[M + 1] == 3.0), "stored outside out"
+    assert torch.all(got[1 + rows:M + 1] == 3.0), "rows past the group were written"
+    ref = ref_torch.grouped_gemm_fp32(a[:rows], w, [rows])
+    if swiglu:
+        ref = ref_torch.swiglu(ref)
+    _check(got[1:rows + 1], ref, f"split M={M} K={K} N={N} swiglu={swiglu} gather={gather} rows={rows}")
+    empty = torch.empty(0, dtype=torch.uint8, device=dev)
+    if gather:
+        plain = ops.grouped_gemm_gather(x.to(dev), src.to(dev), w.to(dev), offs, swiglu=swiglu, workspace=empty)
+    else:
+        plain = ops.grouped_gemm(x.to(dev), w.to(dev), offs, swiglu=swiglu, workspace=empty)
+    _check(got[1:rows + 1], plain[:rows], "split against unsplit")
+
+
 def _sampled_check(x, w, offs, out, swiglu, rows_per_group=48, seed=0, full_groups=()):
     """Rows of every group (all rows of the groups in full_groups, else a sample plus both
     ends) against the CPU oracle, one group at a time (x, w and out may live on the GPU)."""
