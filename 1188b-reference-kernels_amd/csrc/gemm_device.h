@@ -21,6 +21,16 @@ typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 
 constexpr int kBK = 64;  // reduction depth of one pipeline stage
 
+// Loads of data that nothing writes while the kernel runs (group offsets, the
+// lists an earlier kernel made): through the constant address space, so that a
+// wave-uniform index becomes a scalar load. A vector load would sit in the
+// wavefront's in-order vector-memory counter behind its LDS DMAs, and the wait
+// for its value would wait for all of them.
+typedef __attribute__((address_space(4))) const int32_t const_i32;
+typedef __attribute__((address_space(4))) const int16_t const_i16;
+__device__ __forceinline__ int32_t ld_inv(const int32_t *p, int64_t i) { return ((const const_i32 *)p)[i]; }
+__device__ __forceinline__ int32_t ld_inv(const int16_t *p, int64_t i) { return ((const const_i16 *)p)[i]; }
+
 // s_waitcnt immediates (gfx9 encoding: vmcnt [3:0],[15:14]; expcnt [6:4]; lgkmcnt [11:8]).
 constexpr int kWaitVm0 = 0x0f70;    // vmcnt(0)
 constexpr int kWaitLgkm0 = 0xc07f;  // lgkmcnt(0)

@@ -144,8 +144,8 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs p) {
   const bool ktail = (K % kBK) != 0;
 
   auto group_rows = [&](int64_t g, int64_t &lo, int64_t &hi) {
-    lo = min(max(static_cast<int64_t>(p.offsets[g]), int64_t(0)), p.M);
-    hi = min(max(static_cast<int64_t>(p.offsets[g + 1]), lo), p.M);
+    lo = min(max(static_cast<int64_t>(ld_inv(p.offsets, g)), int64_t(0)), p.M);
+    hi = min(max(static_cast<int64_t>(ld_inv(p.offsets, g + 1)), lo), p.M);
   };
   int64_t g_cur = 0, tiles_before = 0, m_lo, m_hi;
   group_rows(0, m_lo, m_hi);
@@ -876,8 +876,8 @@ __device__ __forceinline__ int64_t static_tile_count(const GemmArgs &p) {
   const int M32 = static_cast<int>(p.M);
   int64_t total = 0;
   for (int g = 0; g < static_cast<int>(p.G); ++g) {
-    const int lo = min(max(p.offsets[g], 0), M32);
-    const int hi = min(max(p.offsets[g + 1], lo), M32);
+    const int lo = min(max(ld_inv(p.offsets, g), 0), M32);
+    const int hi = min(max(ld_inv(p.offsets, g + 1), lo), M32);
     total += static_cast<int64_t>((hi - lo + 255) / 256) * p.ntiles;
   }
   return total;
@@ -904,8 +904,8 @@ __device__ __forceinline__ bool static_tile(const GemmArgs &p, int64_t L, PpTile
   const int M32 = static_cast<int>(p.M);
   int64_t before = 0;
   for (int g = 0; g < static_cast<int>(p.G); ++g) {
-    const int lo = min(max(p.offsets[g], 0), M32);
-    const int hi = min(max(p.offsets[g + 1], lo), M32);
+    const int lo = min(max(ld_inv(p.offsets, g), 0), M32);
+    const int hi = min(max(ld_inv(p.offsets, g + 1), lo), M32);
     const int mt_g = (hi - lo + 255) / 256;
     const int64_t n = static_cast<int64_t>(mt_g) * p.ntiles;
     if (L < before + n) {
@@ -992,8 +992,8 @@ __device__ __forceinline__ void pp_body(const GemmArgs &p, char *smem, const PpT
   const int M32 = static_cast<int>(p.M);
   const int G32 = static_cast<int>(p.G);
   auto group_rows = [&](int g, int &lo, int &hi) {
-    lo = min(max(p.offsets[g], 0), M32);
-    hi = min(max(p.offsets[g + 1], lo), M32);
+    lo = min(max(ld_inv(p.offsets, g), 0), M32);
+    hi = min(max(ld_inv(p.offsets, g + 1), lo), M32);
   };
   // 256-row tiles of a group (kTails: all but a last tile of at most 128
   // rows, which the 128-row form takes).
@@ -1380,11 +1380,11 @@ __global__ __launch_bounds__(512) void grouped_gemm_pp_kernel(GemmArgs p) {
     __syncthreads();
     const int u = __builtin_amdgcn_readfirstlane(bcast[0]);
     __syncthreads();  // every wavefront has read it before the ring is used again
-    if (u >= p.tails[kTailCount] * ntl) break;
-    const int g = p.tails[kTailList + u / ntl];
+    if (u >= ld_inv(p.tails, kTailCount) * ntl) break;
+    const int g = ld_inv(p.tails, kTailList + u / ntl);
     const int M32 = static_cast<int>(p.M);
-    const int lo = min(max(p.offsets[g], 0), M32);
-    const int hi = min(max(p.offsets[g + 1], lo), M32);
+    const int lo = min(max(ld_inv(p.offsets, g), 0), M32);
+    const int hi = min(max(ld_inv(p.offsets, g + 1), lo), M32);
     const int r = (hi - lo) % 256;
     const PpTile t{g, hi - r, static_cast<uint32_t>(u % ntl), r};
     pp_body<kSwiglu, kGather, 128, kTails>(p, smem, &t);

@@ -77,6 +77,7 @@ struct BwdArgs {
   int64_t chunk;            // rows per group when offsets is nullptr
   int64_t kchunk;           // split dgrad: reduction columns of split g = [g kchunk, (g + 1) kchunk), the last to N
   const int16_t *order;     // wgrad (kOrder): the groups in the order the tiles take them
+  const int32_t *order_rows;  // wgrad (kOrder): [2 G] the clamped row range (lo, hi) of order[i] at 2 i
   int *tails;               // dgrad ping-pong kernel: tail list (kTail* layout) or nullptr
 };
 
@@ -155,8 +156,8 @@ __global__ __launch_bounds__(256) void grouped_gemm_dgrad128_kernel(BwdArgs p) {
       hi = min(lo + p.chunk, p.M);
       return;
     }
-    lo = min(max(static_cast<int64_t>(p.offsets[g]), int64_t(0)), p.M);
-    hi = min(max(static_cast<int64_t>(p.offsets[g + 1]), lo), p.M);
+    lo = min(max(static_cast<int64_t>(ld_inv(p.offsets, g)), int64_t(0)), p.M);
+    hi = min(max(static_cast<int64_t>(ld_inv(p.offsets, g + 1)), lo), p.M);
   };
   auto row_tiles = [&](int64_t lo, int64_t hi) -> int64_t { return ceil_div(hi - lo, kBM); };
   int64_t g_cur = 0, tiles_before = 0, g_lo, g_hi;
@@ -1076,8 +1077,15 @@ __device__ __forceinline__ void bwd_pp_body(const BwdArgs &p, char *smem, const 
   const int m32 = static_cast<int>(p.M);
   const int g_count = static_cast<int>(p.G);
   auto group_range = [&](int g, int &lo, int &hi) {
-    lo = min(max(__builtin_amdgcn_readfirstlane(p.offsets[g]), 0), m32);
-    hi = min(max(__builtin_amdgcn_readfirstlane(p.offsets[g + 1]), lo), m32);
+    if constexpr (kWgrad) {
+      lo = min(max(ld_inv(p.offsets, g), 0), m32);
+      hi = min(max(ld_inv(p.offsets, g + 1), lo), m32);
+    } else {
+      // dgrad: vector loads (measured: the scalar loads' waits, which share the LDS counter, cost c5 fc2
+      // dgrad 3% where they fall after the fragment reads; the wgrad walker gains from them)
+      lo = min(max(__builtin_amdgcn_readfirstlane(p.offsets[g]), 0), m32);
+      hi = min(max(__builtin_amdgcn_readfirstlane(p.offsets[g + 1]), lo), m32);
+    }
   };
   const uint32_t ntl = static_cast<uint32_t>(p.ntiles);
   const uint32_t wg_rows = static_cast<uint32_t>(ceil_div(N, kBM));
@@ -1088,14 +1096,24 @@ __device__ __forceinline__ void bwd_pp_body(const BwdArgs &p, char *smem, const 
   };
   auto group_at = [&](int i) -> int {
     if constexpr (kOrder) {
-      return min(max(__builtin_amdgcn_readfirstlane(static_cast<int>(p.order[i])), 0), g_count - 1);
+      return min(max(ld_inv(p.order, i), 0), g_count - 1);
     } else {
       return i;
     }
   };
+  // Row range of the i-th group taken: with the order, from the ordered copy the order kernel wrote (one
+  // load level per group step instead of the order, then that group's offsets).
+  auto range_at = [&](int i, int g, int &lo, int &hi) {
+    if constexpr (kOrder) {
+      lo = min(max(ld_inv(p.order_rows, 2 * i), 0), m32);
+      hi = min(max(ld_inv(p.order_rows, 2 * i + 1), lo), m32);
+    } else {
+      group_range(g, lo, hi);
+    }
+  };
   int g_cur = 0, g_act = group_at(0), g_lo, g_hi;
   uint32_t tiles_before = 0;
-  group_range(g_act, g_lo, g_hi);
+  range_at(0, g_act, g_lo, g_hi);
   uint32_t mt_g = row_tiles(g_lo, g_hi);
   using Tile = BwdTile;
   const uint32_t P32 = static_cast<uint32_t>(P);
@@ -1115,7 +1133,7 @@ __device__ __forceinline__ void bwd_pp_body(const BwdArgs &p, char *smem, const 
       ++g_cur;
       if (g_cur < g_count) {
         g_act = group_at(g_cur);
-        group_range(g_act, g_lo, g_hi);
+        range_at(g_cur, g_act, g_lo, g_hi);
         mt_g = row_tiles(g_lo, g_hi);
       }
     }
@@ -1431,23 +1449,49 @@ void launch_pp(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
 
 // order[rank] = group, rank = the number of groups with more rows (or as many
 // and a lower index): the groups largest first, a permutation of 0..G-1 (one
-// block; group sizes clamped as the GEMM's tile walker clamps them).
-__global__ __launch_bounds__(1024) void group_order_kernel(const int32_t *offsets, int G, int64_t M, int16_t *order) {
-  __shared__ int32_t s_rows[4096];
-  for (int g = threadIdx.x; g < G; g += 1024) {
-    const int64_t lo = min(max(static_cast<int64_t>(offsets[g]), int64_t(0)), M);
-    const int64_t hi = min(max(static_cast<int64_t>(offsets[g + 1]), lo), M);
-    s_rows[g] = static_cast<int32_t>(hi - lo);
+// block; group sizes clamped as the GEMM's tile walker clamps them). A bitonic
+// sort in LDS of the keys (~rows << 32 | g), ascending, padded with all-ones
+// keys to a power of two: 78 compare-exchange stages of 2 pairs per thread at
+// G = 4096 (the rank count of every pair of groups took G^2 / 1024 compares
+// per thread).
+__global__ __launch_bounds__(1024) void group_order_kernel(const int32_t *offsets, int G, int64_t M, int16_t *order,
+                                                           int32_t *order_rows) {
+  __shared__ uint64_t s_key[4096];
+  int n = 1;
+  while (n < G) n <<= 1;
+  for (int i = threadIdx.x; i < n; i += 1024) {
+    uint64_t key = ~uint64_t(0);
+    if (i < G) {
+      const int64_t lo = min(max(static_cast<int64_t>(offsets[i]), int64_t(0)), M);
+      const int64_t hi = min(max(static_cast<int64_t>(offsets[i + 1]), lo), M);
+      key = (static_cast<uint64_t>(~static_cast<uint32_t>(hi - lo)) << 32) | static_cast<uint32_t>(i);
+    }
+    s_key[i] = key;
   }
   __syncthreads();
-  for (int g = threadIdx.x; g < G; g += 1024) {
-    const int rg = s_rows[g];
-    int rank = 0;
-    for (int h = 0; h < G; ++h) {
-      const int rh = s_rows[h];
-      rank += (rh > rg) || (rh == rg && h < g);
+  for (int k = 2; k <= n; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < n; i += 1024) {
+        const int l = i ^ j;
+        if (l > i) {
+          const uint64_t a = s_key[i], c = s_key[l];
+          const bool up = (i & k) == 0;  // ascending run
+          if ((a > c) == up) {
+            s_key[i] = c;
+            s_key[l] = a;
+          }
+        }
+      }
+      __syncthreads();
     }
-    order[rank] = static_cast<int16_t>(g);
+  }
+  for (int r = threadIdx.x; r < G; r += 1024) {
+    const int g = static_cast<int>(s_key[r] & 0xffffu);
+    const int64_t lo = min(max(static_cast<int64_t>(offsets[g]), int64_t(0)), M);
+    const int64_t hi = min(max(static_cast<int64_t>(offsets[g + 1]), lo), M);
+    order[r] = static_cast<int16_t>(g);
+    order_rows[2 * r] = static_cast<int32_t>(lo);
+    order_rows[2 * r + 1] = static_cast<int32_t>(hi);
   }
 }
 
@@ -1658,6 +1702,7 @@ int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, con
   p.chunk = 0;
   p.kchunk = 0;
   p.order = nullptr;
+  p.order_rows = nullptr;
   p.tails = nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
   // One group with few output tiles (fewer than half the CUs) and a workspace
@@ -1706,7 +1751,7 @@ int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, con
 size_t moe_grouped_gemm_wgrad_workspace_size(int64_t M_total, int64_t N, int64_t K, int64_t G) {
   (void)M_total;
   if (G < 2 || G > 4096 || N <= 0 || K <= 0) return 0;
-  return moe::align_up(static_cast<size_t>(G) * sizeof(int16_t));
+  return moe::align_up(static_cast<size_t>(G) * sizeof(int16_t)) + static_cast<size_t>(G) * 2 * sizeof(int32_t);
 }
 
 int moe_grouped_gemm_wgrad(const moe_bf16_t *dy, const moe_bf16_t *x, int64_t M_total, int64_t N, int64_t K,
@@ -1741,6 +1786,7 @@ int moe_grouped_gemm_wgrad(const moe_bf16_t *dy, const moe_bf16_t *x, int64_t M_
   p.chunk = 0;
   p.kchunk = 0;
   p.order = nullptr;
+  p.order_rows = nullptr;
   p.tails = nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t tiles = G * ceil_div(N, 256) * p.ntiles;
@@ -1748,10 +1794,14 @@ int moe_grouped_gemm_wgrad(const moe_bf16_t *dy, const moe_bf16_t *x, int64_t M_
   // group's rows: with a workspace the tiles take the groups largest first,
   // which spreads the work over the workgroups more evenly (skewed routing).
   const size_t need = moe_grouped_gemm_wgrad_workspace_size(M_total, N, K, G);
-  if (need > 0 && workspace != nullptr && workspace_bytes >= need && is_aligned(workspace, 2)) {
+  if (need > 0 && workspace != nullptr && workspace_bytes >= need && is_aligned(workspace, 4)) {
     int16_t *order = static_cast<int16_t *>(workspace);
-    group_order_kernel<<<dim3(1), dim3(1024), 0, s>>>(group_offsets, static_cast<int>(G), M_total, order);
+    int32_t *order_rows = reinterpret_cast<int32_t *>(static_cast<char *>(workspace) +
+                                                      align_up(static_cast<size_t>(G) * sizeof(int16_t)));
+    group_order_kernel<<<dim3(1), dim3(1024), 0, s>>>(group_offsets, static_cast<int>(G), M_total, order,
+                                                      order_rows);
     p.order = order;
+    p.order_rows = order_rows;
     if (MOE_GEMM_BWD_PINGPONG) {
       launch_pp<true, true>(p, tiles, s);
     } else {
@@ -1817,6 +1867,7 @@ int moe_router_dgrad_tf32(const float *grad_output, int64_t M, int64_t K, const 
   p.chunk = M;
   p.kchunk = 0;
   p.order = nullptr;
+  p.order_rows = nullptr;
   p.tails = nullptr;
   if (M <= 160 || (3 * K) % kBK != 0 || 3 * K < 3 * kBK) launch_dgrad128<1>(p, (ceil_div(M, 128) + 1) * p.ntiles, s);
   else launch_pipe<false, 1>(p, (ceil_div(M, 256) + 1) * p.ntiles, s);
@@ -1918,6 +1969,7 @@ int moe_router_wgrad_tf32(const float *grad_output, int64_t M, int64_t N, const 
   p.chunk = pl.c;
   p.kchunk = 0;
   p.order = nullptr;
+  p.order_rows = nullptr;
   p.tails = nullptr;
   launch_pipe<true, 1>(p, ceil_div(N, 256) * p.ntiles * p.G, s);
   if (split) {

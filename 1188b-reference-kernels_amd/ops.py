@@ -523,10 +523,12 @@ def grouped_gemm_dgrad(dy: torch.Tensor, w: torch.Tensor, group_offsets: torch.T
 
 
 def grouped_gemm_wgrad(dy: torch.Tensor, x: torch.Tensor, group_offsets: torch.Tensor, *,
-                       out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                       out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """dw[g] = dy[rows of g]^T @ x[rows of g] (bf16 in, fp32 accumulate, bf16 out); empty groups give zeros.
 
     dy bf16 [M, N]; x bf16 [M, K]; group_offsets int32 [G+1] on the device; returns dw bf16 [G, N, K].
+    workspace: uint8 device tensor of moe_grouped_gemm_wgrad_workspace_size bytes for the group order (largest
+    first; the same result bit for bit); allocated when None, an empty tensor runs without it.
     """
     _on_gpu("dy", dy)
     _on_gpu("x", x)
@@ -543,6 +545,11 @@ def grouped_gemm_wgrad(dy: torch.Tensor, x: torch.Tensor, group_offsets: torch.T
     out = _out(out, (G, N, K), torch.bfloat16, dy.device)
     # The group order (largest first) that balances the tiles over the workgroups for skewed group sizes.
     nbytes = _lib.lib().moe_grouped_gemm_wgrad_workspace_size(M, N, K, G)
-    ws = _ws(nbytes, dy.device)
+    if workspace is not None and workspace.numel() == 0:
+        nbytes = 0
+    if workspace is None or workspace.numel() * workspace.element_size() < nbytes:
+        ws = _ws(nbytes, dy.device)
+    else:
+        ws, nbytes = workspace, workspace.numel() * workspace.element_size()
     call("moe_grouped_gemm_wgrad", ptr(dyc), ptr(xc), M, N, K, G, ptr(oc), ptr(out), ptr(ws), nbytes, stream_handle())
     return out

@@ -339,11 +339,12 @@ int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, con
  * Limits: N % 8 == 0, K % 8 == 0, 1 <= G <= 4096, M_total * N, M_total * K and
  *   N * K < 2^30; dy, x, dw 16-byte aligned.
  * Workspace: optional. With moe_grouped_gemm_wgrad_workspace_size bytes
- *   (2-byte aligned; 2 G bytes rounded up), a first kernel lists the groups
- *   largest first and the GEMM's tiles take them in that order, dealt to the
- *   workgroups in reverse on every other round, which evens out the work per
- *   workgroup when the group sizes are skewed; each tile's result is the same
- *   bit for bit either way. The size is 0 (no order) for one group. */
+ *   (4-byte aligned; 2 G bytes rounded up to 256, then 8 G bytes), a first
+ *   kernel lists the groups largest first (int16 group ids, then each one's
+ *   int32 row range) and the GEMM's tiles take them in that order, dealt to
+ *   the workgroups in reverse on every other round, which evens out the work
+ *   per workgroup when the group sizes are skewed; each tile's result is the
+ *   same bit for bit either way. The size is 0 (no order) for one group. */
 size_t moe_grouped_gemm_wgrad_workspace_size(int64_t M_total, int64_t N, int64_t K, int64_t G);
 int moe_grouped_gemm_wgrad(const moe_bf16_t *dy, const moe_bf16_t *x, int64_t M_total, int64_t N,
                            int64_t K, int64_t G, const int32_t *group_offsets, moe_bf16_t *dw,

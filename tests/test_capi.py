@@ -185,10 +185,11 @@ def test_workspace_sizes():
     assert lib.moe_grouped_gemm_dgrad_workspace_size(288, 320, 8192, 1) == 0     # too short a reduction
     assert lib.moe_grouped_gemm_dgrad_workspace_size(288, 5128, 8192, 1) == 0    # N % 64 != 0
     # wgrad group order: one int16 per group, for two or more groups
-    assert lib.moe_grouped_gemm_wgrad_workspace_size(131072, 7168, 2048, 64) == 256    # c5 fc2: 28 x 8 tiles
-    assert lib.moe_grouped_gemm_wgrad_workspace_size(131072, 4096, 7168, 64) == 256    # c5 fc1: 16 x 28 tiles
+    # group order: int16 ids (rounded to 256 bytes), then the int32 (lo, hi) row range of each
+    assert lib.moe_grouped_gemm_wgrad_workspace_size(131072, 7168, 2048, 64) == 256 + 512   # c5 fc2: 28 x 8 tiles
+    assert lib.moe_grouped_gemm_wgrad_workspace_size(131072, 4096, 7168, 64) == 256 + 512   # c5 fc1: 16 x 28 tiles
     assert lib.moe_grouped_gemm_wgrad_workspace_size(4096, 64, 64, 1) == 0
-    assert lib.moe_grouped_gemm_wgrad_workspace_size(4096, 64, 64, 4096) == 8192
+    assert lib.moe_grouped_gemm_wgrad_workspace_size(4096, 64, 64, 4096) == 8192 + 32768
     # forward grouped GEMM: the tail list (counter, count, one int per group), for reductions of
     # at least 4096 in whole 64-column steps
     assert lib.moe_grouped_gemm_workspace_size(131072, 7168, 4096, 64) == 512     # c5 fc1: 4 * (64 + 64)

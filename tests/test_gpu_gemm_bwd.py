@@ -217,6 +217,31 @@ def test_wgrad_group_order_is_bit_identical(pkg, dev, sizes, N, K):
     _check(ordered, ref_torch.grouped_gemm_wgrad_fp32(dy.cpu(), x.cpu(), sizes), "wgrad ordered")
 
 
+@pytest.mark.parametrize("G", [1, 2, 5, 64, 1000, 4096])
+def test_wgrad_group_order_matches_stable_sort(pkg, dev, G):
+    # The workspace's group order (int16 [G]): groups by descending rows, ties by ascending index -- a
+    # CPU stable sort of the clamped group sizes (ties, empty groups and a non-power-of-two G included).
+    lib, ptr = pkg._lib.lib(), pkg._lib.ptr
+    g = torch.Generator().manual_seed(G)
+    sizes = torch.randint(0, 4, (G,), generator=g).tolist()
+    N = K = 64
+    M = sum(sizes)
+    dy = torch.randn(max(M, 1), N, generator=g).to(torch.bfloat16).to(dev)
+    x = torch.randn(max(M, 1), K, generator=g).to(torch.bfloat16).to(dev)
+    offs = _offsets(sizes, dev)
+    nbytes = lib.moe_grouped_gemm_wgrad_workspace_size(M, N, K, G)
+    if G == 1:
+        assert nbytes == 0
+        return
+    ws = torch.full((nbytes,), 0x55, dtype=torch.uint8, device=dev)
+    dw = pkg.ops.grouped_gemm_wgrad(dy[:M], x[:M], offs, workspace=ws)
+    order = ws[:2 * G].view(torch.int16).cpu().long()
+    want = sorted(range(G), key=lambda i: (-sizes[i], i))
+    assert order.tolist() == want
+    plain = pkg.ops.grouped_gemm_wgrad(dy[:M], x[:M], offs, workspace=torch.empty(0, dtype=torch.uint8, device=dev))
+    assert_bits_equal(dw, plain, "wgrad with the workspace order vs by index")
+
+
 def test_wgrad_one_row_groups_exact(pkg, dev):
     # A group of one row is the outer product dy[r] x[r]^T: exact in fp32, one rounding.
     g = torch.Generator().manual_seed(91)

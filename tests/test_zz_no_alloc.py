@@ -66,3 +66,40 @@ def test_row_id_map_noalloc_rejects_sizes_beyond_its_limits(dev):
         st = lib.moe_row_id_map_noalloc(ctypes.c_void_p(0x1000), T, E, None, None, None, None, None, 0, None)
         assert st == L.MOE_ERR_CAPACITY and needle in lib.moe_last_error().decode(), (T, E)
     assert lib.moe_row_id_map_workspace_size((1 << 31) // 4096 - 1, 4096) <= 2 << 20
+
+
+def test_row_id_map_noalloc_under_graph_capture(dev):
+    # Captured once in a graph (the call allocates nothing and records only kernels), then replayed after the
+    # mask changes in place; every replay, with eager work and a synchronisation between replays, is bit-equal
+    # to moe_row_id_map with a workspace on the same mask.
+    lib = L.lib()
+    T, E, k = 4096, 64, 8
+    mask = _mask(T, E, k, seed=1).to(dev)
+    got = _outputs(T, E, k, dev)
+    # first call outside the graph: the scratch address is looked up once per device here
+    st = lib.moe_row_id_map_noalloc(_ptr(mask), T, E, *(_ptr(t) for t in got), T * k,
+                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert st == L.MOE_OK, lib.moe_last_error().decode()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        st = lib.moe_row_id_map_noalloc(_ptr(mask), T, E, *(_ptr(t) for t in got), T * k,
+                                        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert st == L.MOE_OK, lib.moe_last_error().decode()
+    ws_bytes = lib.moe_row_id_map_workspace_size(T, E)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for rep, seed in enumerate((2, 3, 4)):
+        print(f"replay {rep}: mask seed {seed}", flush=True)
+        mask.copy_(_mask(T, E, k, seed=seed).to(dev))
+        for t in got:
+            t.fill_(-7)
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = _outputs(T, E, k, dev)
+        st = lib.moe_row_id_map(_ptr(mask), T, E, *(_ptr(t) for t in ref), T * k, _ptr(ws), ws_bytes, stream)
+        assert st == L.MOE_OK, lib.moe_last_error().decode()
+        torch.cuda.synchronize()
+        for name, g, r in zip(("expert-major", "token-major", "int32 expert-major", "offsets", "source tokens"),
+                              got, ref):
+            assert_bits_equal(g, r, f"replay {rep} {name}")
