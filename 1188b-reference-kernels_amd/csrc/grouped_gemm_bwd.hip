@@ -1158,7 +1158,9 @@ __device__ __forceinline__ void bwd_pp_body(const BwdArgs &p, char *smem, const 
     t.nt = nt;
     t.rows_valid = min((kWgrad ? static_cast<int>(N) : g_hi) - t.i0, kBM);
     const int red = kWgrad ? g_hi - g_lo : static_cast<int>(N);
-    t.ktiles = max((red + kBK - 1) / kBK, 3);
+    // Two stages suffice for the ring (a tile's stages s + 2 and s + 1 + grp cross into the next tile);
+    // dgrad reductions have at least three (host).
+    t.ktiles = max((red + kBK - 1) / kBK, 2);
     return true;
   };
 
