@@ -192,6 +192,148 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(RouterArgs p) {
   }
 }
 
+// Router GEMM for 128 < N <= 512 with K % 64 == 0 (case38: N = 320): one
+// workgroup of 4 wavefronts per 128-row x 32 kNB-column tile (kNB = ceil(N /
+// 64), so two column tiles cover N: each CU streams half the weight, where the
+// 64-row tiles above stream all of it for half the rows). Consecutive tiles are
+// the two column halves of one row tile, and an XCD takes a contiguous run of
+// tiles, so the input rows are fetched once into that XCD's L2 for both halves
+// (the weight, 5.2 MB at case38, comes from the Infinity Cache). Wavefront w computes
+// rows (w / 2) 64 .. + 63, columns (w % 2) 16 kNB .. as 4 x kNB blocks of
+// v_mfma_f32_16x16x32_bf16. Fragments of the two 32-deep halves of a step are
+// double-buffered in registers: each half's MFMAs run while the other half's
+// fragments are read, and the step's DMAs (4 + kNB per wavefront, 4 stages
+// ahead) are spread among the first half's MFMAs; one barrier per step. fp32
+// results are stored from the accumulators (a lane holds 4 consecutive columns
+// of one row).
+template <int kNB>
+__global__ __launch_bounds__(256) void router_tile_kernel(RouterArgs p, int tiles) {
+  constexpr int kTM = 128;
+  constexpr int kTN = 32 * kNB;                  // columns per tile
+  constexpr int kABytes = kTM * kRow;            // 16 KiB
+  constexpr int kBBytes = kTN * kRow;
+  constexpr int kStageBytes = kABytes + kBBytes;
+  constexpr int kSt = 4 * kStageBytes <= 160 * 1024 ? 4 : 3;
+  constexpr int kDmaA = kABytes / 1024 / 4, kDmaB = kBBytes / 1024 / 4;
+  constexpr int kDma = kDmaA + kDmaB;            // DMA instructions per wavefront per stage
+  constexpr int kReads = 4 + kNB;                // fragment reads per wavefront per half step
+  static_assert(kSt * kStageBytes <= 160 * 1024, "LDS budget");
+  static_assert((kSt - 1) * kDma <= 63, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) char smem[kSt * kStageBytes];
+  lds_char *const sbase = (lds_char *)smem;
+  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sbase));
+
+  const int64_t P = gridDim.x, b = blockIdx.x;
+  const int tile = static_cast<int>((b % 8) * (P / 8) + b / 8);
+  if (tile >= tiles) return;
+  const int rt = tile >> 1, ct = tile & 1;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave >> 1, wc = wave & 1;
+  const int64_t K = p.K;
+  const int N = p.N;
+  const int64_t row0 = static_cast<int64_t>(rt) * kTM;
+  const int col0 = ct * kTN;
+  const int rows_valid = static_cast<int>(min(p.M - row0, int64_t(kTM)));
+  const int cols_valid = min(N - col0, kTN);
+  const int ktiles = static_cast<int>(K / kBK);
+
+  // Rows past the tile's valid rows / columns lie past the resources: zeros.
+  const uint32_t row_bytes = static_cast<uint32_t>(K) * 2u;
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.inp + row0 * K, static_cast<uint32_t>(rows_valid) * row_bytes);
+  const __amdgpu_buffer_rsrc_t rb =
+      make_rsrc(p.w + static_cast<int64_t>(col0) * K, static_cast<uint32_t>(cols_valid) * row_bytes);
+  int a_off[kDmaA], b_off[kDmaB];
+#pragma unroll
+  for (int j = 0; j < kDmaA; ++j) {
+    const int r = (j * 4 + wave) * 8 + (lane >> 3);
+    a_off[j] = static_cast<int>(static_cast<uint32_t>(r) * row_bytes + (((lane & 7) ^ swz(r)) << 4));
+  }
+#pragma unroll
+  for (int j = 0; j < kDmaB; ++j) {
+    const int r = (j * 4 + wave) * 8 + (lane >> 3);
+    b_off[j] = static_cast<int>(static_cast<uint32_t>(r) * row_bytes + (((lane & 7) ^ swz(r)) << 4));
+  }
+  auto issue = [&](int kt, int slot) {
+    const uint32_t st = lds_base + (slot % kSt) * kStageBytes;
+    const int soff = kt * kBK * 2;
+#pragma unroll
+    for (int j = 0; j < kDmaA; ++j) dma16b(ra, (lds_void *)(uintptr_t)(st + (j * 4 + wave) * 1024), a_off[j], soff);
+#pragma unroll
+    for (int j = 0; j < kDmaB; ++j)
+      dma16b(rb, (lds_void *)(uintptr_t)(st + kABytes + (j * 4 + wave) * 1024), b_off[j], soff);
+  };
+  const int frow = lane & 15, fq = lane >> 4;
+  auto frag_addr = [&](uint32_t slot_base, int r, int ks) {
+    return slot_base + r * kRow + ((((ks << 2) | fq) ^ swz(r)) << 4);
+  };
+  bf16x8 fa[2][4], fb[2][kNB];
+  auto read_half = [&](int kt, int ks, int buf) {
+    const uint32_t sb = lds_base + (kt % kSt) * kStageBytes;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      fa[buf][i] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)frag_addr(sb, wr * 64 + i * 16 + frow, ks));
+#pragma unroll
+    for (int j = 0; j < kNB; ++j)
+      fb[buf][j] = *reinterpret_cast<const lds_bf16x8 *>(
+          (uintptr_t)frag_addr(sb + kABytes, wc * 16 * kNB + j * 16 + frow, ks));
+  };
+  f32x4 acc[4][kNB];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < kNB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto mfma_half = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < kNB; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[buf][j], fa[buf][i], acc[i][j], 0, 0, 0);
+  };
+
+  // Prologue: stages 0 .. kSt - 2 (stages past the last re-read it, which keeps the count of outstanding
+  // DMAs the same in every step; they land in slots nothing reads any more).
+#pragma unroll
+  for (int st = 0; st < kSt - 1; ++st) issue(min(st, ktiles - 1), st);
+  wait_vm_n<(kSt - 2) * kDma>();
+  barrier();
+  read_half(0, 0, 0);
+  for (int kt = 0; kt < ktiles; ++kt) {
+    // First half: read the second half's fragments of this stage, DMA stage kt + kSt - 1 into the slot
+    // of stage kt - 1 (every wavefront finished reading it before the previous step's barrier), multiply
+    // the first half.
+    read_half(kt, 1, 1);
+    issue(min(kt + kSt - 1, ktiles - 1), kt + kSt - 1);
+    mfma_half(0);
+    sched_mix<4 * kNB, kReads, kDma>();
+    __builtin_amdgcn_sched_barrier(0);
+    // Stage kt + 1 has landed (younger: the DMAs of stages kt + 2 .. kt + kSt - 1), and every wavefront's
+    // reads of stage kt are done.
+    wait_vm_n<(kSt - 2) * kDma>();
+    wait_lds();
+    barrier();
+    if (kt + 1 < ktiles) read_half(kt + 1, 0, 0);
+    mfma_half(1);
+    sched_mix<4 * kNB, kReads, 0>();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  wait_dma();  // the re-reads of the last steps
+
+  // acc[i][j] register r of lane l: row wr 64 + i 16 + l % 16, column wc 16 kNB + j 16 + 4 (l / 16) + r.
+  float *out = p.out;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = wr * 64 + i * 16 + frow;
+    if (r >= rows_valid) continue;
+#pragma unroll
+    for (int j = 0; j < kNB; ++j) {
+      const int c = wc * 16 * kNB + j * 16 + fq * 4;
+      if (c < cols_valid) *reinterpret_cast<f32x4 *>(out + (row0 + r) * N + col0 + c) = acc[i][j];
+    }
+  }
+}
+
 // Top-k pass, one wavefront per row of the logits (topk_device.h).
 struct TopkArgs {
   const float *logits;
@@ -253,7 +395,21 @@ int launch(const char *fn, const moe_bf16_t *inp, int64_t M, int64_t K, const mo
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t grid = ceil_div(M, kBM);
   const int nb = static_cast<int>(ceil_div(N, 64));
-  switch (nb) {
+  // 128 < N with whole 64-column steps and 16-byte output rows: 128-row tiles over half of N each.
+  const bool tiled = N > 128 && K % kBK == 0 && p.vec_out && ceil_div(M, 128) * 2 <= 0x7fffffff;
+  if (tiled) {
+    const int row_tiles = static_cast<int>(ceil_div(M, 128));
+    const int tiles = row_tiles * 2;
+    const dim3 g(static_cast<uint32_t>((tiles + 7) / 8 * 8));
+    switch (nb) {
+      case 3: router_tile_kernel<3><<<g, dim3(256), 0, s>>>(p, tiles); break;
+      case 4: router_tile_kernel<4><<<g, dim3(256), 0, s>>>(p, tiles); break;
+      case 5: router_tile_kernel<5><<<g, dim3(256), 0, s>>>(p, tiles); break;
+      case 6: router_tile_kernel<6><<<g, dim3(256), 0, s>>>(p, tiles); break;
+      case 7: router_tile_kernel<7><<<g, dim3(256), 0, s>>>(p, tiles); break;
+      default: router_tile_kernel<8><<<g, dim3(256), 0, s>>>(p, tiles); break;
+    }
+  } else switch (nb) {
     case 1: router_gemm_kernel<1><<<dim3(grid), dim3(256), 0, s>>>(p); break;
     case 2: router_gemm_kernel<2><<<dim3(grid), dim3(256), 0, s>>>(p); break;
     case 3: router_gemm_kernel<3><<<dim3(grid), dim3(256), 0, s>>>(p); break;
