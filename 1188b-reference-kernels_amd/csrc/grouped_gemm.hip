@@ -1461,6 +1461,15 @@ __global__ __launch_bounds__(256) void split_sum_kernel(GemmArgs p) {
 
 namespace {
 
+// The tail list applies with long reductions (K >= 4096: c5 fc1 2.4% faster),
+// and with short ones where the groups average fewer than 256 rows, i.e. most
+// of their rows lie in a tail (case04, 40 groups of 102 rows, K = 2560: 8%
+// faster); with short reductions and long groups the 128-row tiles' start and
+// drain cost more than the padding they save (c5 fc2: 1.2-2.4% slower).
+bool tails_apply(int64_t M_total, int64_t K, int64_t G) {
+  return K % moe::gemm::kBK == 0 && (K >= moe::gemm::kTailsMinK || M_total < 256 * G);
+}
+
 // Reduction split plan of a one-group GEMM whose 256-row tiles leave the last
 // round at most half full (e.g. 320 tiles on 256 CUs): the last `tiles` tiles
 // run as `ways` K ranges each, one unit per CU, after the other tiles.
@@ -1581,7 +1590,7 @@ int launch_grouped_gemm(const char *fn, const moe_bf16_t *a, int64_t a_src_rows,
     }
     return check_launch(fn);
   }
-  if (pingpong && K >= kTailsMinK && workspace != nullptr && workspace_bytes >= tails_bytes(G) &&
+  if (pingpong && tails_apply(M_total, K, G) && workspace != nullptr && workspace_bytes >= tails_bytes(G) &&
       is_aligned(workspace, 256)) {
     p.tails = static_cast<int *>(workspace);
     tails_init_kernel<<<dim3(1), dim3(256), 0, s>>>(p.offsets, p.G, p.M, p.tails);
@@ -1628,7 +1637,7 @@ size_t moe_grouped_gemm_workspace_size(int64_t M_total, int64_t K, int64_t N, in
   if (G < 1 || G > 4096 || K % moe::gemm::kBK != 0 || K < 0 || N < 0 || M_total < 0) return 0;
   const SplitPlan sp = split_plan(M_total, K, N, G, moe::gemm::num_cus());
   if (sp.tiles > 0) return sp.bytes;
-  if (K < moe::gemm::kTailsMinK) return 0;
+  if (!tails_apply(M_total, K, G)) return 0;
   return (moe::gemm::tails_bytes(G) + 255) / 256 * 256;
 }
 

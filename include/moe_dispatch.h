@@ -266,14 +266,15 @@ int moe_index_select(const moe_bf16_t *src, int64_t src_rows, int64_t row_elems,
  *     a tile's planes in range order and rounds once. The result is
  *     deterministic; it differs from the unsplit one only in the order of
  *     the fp32 partial sums (both are within the fp32-accumulation bound).
- *   - otherwise, K % 64 == 0 and K >= 4096: a group whose last 256-row tile
+ *   - otherwise, K % 64 == 0 and either K >= 4096 or M_total < 256 G (the
+ *     groups average fewer than 256 rows): a group whose last 256-row tile
  *     would hold 1 to 128 rows has that tile computed as a 128-row tile: a
  *     small kernel first lists those groups, and the GEMM's workgroups take
  *     the 128-row tiles from the list after their 256-row tiles (so the tiles
  *     also even out the last round). Every output element is summed in the
  *     same order either way: the result is the same bit for bit. With shorter
- *     reductions a 128-row tile's start and drain cost more than the padding
- *     rows it saves, and the size is 0.
+ *     reductions and longer groups a 128-row tile's start and drain cost more
+ *     than the padding rows it saves, and the size is 0.
  *   Either is used only where the two-wavefronts-per-SIMD kernel runs (output
  *   rows of a multiple of 16 bytes on a 16-byte aligned out, fewer than 2^22
  *   output columns, M_total < 2^31, and M_total < 2^29 for the gather form);

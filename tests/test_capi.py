@@ -195,6 +195,7 @@ def test_workspace_sizes():
     assert lib.moe_grouped_gemm_workspace_size(131072, 7168, 4096, 64) == 512     # c5 fc1: 4 * (64 + 64)
     assert lib.moe_grouped_gemm_workspace_size(131072, 7168, 4096, 4096) == (4 * (64 + 4096) + 255) // 256 * 256
     assert lib.moe_grouped_gemm_workspace_size(131072, 2048, 7168, 64) == 0       # c5 fc2: short reduction
+    assert lib.moe_grouped_gemm_workspace_size(4096, 2560, 8192, 40) == 512        # case04: 102 rows per group
     assert lib.moe_grouped_gemm_workspace_size(4096, 4100, 256, 4) == 0           # K % 64 != 0
     assert lib.moe_grouped_gemm_workspace_size(4096, 4096, 256, 0) == 0
     # one group whose last round of 256 x 256 tiles is at most half full (256 CUs; no GPU here: the default):

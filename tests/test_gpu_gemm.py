@@ -228,6 +228,8 @@ def test_pipelined_kernel_matches_drained_kernel(pkg, dev, sizes, K, N, swiglu, 
     ([3, 0, 70, 2000, 128, 4097], 7168, 4096, True, False),       # fc1 class, K of the benchmark
     ([40] * 200 + [300] * 20, 4096, 256, False, True),            # many 128-row tiles: several per workgroup
     ([1] * 64, 4096, 8, False, False),                            # tails only, one partial column tile
+    ([102] * 39 + [118], 2560, 1024, False, False),               # short reduction, groups under 256 rows (case04)
+    ([90, 0, 300, 17] * 5, 448, 512, True, True),                 # short reduction, 101 rows per group on average
 ])
 def test_tail_tiles_match_full_tiles(pkg, dev, sizes, K, N, swiglu, gather):
     """With its workspace the forward GEMM computes a group's last row tile of 1 to 128 rows as a
