@@ -389,6 +389,11 @@ def router_section(pkg, x, dev):
     return out
 
 
+def _progress(msg: str) -> None:
+    """One line on stderr per finished section (stdout carries only the JSON result)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def _median_ms(fn, flush, reps=50, warm=25):
     """Median device time of fn over `reps` calls after `warm` calls; 1 GiB is overwritten before each
     timed call so no input is served from the 256 MB Infinity Cache."""
@@ -679,6 +684,7 @@ def main():
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1e3 / args.steps
     tokens_per_s = T / (elapsed / args.steps)
+    _progress(f"{args.steps} timed steps: {ms_per_step:.3f} ms per step")
 
     work = stage_work(T, H, F, E, k)
     stages = {}
@@ -738,8 +744,11 @@ def main():
         maps = ops.row_id_map(mask, expert_major=False, token_major=True, expert_offsets=True, workspace=b["ws"])
         backward = backward_gemms(pkg, x, maps["token_major"], maps["expert_offsets"], b["h"], w1, w2, dev,
                                   library=args.library_reference)
+        _progress("backward GEMMs and reference GEMM cases done")
 
     router = None if args.no_router else router_section(pkg, x, dev)
+    if router is not None:
+        _progress("router section done")
 
     library = None
     if args.library_reference:
@@ -748,6 +757,7 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(pkg, x, logits, w1, w2, k)
+        _progress("CPU baseline done")
 
     line = {
         "metric": METRIC, "value": round(tokens_per_s, 1), "unit": "tokens/s", "n_gpus": 1,
