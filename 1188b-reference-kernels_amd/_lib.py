@@ -113,6 +113,28 @@ def lib() -> ctypes.CDLL:
     return _LIB
 
 
+PROBES_PATH = PKG_DIR / "libmoe_probes.so"
+_PROBES = None
+
+
+def probes() -> ctypes.CDLL:
+    """The measurement probes (include/moe_probes.h: moe_probe_mfma, moe_probe_stream), a library of their own
+    that takes its status functions from libmoe_dispatch.so (loaded first); used by bench.py --ceilings."""
+    global _PROBES
+    if _PROBES is None:
+        lib()
+        if not PROBES_PATH.exists():
+            raise RuntimeError(f"{PROBES_PATH} is not built: run `python -c 'import __graft_entry__ as g; g.build()'`")
+        handle = ctypes.CDLL(str(PROBES_PATH), mode=os.RTLD_NOW | os.RTLD_LOCAL)
+        P, I64 = ctypes.c_void_p, ctypes.c_int64
+        handle.moe_probe_mfma.restype = ctypes.c_int
+        handle.moe_probe_mfma.argtypes = [I64, I64, P, P]
+        handle.moe_probe_stream.restype = ctypes.c_int
+        handle.moe_probe_stream.argtypes = [ctypes.c_int, P, P, I64, I64, P]
+        _PROBES = handle
+    return _PROBES
+
+
 def call(name: str, *args) -> None:
     """Calls C ABI function `name`; raises MoeError on a non-zero status."""
     status = getattr(lib(), name)(*args)

@@ -4,7 +4,10 @@
     python -c "import __graft_entry__ as g; g.build()"   # from the repo root
 
 Each .hip file compiles to an object under csrc/_build/ (in parallel), then the
-objects link into <package>/libmoe_dispatch.so next to the Python loader.
+objects link into <package>/libmoe_dispatch.so next to the Python loader. The
+measurement probes (probes.hip: bench.py --ceilings) link into a library of
+their own, <package>/libmoe_probes.so, which takes the status functions from
+libmoe_dispatch.so.
 """
 from __future__ import annotations
 
@@ -19,6 +22,7 @@ CSRC = Path(__file__).resolve().parent
 PKG = CSRC.parent
 REPO = PKG.parent
 LIB = PKG / "libmoe_dispatch.so"
+PROBE_LIB = PKG / "libmoe_probes.so"
 BUILD = CSRC / "_build"
 
 SOURCES = [
@@ -32,8 +36,8 @@ SOURCES = [
     "grouped_gemm_bwd.hip",
     "router.hip",
     "cast.hip",
-    "probes.hip",
 ]
+PROBE_SOURCES = ["probes.hip"]
 
 ARCH = os.environ.get("MOE_OFFLOAD_ARCH", "gfx950")
 
@@ -75,18 +79,25 @@ def _compile(src: str, hipcc: str) -> Path:
 def build(jobs: int | None = None) -> Path:
     hipcc = _hipcc()
     BUILD.mkdir(exist_ok=True)
-    jobs = jobs or min(len(SOURCES), max(1, (os.cpu_count() or 4)))
+    every = SOURCES + PROBE_SOURCES
+    jobs = jobs or min(len(every), max(1, (os.cpu_count() or 4)))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(s, hipcc), SOURCES))
-    tmp = LIB.with_suffix(".so.tmp")
+        objs = dict(zip(every, ex.map(lambda s: _compile(s, hipcc), every)))
     # --no-undefined: a kernel whose host launch stub was not emitted fails here, not at load time.
+    _link(hipcc, LIB, [objs[s] for s in SOURCES], [])
+    _link(hipcc, PROBE_LIB, [objs[s] for s in PROBE_SOURCES],
+          [f"-L{PKG}", f"-l:{LIB.name}", "-Wl,-rpath,$ORIGIN"])
+    return LIB
+
+
+def _link(hipcc: str, out: Path, objs: list, extra: list) -> None:
+    tmp = out.with_suffix(".so.tmp")
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", str(tmp),
-           *map(str, objs)]
+           *map(str, objs), *extra]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, out)
 
 
 if __name__ == "__main__":

@@ -13,7 +13,7 @@ import subprocess
 import sys
 from pathlib import Path
 
-from build import ARCH, COMMON_FLAGS, CSRC, SOURCES, _hipcc
+from build import ARCH, COMMON_FLAGS, CSRC, PROBE_SOURCES, SOURCES, _hipcc
 
 
 def usage(src: str, hipcc: str) -> list[tuple[str, dict]]:
@@ -43,7 +43,7 @@ def demangle(names: list[str]) -> list[str]:
 
 def main(argv: list[str]) -> int:
     hipcc = _hipcc()
-    srcs = argv or SOURCES
+    srcs = argv or SOURCES + PROBE_SOURCES
     print(f"| source | kernel ({ARCH}) | VGPR | AGPR | scratch B/lane | waves/SIMD |")
     print("|---|---|---|---|---|---|")
     bad = 0

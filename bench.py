@@ -169,10 +169,7 @@ def ceilings(pkg, dev):
     clock the c5 GEMMs (and hipBLASLt on the fc1 shape) run at.  One JSON line."""
     import ctypes
 
-    lib = pkg._lib.lib()
-    P, I64 = ctypes.c_void_p, ctypes.c_int64
-    lib.moe_probe_mfma.argtypes = [I64, I64, P, P]
-    lib.moe_probe_stream.argtypes = [ctypes.c_int, P, P, I64, I64, P]
+    lib = pkg._lib.probes()
     s = torch.cuda.current_stream().cuda_stream
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     pc = _PowerClock()

@@ -1,10 +1,12 @@
 /*
- * moe_probes.h -- measurement probes in libmoe_dispatch.so (gfx950).
+ * moe_probes.h -- measurement probes in libmoe_probes.so (gfx950).
  *
  * Not part of the dispatch path and no counterpart in the reference: small
  * kernels that measure, on the GPU at hand, the ceilings the dispatch kernels'
- * roofline fractions are read against (bench.py --ceilings).  Same conventions
- * as moe_dispatch.h (status codes, moe_last_error(), `void *stream`).
+ * roofline fractions are read against (bench.py --ceilings).  A library of
+ * their own, kept out of libmoe_dispatch.so; it links libmoe_dispatch.so for
+ * the status functions, so the conventions are those of moe_dispatch.h
+ * (status codes, moe_last_error() of libmoe_dispatch.so, `void *stream`).
  */
 #ifndef MOE_PROBES_H_
 #define MOE_PROBES_H_

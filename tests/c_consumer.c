@@ -1,5 +1,5 @@
 /* A plain C99 consumer of the C ABI: includes both public headers, links
- * libmoe_dispatch.so and calls entry points whose argument checks fail before
+ * libmoe_dispatch.so (and libmoe_probes.so for the probes) and calls entry points whose argument checks fail before
  * any HIP call (no GPU needed). Prints one line per check; exit status 0 when
  * every call returned what the header documents. */
 #include <stdint.h>

@@ -235,14 +235,14 @@ def test_inputs_generators_cpu():
 
 
 def test_probe_entry_points_validate_before_launch():
-    # measurement probes (include/moe_probes.h): exported, and bad arguments fail on the host
-    lib = L.lib()
-    P, I64 = ctypes.c_void_p, ctypes.c_int64
-    lib.moe_probe_mfma.argtypes = [I64, I64, P, P]
-    lib.moe_probe_stream.argtypes = [ctypes.c_int, P, P, I64, I64, P]
+    # measurement probes (include/moe_probes.h, in libmoe_probes.so): exported, and bad arguments fail on the
+    # host with the status (and the message) of libmoe_dispatch.so's status functions
+    lib = L.probes()
+    assert not hasattr(L.lib(), "moe_probe_mfma"), "the probes are not in the product library"
     assert lib.moe_probe_mfma(6, 10, FAKE, None) == L.MOE_ERR_SHAPE
     assert lib.moe_probe_mfma(8, 10, None, None) == L.MOE_ERR_INVALID_ARG
     assert lib.moe_probe_stream(3, FAKE, FAKE, 16, 1, None) == L.MOE_ERR_INVALID_ARG
     assert lib.moe_probe_stream(7, FAKE, FAKE, 16, 1, None) == L.MOE_ERR_INVALID_ARG
     assert lib.moe_probe_stream(0, None, FAKE, 16, 1, None) == L.MOE_ERR_INVALID_ARG
     assert lib.moe_probe_stream(2, None, ctypes.c_void_p(0x1004), 16, 1, None) == L.MOE_ERR_ALIGN
+    assert b"moe_probe_stream" in L.lib().moe_last_error()
