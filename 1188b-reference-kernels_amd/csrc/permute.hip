@@ -355,21 +355,21 @@ __global__ __launch_bounds__(256) void permute_index_kernel(const void *map, int
 // Extent of a row-id map: max(-1, max entry), the number of entries >= 0 and
 // whether those entries are distinct, in one pass. Each block reduces a
 // grid-stride share of the entries (16-byte loads when kVec) into partials
-// [2 * gridDim.x] and sets bit v of `bits` (zeroed by the caller, n bits) for
-// every entry v in [0, n); map_extent_final_kernel adds the partials up in
-// block order and counts the bits of [0, max]: the map names every row of
-// [0, max] exactly once iff count == max + 1 == that bit count.
+// [2 * gridDim.x] and sets byte v of `seen` (zeroed by the caller, n bytes) to
+// 1 for every entry v in [0, n) with a plain byte store (an entry named twice
+// writes the same value twice: no atomics, whose contention on a bitmap cost
+// more than the pass); map_extent_final_kernel adds the partials up in block
+// order and counts the set bytes of [0, max]: the map names every row of
+// [0, max] exactly once iff count == max + 1 == that byte count.
 constexpr int kExtentMaxBlocks = 1024;
 template <bool kI64, bool kVec>
 __global__ __launch_bounds__(256) void map_extent_partial_kernel(const void *map, int64_t n, int64_t *partials,
-                                                                 uint32_t *bits) {
+                                                                 uint8_t *seen) {
   int64_t mx = -1, cnt = 0;
   auto take = [&](int64_t e) {
     mx = e > mx ? e : mx;
     cnt += e >= 0;
-    if (e >= 0 && e < n) {
-      __hip_atomic_fetch_or(bits + (e >> 5), 1u << (e & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (e >= 0 && e < n) seen[e] = 1;
   };
   const int64_t gtid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   const int64_t gstride = static_cast<int64_t>(gridDim.x) * 256;
@@ -411,12 +411,13 @@ __global__ __launch_bounds__(256) void map_extent_partial_kernel(const void *map
   }
 }
 
-__global__ __launch_bounds__(256) void map_extent_final_kernel(const int64_t *partials, int nblocks,
-                                                               const uint32_t *bits, int64_t *out) {
-  __shared__ int64_t s_a[256 / kWave], s_b[256 / kWave];
+constexpr int kExtentFinal = 1024;  // threads of the final kernel (the sum over the row marks)
+__global__ __launch_bounds__(kExtentFinal) void map_extent_final_kernel(const int64_t *partials, int nblocks,
+                                                               const uint8_t *seen, int64_t *out) {
+  __shared__ int64_t s_a[kExtentFinal / kWave], s_b[kExtentFinal / kWave];
   const int wave = threadIdx.x / kWave;
   int64_t mx = -1, cnt = 0;
-  for (int b = threadIdx.x; b < nblocks; b += 256) {
+  for (int b = threadIdx.x; b < nblocks; b += kExtentFinal) {
     mx = partials[2 * b] > mx ? partials[2 * b] : mx;
     cnt += partials[2 * b + 1];
   }
@@ -433,27 +434,28 @@ __global__ __launch_bounds__(256) void map_extent_final_kernel(const int64_t *pa
   __syncthreads();
   mx = s_a[0];
   cnt = s_b[0];
-  for (int w = 1; w < 256 / kWave; ++w) {
+  for (int w = 1; w < kExtentFinal / kWave; ++w) {
     mx = s_a[w] > mx ? s_a[w] : mx;
     cnt += s_b[w];
   }
   __syncthreads();
-  // Distinct entries of [0, max]: only needed when the count matches.
+  // Distinct entries of [0, max]: only needed when the count matches (the bytes are 0 or 1; 16 at a time
+  // where the buffer's alignment allows, which the workspace layout gives).
   int64_t pop = 0;
   if (cnt == mx + 1 && mx >= 0) {
-    const int64_t rows = mx + 1, words = (rows + 31) / 32;
-    for (int64_t w = threadIdx.x; w < words; w += 256) {
-      uint32_t v = bits[w];
-      if (w == words - 1 && (rows & 31) != 0) v &= (1u << (rows & 31)) - 1u;
-      pop += __builtin_popcount(v);
+    const int64_t rows = mx + 1, nvec = rows / 16;
+    for (int64_t i = threadIdx.x; i < nvec; i += kExtentFinal) {
+      const u32x4 q = reinterpret_cast<const u32x4 *>(seen)[i];
+      pop += __builtin_popcount(q.x) + __builtin_popcount(q.y) + __builtin_popcount(q.z) + __builtin_popcount(q.w);
     }
+    for (int64_t i = nvec * 16 + threadIdx.x; i < rows; i += kExtentFinal) pop += seen[i];
   }
 #pragma unroll
   for (int off = kWave / 2; off > 0; off >>= 1) pop += __shfl_xor(pop, off);
   if (lane_id() == 0) s_a[wave] = pop;
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < 256 / kWave; ++w) pop += s_a[w];
+    for (int w = 1; w < kExtentFinal / kWave; ++w) pop += s_a[w];
     out[0] = mx;
     out[1] = cnt;
     out[2] = (cnt == mx + 1 && pop == cnt) ? 1 : 0;
@@ -461,9 +463,17 @@ __global__ __launch_bounds__(256) void map_extent_final_kernel(const int64_t *pa
 }
 
 int64_t map_extent_blocks(int64_t n) { return std::max<int64_t>(1, std::min<int64_t>(kExtentMaxBlocks, ceil_div(n, 256 * 16))); }
-// Workspace of moe_map_extent: the partials, then (256-byte aligned) the n-bit bitmap.
-size_t map_extent_bits_offset(int64_t n) {
+// Workspace of moe_map_extent: the partials, then (256-byte aligned) the n bytes of seen rows.
+size_t map_extent_seen_offset(int64_t n) {
   return static_cast<size_t>((map_extent_blocks(n) * 2 * sizeof(int64_t) + 255) / 256 * 256);
+}
+
+// Zeroes n 16-byte vectors.
+__global__ __launch_bounds__(256) void fill_u32x4_kernel(u32x4 *p, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    p[i] = u32x4{0u, 0u, 0u, 0u};
+  }
 }
 
 __global__ __launch_bounds__(256) void fill_i32_kernel(int32_t *p, int64_t n, int32_t v) {
@@ -573,7 +583,7 @@ int moe_permute(const moe_bf16_t *x, int64_t T, int64_t H, const void *row_id_ma
 
 size_t moe_map_extent_workspace_size(int64_t n) {
   if (n < 0) return 0;
-  return moe::map_extent_bits_offset(n) + static_cast<size_t>(moe::ceil_div(n, 32)) * sizeof(uint32_t);
+  return moe::map_extent_seen_offset(n) + static_cast<size_t>(moe::ceil_div(n, 16)) * 16;
 }
 
 int moe_map_extent(const void *row_id_map, int idx_dtype, int64_t n, int64_t *out, void *workspace,
@@ -585,26 +595,26 @@ int moe_map_extent(const void *row_id_map, int idx_dtype, int64_t n, int64_t *ou
   }
   if (out == nullptr || (n > 0 && row_id_map == nullptr)) return fail(MOE_ERR_INVALID_ARG, "moe_map_extent: null map or out");
   const size_t need = moe_map_extent_workspace_size(n);
-  if (workspace == nullptr || workspace_bytes < need || !is_aligned(workspace, 8)) {
-    return fail(MOE_ERR_WORKSPACE, "moe_map_extent: an 8-byte aligned workspace of %zu bytes is needed (got %zu)", need,
+  if (workspace == nullptr || workspace_bytes < need || !is_aligned(workspace, 16)) {
+    return fail(MOE_ERR_WORKSPACE, "moe_map_extent: a 16-byte aligned workspace of %zu bytes is needed (got %zu)", need,
                 workspace == nullptr ? size_t(0) : workspace_bytes);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t nb = map_extent_blocks(n);
   int64_t *partials = static_cast<int64_t *>(workspace);
-  uint32_t *bits = reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) + map_extent_bits_offset(n));
-  const int64_t words = ceil_div(n, 32);
-  if (words > 0) {
-    fill_i32_kernel<<<dim3(std::min<int64_t>(1024, ceil_div(words, 256))), dim3(256), 0, s>>>(
-        reinterpret_cast<int32_t *>(bits), words, 0);
+  uint8_t *seen = reinterpret_cast<uint8_t *>(static_cast<char *>(workspace) + map_extent_seen_offset(n));
+  const int64_t vecs = ceil_div(n, 16);
+  if (vecs > 0) {
+    fill_u32x4_kernel<<<dim3(std::min<int64_t>(2048, ceil_div(vecs, 256))), dim3(256), 0, s>>>(
+        reinterpret_cast<u32x4 *>(seen), vecs);
   }
   const bool vec = is_aligned(row_id_map, 16);
   const bool i64 = idx_dtype == MOE_IDX_I64;
-  if (i64 && vec) map_extent_partial_kernel<true, true><<<dim3(nb), dim3(256), 0, s>>>(row_id_map, n, partials, bits);
-  else if (i64) map_extent_partial_kernel<true, false><<<dim3(nb), dim3(256), 0, s>>>(row_id_map, n, partials, bits);
-  else if (vec) map_extent_partial_kernel<false, true><<<dim3(nb), dim3(256), 0, s>>>(row_id_map, n, partials, bits);
-  else map_extent_partial_kernel<false, false><<<dim3(nb), dim3(256), 0, s>>>(row_id_map, n, partials, bits);
-  map_extent_final_kernel<<<dim3(1), dim3(256), 0, s>>>(partials, static_cast<int>(nb), bits, out);
+  if (i64 && vec) map_extent_partial_kernel<true, true><<<dim3(nb), dim3(256), 0, s>>>(row_id_map, n, partials, seen);
+  else if (i64) map_extent_partial_kernel<true, false><<<dim3(nb), dim3(256), 0, s>>>(row_id_map, n, partials, seen);
+  else if (vec) map_extent_partial_kernel<false, true><<<dim3(nb), dim3(256), 0, s>>>(row_id_map, n, partials, seen);
+  else map_extent_partial_kernel<false, false><<<dim3(nb), dim3(256), 0, s>>>(row_id_map, n, partials, seen);
+  map_extent_final_kernel<<<dim3(1), dim3(kExtentFinal), 0, s>>>(partials, static_cast<int>(nb), seen, out);
   return check_launch("moe_map_extent");
 }
 

@@ -195,10 +195,10 @@ int moe_permute_index(const void *row_id_map, int idx_dtype, int map_layout, int
  *            does a scatter write every output row, so that the reference's
  *            zero-initialised output (new_zeros) needs no clearing.
  * out: int64 [3] on the device, written by the last of three kernels (a
- * bitmap clear; per-block partials that also set one bit per entry; their
- * sum in block order with the bit count). Workspace:
- * moe_map_extent_workspace_size(n) bytes (the partials and an n-bit bitmap),
- * 8-byte aligned. */
+ * clear of n bytes; per-block partials that also mark each entry's row with
+ * a byte; their sum in block order with the count of marked rows).
+ * Workspace: moe_map_extent_workspace_size(n) bytes (the partials and n
+ * bytes of row marks), 16-byte aligned. */
 size_t moe_map_extent_workspace_size(int64_t n);
 int moe_map_extent(const void *row_id_map, int idx_dtype, int64_t n, int64_t *out, void *workspace,
                    size_t workspace_bytes, void *stream);

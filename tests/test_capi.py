@@ -162,9 +162,9 @@ def test_workspace_sizes():
     assert lib.moe_row_id_map_workspace_size(1 << 26, 32) <= 64 * 33 * 4 + 256
     assert lib.moe_permute_workspace_size(16384) >= 4096 * 4
     # map extent: one (max, count) int64 pair per partial block, at most 1024 blocks
-    assert lib.moe_map_extent_workspace_size(0) == 256  # partials (256-byte aligned), then the n-bit bitmap
-    assert lib.moe_map_extent_workspace_size(320 * 16384) == 1024 * 16 + 320 * 16384 // 8
-    assert lib.moe_map_extent_workspace_size(33) == 256 + 8
+    assert lib.moe_map_extent_workspace_size(0) == 256  # partials (256-byte aligned), then n bytes of row marks
+    assert lib.moe_map_extent_workspace_size(320 * 16384) == 1024 * 16 + 320 * 16384
+    assert lib.moe_map_extent_workspace_size(33) == 256 + 48
     assert lib.moe_map_extent_workspace_size(-1) == 0
     assert lib.moe_row_id_map_workspace_size(-1, 4) == 0
     # router: one fp32 logits plane (used when the top-k call gets no logits output)
