@@ -3,9 +3,9 @@
 Tolerance: rtol 1.6e-2 / atol 1e-2 against the fp32-accumulated golden
 (per group dy.float() @ w.float() / dy.float().T @ x.float();
 kernel_cases/case37_ref_musa_asm_bf16_gemm_nn_256x384.py:47-49 is the same
-rule for one group) -- one bf16 rounding of an fp32 sum.  Small shapes are
-checked in full against the CPU oracle; the reference cases' own shapes
-(case05/07/08/09/13/19/37) in full against an fp32 torch reference on the GPU.
+rule for one group) -- one bf16 rounding of an fp32 sum.  Small shapes and
+the reference cases' own shapes (case05/07/08/09/13/19/37) are checked in
+full against the CPU oracle.
 Exact cases (scaled identities, one-row outer products) must be bit-identical.
 """
 from __future__ import annotations
