@@ -19,6 +19,7 @@
 // keeps the whole chip busy (run in the GEMM's epilogue it serialised 16 rows
 // per wavefront and was slower than the GEMM plus the pass).
 #include <algorithm>
+#include <type_traits>
 
 #include "gemm_device.h"
 #include "topk_device.h"
@@ -193,44 +194,71 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(RouterArgs p) {
 }
 
 // Router GEMM for 128 < N <= 512 with K % 64 == 0 (case38: N = 320): one
-// workgroup of 4 wavefronts per 128-row x 32 kNB-column tile (kNB = ceil(N /
-// 64), so two column tiles cover N: each CU streams half the weight, where the
-// 64-row tiles above stream all of it for half the rows). Consecutive tiles are
-// the two column halves of one row tile, and an XCD takes a contiguous run of
-// tiles, so the input rows are fetched once into that XCD's L2 for both halves
-// (the weight, 5.2 MB at case38, comes from the Infinity Cache). Wavefront w computes
-// rows (w / 2) 64 .. + 63, columns (w % 2) 16 kNB .. as 4 x kNB blocks of
-// v_mfma_f32_16x16x32_bf16. Fragments of the two 32-deep halves of a step are
-// double-buffered in registers: each half's MFMAs run while the other half's
-// fragments are read, and the step's DMAs (4 + kNB per wavefront, 4 stages
-// ahead) are spread among the first half's MFMAs; one barrier per step. fp32
-// results are stored from the accumulators (a lane holds 4 consecutive columns
-// of one row).
+// workgroup per 128-row x 32 kNB-column tile (kNB = ceil(N / 64), so two
+// column tiles cover N: each CU streams half the weight, where the 64-row
+// tiles above stream all of it for half the rows). Consecutive tiles are the
+// two column halves of one row tile, and an XCD takes a contiguous run of
+// tiles, so the input rows are fetched once into that XCD's L2 for both
+// halves. 8 wavefronts, on each SIMD one computing and one loading: the
+// computing wavefront of SIMD w computes rows (w / 2) 64 .. + 63, columns
+// (w % 2) 16 kNB .. as 4 x kNB blocks of v_mfma_f32_16x16x32_bf16 (the same
+// MFMA sequence over K as the 64-row kernel, so the logits are bit-identical),
+// with the fragments of the two 32-deep halves of a step double-buffered in
+// registers (each half's reads go out under the other half's MFMAs). Two
+// loading wavefronts DMA the input rows into a ring of kSA stages, two the
+// weight rows into a ring of kSB stages. A wavefront's loads complete in issue
+// order, so with the loads split by operand each ring runs its own lookahead:
+// the input (HBM) kSA - 1 steps ahead, the weight (Infinity Cache / L2)
+// kSB - 1, the LDS split between the rings (one ring holding both operands
+// at one depth, loaded by the computing wavefronts, ran case38 in 125 us
+// against 97). One workgroup barrier per step: the loaders have waited for
+// stage kt + 1, the computing wavefronts have read all of stage kt. fp32
+// results are stored from the accumulators (a lane holds 4 consecutive
+// columns of one row).
 template <int kNB>
-__global__ __launch_bounds__(256) void router_tile_kernel(RouterArgs p, int tiles) {
+__global__ __launch_bounds__(512) void router_ws_kernel(RouterArgs p, int tiles) {
   constexpr int kTM = 128;
-  constexpr int kTN = 32 * kNB;                  // columns per tile
+  constexpr int kTN = 32 * kNB;
   constexpr int kABytes = kTM * kRow;            // 16 KiB
   constexpr int kBBytes = kTN * kRow;
-  constexpr int kStageBytes = kABytes + kBBytes;
-  constexpr int kSt = 4 * kStageBytes <= 160 * 1024 ? 4 : 3;
-  constexpr int kDmaA = kABytes / 1024 / 4, kDmaB = kBBytes / 1024 / 4;
-  constexpr int kDma = kDmaA + kDmaB;            // DMA instructions per wavefront per stage
-  constexpr int kReads = 4 + kNB;                // fragment reads per wavefront per half step
-  static_assert(kSt * kStageBytes <= 160 * 1024, "LDS budget");
-  static_assert((kSt - 1) * kDma <= 63, "vmcnt range");
-  __shared__ __attribute__((aligned(1024))) char smem[kSt * kStageBytes];
+  constexpr int kSA = kNB <= 5 ? 5 : 4;
+  constexpr int kSBFit = (160 * 1024 - kSA * kABytes) / kBBytes;
+  constexpr int kSB = kSBFit > 4 ? 4 : kSBFit;
+  constexpr int kDmaA = kABytes / 1024 / 2, kDmaB = kBBytes / 1024 / 2;  // per loading wavefront
+  constexpr int kReads = 4 + kNB;
+  static_assert(kSB >= 3 && kSA * kABytes + kSB * kBBytes <= 160 * 1024, "LDS budget");
+  static_assert((kSA - 1) * kDmaA <= 63 && (kSB - 1) * kDmaB <= 63, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) char smem[kSA * kABytes + kSB * kBBytes];
   lds_char *const sbase = (lds_char *)smem;
-  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sbase));
+  const uint32_t a_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sbase));
+  const uint32_t b_lds = a_lds + kSA * kABytes;
 
   const int64_t P = gridDim.x, b = blockIdx.x;
   const int tile = static_cast<int>((b % 8) * (P / 8) + b / 8);
   if (tile >= tiles) return;
   const int rt = tile >> 1, ct = tile & 1;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wr = wave >> 1, wc = wave & 1;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  // ---- roles: the first wavefront of each SIMD computes (index = its SIMD), the second loads
+  // (SIMD 0 and 1: input rows, 2 and 3: weight rows), read from HW_ID and exchanged through LDS.
+  int role_simd, loader;
+  {
+    const int simd = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_s_getreg((1 << 11) | (4 << 6) | 4)) & 3;
+    volatile int *sid = reinterpret_cast<volatile int *>(smem);
+    if (lane == 0) sid[wave] = simd;
+    __syncthreads();
+    int before = 0, per_simd[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      const int sv = sid[w] & 3;
+      per_simd[sv] += 1;
+      before += (sv == simd) && (w < wave);
+    }
+    __syncthreads();
+    const bool ok = per_simd[0] == 2 && per_simd[1] == 2 && per_simd[2] == 2 && per_simd[3] == 2;
+    role_simd = __builtin_amdgcn_readfirstlane(ok ? simd : (wave & 3));
+    loader = __builtin_amdgcn_readfirstlane(ok ? before : (wave >> 2));
+  }
   const int64_t K = p.K;
   const int N = p.N;
   const int64_t row0 = static_cast<int64_t>(rt) * kTM;
@@ -238,46 +266,77 @@ __global__ __launch_bounds__(256) void router_tile_kernel(RouterArgs p, int tile
   const int rows_valid = static_cast<int>(min(p.M - row0, int64_t(kTM)));
   const int cols_valid = min(N - col0, kTN);
   const int ktiles = static_cast<int>(K / kBK);
-
-  // Rows past the tile's valid rows / columns lie past the resources: zeros.
   const uint32_t row_bytes = static_cast<uint32_t>(K) * 2u;
-  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.inp + row0 * K, static_cast<uint32_t>(rows_valid) * row_bytes);
-  const __amdgpu_buffer_rsrc_t rb =
-      make_rsrc(p.w + static_cast<int64_t>(col0) * K, static_cast<uint32_t>(cols_valid) * row_bytes);
-  int a_off[kDmaA], b_off[kDmaB];
+
+  if (loader) {
+    // Rows past the tile's valid rows / columns lie past the resources: zeros.
+    const bool is_a = role_simd < 2;
+    const int li = role_simd & 1;
+    const __amdgpu_buffer_rsrc_t rsrc =
+        is_a ? make_rsrc(p.inp + row0 * K, static_cast<uint32_t>(rows_valid) * row_bytes)
+             : make_rsrc(p.w + static_cast<int64_t>(col0) * K, static_cast<uint32_t>(cols_valid) * row_bytes);
+    const int ndma = is_a ? kDmaA : kDmaB;
+    const int blk0 = li * ndma;  // this wavefront's 1 KiB blocks (8 rows each) of a stage: blk0 ..
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int r0 = blk0 * 8 + (ln >> 3);  // row of block blk0 + j: r0 + 8 j
+    auto issue = [&](auto is_a_c, int kt, int slot) {
+      constexpr bool kA = decltype(is_a_c)::value;
+      constexpr int n = kA ? kDmaA : kDmaB;
+      const uint32_t st = (kA ? a_lds + slot * kABytes : b_lds + slot * kBBytes) + blk0 * 1024;
+      const int soff = kt * kBK * 2;
 #pragma unroll
-  for (int j = 0; j < kDmaA; ++j) {
-    const int r = (j * 4 + wave) * 8 + (lane >> 3);
-    a_off[j] = static_cast<int>(static_cast<uint32_t>(r) * row_bytes + (((lane & 7) ^ swz(r)) << 4));
+      for (int j = 0; j < n; ++j) {
+        const int r = r0 + j * 8;
+        const int off = static_cast<int>(static_cast<uint32_t>(r) * row_bytes + (((ln & 7) ^ swz(r)) << 4));
+        dma16b(rsrc, (lds_void *)(uintptr_t)(st + j * 1024), off, soff);
+      }
+    };
+    // Stages past the last re-read it (the count of outstanding loads stays the same in every step);
+    // they land in slots nothing reads any more.
+    if (is_a) {
+      for (int st = 0; st < kSA - 1; ++st) issue(std::true_type{}, min(st, ktiles - 1), st);
+      wait_vm_n<(kSA - 2) * kDmaA>();
+      barrier();
+      int slot = kSA - 1;  // slot of stage kt + kSA - 1 = slot of stage kt - 1
+      for (int kt = 0; kt < ktiles; ++kt) {
+        issue(std::true_type{}, min(kt + kSA - 1, ktiles - 1), slot);
+        slot = slot + 1 == kSA ? 0 : slot + 1;
+        wait_vm_n<(kSA - 2) * kDmaA>();  // stage kt + 1 has landed
+        barrier();
+      }
+    } else {
+      for (int st = 0; st < kSB - 1; ++st) issue(std::false_type{}, min(st, ktiles - 1), st);
+      wait_vm_n<(kSB - 2) * kDmaB>();
+      barrier();
+      int slot = kSB - 1;
+      for (int kt = 0; kt < ktiles; ++kt) {
+        issue(std::false_type{}, min(kt + kSB - 1, ktiles - 1), slot);
+        slot = slot + 1 == kSB ? 0 : slot + 1;
+        wait_vm_n<(kSB - 2) * kDmaB>();
+        barrier();
+      }
+    }
+    (void)ndma;
+    wait_dma();  // the re-reads of the last steps
+    return;
   }
-#pragma unroll
-  for (int j = 0; j < kDmaB; ++j) {
-    const int r = (j * 4 + wave) * 8 + (lane >> 3);
-    b_off[j] = static_cast<int>(static_cast<uint32_t>(r) * row_bytes + (((lane & 7) ^ swz(r)) << 4));
-  }
-  auto issue = [&](int kt, int slot) {
-    const uint32_t st = lds_base + (slot % kSt) * kStageBytes;
-    const int soff = kt * kBK * 2;
-#pragma unroll
-    for (int j = 0; j < kDmaA; ++j) dma16b(ra, (lds_void *)(uintptr_t)(st + (j * 4 + wave) * 1024), a_off[j], soff);
-#pragma unroll
-    for (int j = 0; j < kDmaB; ++j)
-      dma16b(rb, (lds_void *)(uintptr_t)(st + kABytes + (j * 4 + wave) * 1024), b_off[j], soff);
-  };
+
+  const int wr = role_simd >> 1, wc = role_simd & 1;
   const int frow = lane & 15, fq = lane >> 4;
   auto frag_addr = [&](uint32_t slot_base, int r, int ks) {
     return slot_base + r * kRow + ((((ks << 2) | fq) ^ swz(r)) << 4);
   };
   bf16x8 fa[2][4], fb[2][kNB];
-  auto read_half = [&](int kt, int ks, int buf) {
-    const uint32_t sb = lds_base + (kt % kSt) * kStageBytes;
+  int sa = 0, sb = 0;  // ring slots of the stage being read
+  auto read_half = [&](int ks, int buf) {
+    const uint32_t ab = a_lds + sa * kABytes, bb = b_lds + sb * kBBytes;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      fa[buf][i] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)frag_addr(sb, wr * 64 + i * 16 + frow, ks));
+      fa[buf][i] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)frag_addr(ab, wr * 64 + i * 16 + frow, ks));
 #pragma unroll
     for (int j = 0; j < kNB; ++j)
-      fb[buf][j] = *reinterpret_cast<const lds_bf16x8 *>(
-          (uintptr_t)frag_addr(sb + kABytes, wc * 16 * kNB + j * 16 + frow, ks));
+      fb[buf][j] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)frag_addr(bb, wc * 16 * kNB + j * 16 + frow, ks));
   };
   f32x4 acc[4][kNB];
 #pragma unroll
@@ -291,34 +350,22 @@ __global__ __launch_bounds__(256) void router_tile_kernel(RouterArgs p, int tile
       for (int j = 0; j < kNB; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[buf][j], fa[buf][i], acc[i][j], 0, 0, 0);
   };
-
-  // Prologue: stages 0 .. kSt - 2 (stages past the last re-read it, which keeps the count of outstanding
-  // DMAs the same in every step; they land in slots nothing reads any more).
-#pragma unroll
-  for (int st = 0; st < kSt - 1; ++st) issue(min(st, ktiles - 1), st);
-  wait_vm_n<(kSt - 2) * kDma>();
-  barrier();
-  read_half(0, 0, 0);
+  barrier();  // stage 0 has landed
+  read_half(0, 0);
   for (int kt = 0; kt < ktiles; ++kt) {
-    // First half: read the second half's fragments of this stage, DMA stage kt + kSt - 1 into the slot
-    // of stage kt - 1 (every wavefront finished reading it before the previous step's barrier), multiply
-    // the first half.
-    read_half(kt, 1, 1);
-    issue(min(kt + kSt - 1, ktiles - 1), kt + kSt - 1);
+    read_half(1, 1);
     mfma_half(0);
-    sched_mix<4 * kNB, kReads, kDma>();
+    sched_mix<4 * kNB, kReads, 0>();
     __builtin_amdgcn_sched_barrier(0);
-    // Stage kt + 1 has landed (younger: the DMAs of stages kt + 2 .. kt + kSt - 1), and every wavefront's
-    // reads of stage kt are done.
-    wait_vm_n<(kSt - 2) * kDma>();
-    wait_lds();
-    barrier();
-    if (kt + 1 < ktiles) read_half(kt + 1, 0, 0);
+    wait_lds();  // this wavefront's reads of stage kt are done before the slot can be refilled
+    barrier();   // stage kt + 1 has landed
+    sa = sa + 1 == kSA ? 0 : sa + 1;
+    sb = sb + 1 == kSB ? 0 : sb + 1;
+    if (kt + 1 < ktiles) read_half(0, 0);
     mfma_half(1);
     sched_mix<4 * kNB, kReads, 0>();
     __builtin_amdgcn_sched_barrier(0);
   }
-  wait_dma();  // the re-reads of the last steps
 
   // acc[i][j] register r of lane l: row wr 64 + i 16 + l % 16, column wc 16 kNB + j 16 + 4 (l / 16) + r.
   float *out = p.out;
@@ -402,12 +449,12 @@ int launch(const char *fn, const moe_bf16_t *inp, int64_t M, int64_t K, const mo
     const int tiles = row_tiles * 2;
     const dim3 g(static_cast<uint32_t>((tiles + 7) / 8 * 8));
     switch (nb) {
-      case 3: router_tile_kernel<3><<<g, dim3(256), 0, s>>>(p, tiles); break;
-      case 4: router_tile_kernel<4><<<g, dim3(256), 0, s>>>(p, tiles); break;
-      case 5: router_tile_kernel<5><<<g, dim3(256), 0, s>>>(p, tiles); break;
-      case 6: router_tile_kernel<6><<<g, dim3(256), 0, s>>>(p, tiles); break;
-      case 7: router_tile_kernel<7><<<g, dim3(256), 0, s>>>(p, tiles); break;
-      default: router_tile_kernel<8><<<g, dim3(256), 0, s>>>(p, tiles); break;
+      case 3: router_ws_kernel<3><<<g, dim3(512), 0, s>>>(p, tiles); break;
+      case 4: router_ws_kernel<4><<<g, dim3(512), 0, s>>>(p, tiles); break;
+      case 5: router_ws_kernel<5><<<g, dim3(512), 0, s>>>(p, tiles); break;
+      case 6: router_ws_kernel<6><<<g, dim3(512), 0, s>>>(p, tiles); break;
+      case 7: router_ws_kernel<7><<<g, dim3(512), 0, s>>>(p, tiles); break;
+      default: router_ws_kernel<8><<<g, dim3(512), 0, s>>>(p, tiles); break;
     }
   } else switch (nb) {
     case 1: router_gemm_kernel<1><<<dim3(grid), dim3(256), 0, s>>>(p); break;

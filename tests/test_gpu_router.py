@@ -43,6 +43,29 @@ def test_router_logits_shapes(pkg, dev, M, K, N):
     _check_logits(got, inp, w, f"M={M} K={K} N={N}")
 
 
+@pytest.mark.parametrize("M,K,N", [
+    (257, 4096, 320),    # the case's N: 128-row tiles over half of N (kNB = 5)
+    (300, 1024, 136),    # kNB = 3
+    (129, 640, 250),     # kNB = 4, column tail
+    (200, 2048, 384),    # kNB = 6
+    (64, 512, 448),      # kNB = 7
+    (130, 512, 512),     # kNB = 8
+])
+def test_router_tiles_bit_identical_to_row_kernel(pkg, dev, M, K, N):
+    # 128 < N with whole 64-column steps and 16-byte output rows runs as 128-row tiles over half of N, with
+    # the loads in wavefronts of their own; an output 4 bytes off 16-byte alignment runs the 64-row kernel.
+    # Each logit is the same MFMA sequence over K in both: bit-identical, and within the bound of the oracle.
+    g = torch.Generator().manual_seed(5 * M + K + N)
+    inp = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = torch.randn(N, K, generator=g).to(torch.bfloat16)
+    tiled = pkg.ops.router_logits(inp.to(dev), w.to(dev))
+    buf = torch.empty(M * N + 4, dtype=torch.float32, device=dev)
+    rows = pkg.ops.router_logits(inp.to(dev), w.to(dev), out=buf[1:1 + M * N].view(M, N))
+    assert rows.data_ptr() % 16 == 4
+    assert_bits_equal(tiled, rows, f"tiles vs 64-row kernel M={M} K={K} N={N}")
+    _check_logits(tiled, inp, w, f"M={M} K={K} N={N}")
+
+
 def test_case38_full_shape(pkg, dev):
     # The case's seeded inputs at full size: every logit against the CPU oracle, and the case's
     # own explicit-sum rule on its three rows.
