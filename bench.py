@@ -302,7 +302,7 @@ def backward_gemms(pkg, x, row_map, offs, h, w1, w2, dev, library=False):
         case = getattr(pkg.cases, name)
         a, b = case.get_inputs(dev)
         model = case.Model()
-        ms = _time_ms(lambda: model(a, b))
+        ms = _time_ms(lambda: model(a, b), reps=20, warm=5)  # sub-millisecond calls: more of them
         T, N, K, G = case.TOKENS, case.N, case.K, case.NUM_GROUPS
         flops = 2 * T * N * K
         hbm = 2 * (T * N + (G * N * K if kind == "dgrad" else T * K) + (T * K if kind == "dgrad" else G * N * K))
