@@ -59,6 +59,7 @@ namespace {
 using namespace gemm;
 
 typedef __bf16 v4bf16 __attribute__((__vector_size__(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4bf16 lds_v4bf16;
 
 constexpr int kBN = 256;            // output columns per tile
@@ -109,6 +110,24 @@ __device__ __forceinline__ bf16x8 read_rm_frag(uint32_t addr) {
 #else
   (void)addr;
   return bf16x8{};
+#endif
+}
+
+// One 16 x 16 x 32 MFMA on 16-bit operands: bf16, or fp16 (kF16: the tf32 router wgrad's scaled operands,
+// the same bit layout in LDS and registers).
+template <bool kF16>
+__device__ __forceinline__ f32x4_t mma16(bf16x8 a, bf16x8 b, f32x4_t c) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  if constexpr (kF16) {
+    typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+#else
+  (void)a;
+  (void)b;
+  return c;
 #endif
 }
 
@@ -519,8 +538,9 @@ __device__ __forceinline__ int rm16_swz(int krow) { return ((krow & 3) << 2) | (
 // [M, K] of out (at the same row indices).
 // kOrder (wgrad): the tiles take the groups in the order p.order lists them
 // (largest first, from group_order_kernel) instead of by index.
-template <bool kWgrad, int kOut, bool kSplit = false, bool kOrder = false>
+template <bool kWgrad, int kOut, bool kSplit = false, bool kOrder = false, bool kF16 = false>
 __global__ __launch_bounds__(256) void grouped_gemm_bwd_pipe_kernel(BwdArgs p) {
+  static_assert(!kF16 || (kWgrad && kOut == 1), "fp16 operands: the tf32 router wgrad (fp32 planes)");
   static_assert(!kSplit || (!kWgrad && kOut == 1), "the split is a dgrad with fp32 planes");
   static_assert(!kOrder || kWgrad, "the group order is a wgrad schedule");
   constexpr int kBM = 256;
@@ -780,7 +800,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_pipe_kernel(BwdArgs p) {
     for (int j = 0; j < kNI; ++j) {
 #pragma unroll
       for (int i = 4; i < 8; ++i) {
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[1][j], fa[1][i], acc[i][j], 0, 0, 0);
+        acc[i][j] = mma16<kF16>(fb[1][j], fa[1][i], acc[i][j]);
       }
       fb[1][j] = rm_frag(base_b, x, j, 1);
       if (j < 4) {
@@ -798,7 +818,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_pipe_kernel(BwdArgs p) {
     for (int i = 4 * ih; i < 4 * ih + 4; ++i)
 #pragma unroll
       for (int j = 0; j < kNI; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[ks][j], fa[ks][i], zero ? f32x4{} : acc[i][j], 0, 0, 0);
+        acc[i][j] = mma16<kF16>(fb[ks][j], fa[ks][i], zero ? f32x4{} : acc[i][j]);
   };
 
   // Epilogue of tile t from the accumulators: register r of lane l in block
@@ -1432,11 +1452,11 @@ __global__ __launch_bounds__(512) void grouped_gemm_bwd_pp_kernel(BwdArgs p) {
   }
 }
 
-template <bool kWgrad, int kOut = 0, bool kSplit = false, bool kOrder = false>
+template <bool kWgrad, int kOut = 0, bool kSplit = false, bool kOrder = false, bool kF16 = false>
 void launch_pipe(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
   int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
   grid = std::max<int64_t>(8, (grid + 7) / 8 * 8);
-  grouped_gemm_bwd_pipe_kernel<kWgrad, kOut, kSplit, kOrder><<<dim3(grid), dim3(256), 0, s>>>(p);
+  grouped_gemm_bwd_pipe_kernel<kWgrad, kOut, kSplit, kOrder, kF16><<<dim3(grid), dim3(256), 0, s>>>(p);
 }
 
 #ifndef MOE_GEMM_BWD_PINGPONG
@@ -1561,9 +1581,110 @@ void launch_split(const SplitArgs &a, hipStream_t s) {
   tf32_split_kernel<<<dim3(grid), dim3(256), 0, s>>>(a);
 }
 
-// out[i] = sum over s of part[s][i], s ascending (n % 4 == 0, 16-byte aligned).
-__global__ __launch_bounds__(256) void sum_planes_kernel(const float *part, int planes, int64_t n, float *out) {
-  const int64_t q = n / 4;
+// ---- tf32 wgrad on the fp16 matrix cores --------------------------------
+// A tf32 value has 11 significant bits, as many as fp16. Scaled by the power of
+// two 2^e that brings the largest magnitude of its column into [2^14, 2^15),
+// every tf32-rounded value of the column is an fp16 value, exactly unless it
+// lies 2^29 or more below that largest one (it then rounds to an fp16
+// subnormal: an error below 2^-38 of the column's largest magnitude). The
+// product of two fp16 values is exact in fp32, so one fp16 MFMA replaces the
+// three bf16 products of the hi/lo split, and the fp32 sums are scaled back by
+// 2^-(e_row + e_col) (exact) when the reduction planes are added. A column
+// whose largest magnitude is 0, Inf or NaN keeps scale 1.
+__device__ __forceinline__ int scale_exp(float mx) {
+  if (!(mx > 0.f) || !(mx < __builtin_huge_valf())) return 0;
+  int e = 0;
+  (void)__builtin_frexpf(mx, &e);  // mx = f 2^e, f in [0.5, 1)
+  return 15 - e;                   // mx 2^(15 - e) in [2^14, 2^15)
+}
+
+// Largest magnitude per column over a slab of rows: block (x, y) covers cg
+// groups of 4 columns from x 4 cg and rows y rps .. + rps - 1, its threads
+// split over the groups (t % cg) and 256 / cg interleaved row phases (t / cg,
+// combined in LDS), 8 independent rows per round; part[y][c].
+__global__ __launch_bounds__(256) void colmax_partial_kernel(const float *src, int64_t R, int64_t C, int64_t rps, int cg,
+                                                             float *part) {
+  __shared__ u32x4 red[256];
+  const int t = threadIdx.x;
+  const int ph = 256 / cg, g = t % cg, f = t / cg;
+  const int64_t c = (static_cast<int64_t>(blockIdx.x) * cg + g) * 4;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * rps, r1 = min(R, r0 + rps);
+  float m0 = 0.f, m1 = 0.f, m2 = 0.f, m3 = 0.f;
+  if (f < ph && c < C) {
+    for (int64_t r = r0 + f; r < r1; r += 8 * ph) {
+      u32x4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t ru = r + u * ph;
+        v[u] = ru < r1 ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src + ru * C + c)) : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        m0 = fmaxf(m0, fabsf(__uint_as_float(v[u].x)));
+        m1 = fmaxf(m1, fabsf(__uint_as_float(v[u].y)));
+        m2 = fmaxf(m2, fabsf(__uint_as_float(v[u].z)));
+        m3 = fmaxf(m3, fabsf(__uint_as_float(v[u].w)));
+      }
+    }
+  }
+  red[t] = u32x4{__float_as_uint(m0), __float_as_uint(m1), __float_as_uint(m2), __float_as_uint(m3)};
+  __syncthreads();
+  if (f == 0 && c < C) {
+    for (int k = 1; k < ph; ++k) {
+      const u32x4 o = red[t + k * cg];
+      m0 = fmaxf(m0, __uint_as_float(o.x));
+      m1 = fmaxf(m1, __uint_as_float(o.y));
+      m2 = fmaxf(m2, __uint_as_float(o.z));
+      m3 = fmaxf(m3, __uint_as_float(o.w));
+    }
+    *reinterpret_cast<u32x4 *>(part + static_cast<int64_t>(blockIdx.y) * C + c) =
+        u32x4{__float_as_uint(m0), __float_as_uint(m1), __float_as_uint(m2), __float_as_uint(m3)};
+  }
+}
+
+// exp[c] = scale_exp(largest of part[0..S)[c]) (S <= 64: eight independent loads per round).
+__global__ __launch_bounds__(256) void colmax_final_kernel(const float *part, int S, int64_t C, int32_t *exp) {
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (c >= C) return;
+  float m = 0.f;
+  for (int y0 = 0; y0 < S; y0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = y0 + u < S ? part[static_cast<int64_t>(y0 + u) * C + c] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) m = fmaxf(m, v[u]);
+  }
+  exp[c] = scale_exp(m);
+}
+
+// dst[r][c] = fp16(tf32(src[r][c]) 2^exp[c]) (RNE; C % 4 == 0).
+__global__ __launch_bounds__(256) void tf32_to_f16_cols_kernel(const float *src, int64_t R, int64_t C, const int32_t *exp,
+                                                               uint16_t *dst) {
+  const int64_t q = C / 4;
+  const int64_t total = R * q;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < total; i += stride) {
+    const int64_t r = i / q, c = (i - r * q) * 4;
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src + r * C + c));
+    const int4 e = *reinterpret_cast<const int4 *>(exp + c);
+    const uint32_t in[4] = {v.x, v.y, v.z, v.w};
+    const int ex[4] = {e.x, e.y, e.z, e.w};
+    uint32_t h[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float t = __builtin_ldexpf(__uint_as_float(tf32_rne_bits(in[k])), ex[k]);
+      h[k] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(t));
+    }
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<u32x2 *>(dst + r * C + c) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+  }
+}
+
+// out[n][k] = 2^-(row_exp[n] + col_exp[k]) sum over s of part[s][n][k], s ascending (K % 4 == 0).
+__global__ __launch_bounds__(256) void sum_planes_scaled_kernel(const float *part, int planes, int64_t N, int64_t K,
+                                                                const int32_t *row_exp, const int32_t *col_exp, float *out) {
+  const int64_t n = N * K;
+  const int64_t q = n / 4, qk = K / 4;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < q; i += stride) {
     u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(part) + i);
@@ -1575,9 +1696,31 @@ __global__ __launch_bounds__(256) void sum_planes_kernel(const float *part, int 
       z += __uint_as_float(b.z);
       w += __uint_as_float(b.w);
     }
+    const int64_t row = i / qk, col = (i - row * qk) * 4;
+    const int er = row_exp[row];
+    const int4 ec = *reinterpret_cast<const int4 *>(col_exp + col);
+    x = __builtin_ldexpf(x, -(er + ec.x));
+    y = __builtin_ldexpf(y, -(er + ec.y));
+    z = __builtin_ldexpf(z, -(er + ec.z));
+    w = __builtin_ldexpf(w, -(er + ec.w));
     *(reinterpret_cast<u32x4 *>(out) + i) = u32x4{__float_as_uint(x), __float_as_uint(y), __float_as_uint(z), __float_as_uint(w)};
   }
 }
+
+// Column-max slabs of an [R, C] operand: at most 64 slabs of at least 64 rows (C is not used: the slab
+// count only bounds the final pass's loads per column).
+struct ColmaxPlan {
+  int64_t S, rps;
+  int cg;      // groups of 4 columns per block (the rest of the 256 threads split the rows)
+  int64_t xb;  // blocks across the columns
+};
+ColmaxPlan colmax_plan(int64_t R, int64_t C) {
+  const int64_t S = std::max<int64_t>(1, std::min<int64_t>(64, ceil_div(R, 64)));
+  const int64_t rps = std::max<int64_t>(1, ceil_div(R, S));
+  const int cg = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(256, ceil_div(C, 4))));
+  return {ceil_div(std::max<int64_t>(R, 1), rps), rps, cg, std::max<int64_t>(1, ceil_div(ceil_div(C, 4), cg))};
+}
+
 
 // dx rows r of group 0 (offsets[0] <= r < offsets[1], clamped to [0, M)):
 // dx[r][c] = bf16 RNE of the sum over s of part[s][r][c], s ascending; other
@@ -1889,11 +2032,10 @@ struct WgradPlan {
   int64_t c;  // rows per chunk
 };
 
-WgradPlan wgrad_plan(int64_t M, int64_t N, int64_t K) {
-  const int64_t rows = 3 * M;
+WgradPlan wgrad_plan(int64_t rows, int64_t N, int64_t K) {
   WgradPlan pl{1, rows};
   const int64_t tiles = moe::ceil_div(N, 256) * moe::ceil_div(K, 256);
-  if (M == 0 || tiles >= 256) return pl;
+  if (rows == 0 || tiles >= 256) return pl;
   int64_t s = std::min<int64_t>(moe::ceil_div(512, tiles), std::max<int64_t>(1, rows / 512));
   s = std::max<int64_t>(1, std::min<int64_t>(s, 64));
   if (s == 1) return pl;
@@ -1903,9 +2045,38 @@ WgradPlan wgrad_plan(int64_t M, int64_t N, int64_t K) {
   return pl;
 }
 
-size_t wgrad_planes_bytes(const WgradPlan &pl, int64_t N, int64_t K) {
-  return pl.s == 1 ? 0 : moe::align_up(static_cast<size_t>(pl.s) * N * K * 4);
+// Workspace of the tf32 wgrad (byte offsets, each 256-byte aligned): the fp16
+// copies of grad_output [M, N] and inp [M, K], the scale exponents of their
+// columns, the column-max slabs, and the fp32 planes of the reduction chunks
+// (one plane at least: the scale is undone where the planes are added).
+struct WgradTf32Layout {
+  WgradPlan pl;
+  moe::ColmaxPlan ca, cb;
+  size_t a16, b16, row_exp, col_exp, part_a, part_b, planes, total;
+};
+WgradTf32Layout wgrad_tf32_layout(int64_t M, int64_t N, int64_t K) {
+  using moe::align_up;
+  WgradTf32Layout l;
+  l.pl = wgrad_plan(M, N, K);
+  l.ca = moe::colmax_plan(M, N);
+  l.cb = moe::colmax_plan(M, K);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += align_up(bytes);
+    return at;
+  };
+  l.a16 = take(static_cast<size_t>(M) * N * 2);
+  l.b16 = take(static_cast<size_t>(M) * K * 2);
+  l.row_exp = take(static_cast<size_t>(N) * 4);
+  l.col_exp = take(static_cast<size_t>(K) * 4);
+  l.part_a = take(static_cast<size_t>(l.ca.S) * N * 4);
+  l.part_b = take(static_cast<size_t>(l.cb.S) * K * 4);
+  l.planes = take(static_cast<size_t>(l.pl.s) * N * K * 4);
+  l.total = off;
+  return l;
 }
+
 
 }  // namespace
 
@@ -1913,8 +2084,7 @@ extern "C" {
 
 size_t moe_router_wgrad_tf32_workspace_size(int64_t M, int64_t N, int64_t K) {
   if (M < 0 || N < 0 || K < 0) return 0;
-  return moe::align_up(static_cast<size_t>(3 * M) * N * 2) + moe::align_up(static_cast<size_t>(3 * M) * K * 2) +
-         wgrad_planes_bytes(wgrad_plan(M, N, K), N, K);
+  return wgrad_tf32_layout(M, N, K).total;
 }
 
 int moe_router_wgrad_tf32(const float *grad_output, int64_t M, int64_t N, const float *inp, int64_t K,
@@ -1925,8 +2095,8 @@ int moe_router_wgrad_tf32(const float *grad_output, int64_t M, int64_t N, const 
     return fail(MOE_ERR_SHAPE, "%s: negative size (M=%lld N=%lld K=%lld)", fn, (long long)M, (long long)N, (long long)K);
   }
   if (K % 8 != 0 || N % 8 != 0) return fail(MOE_ERR_SHAPE, "%s: N=%lld and K=%lld must be multiples of 8", fn, (long long)N, (long long)K);
-  if (3 * M * N > (int64_t(1) << 30) - 1 || 3 * M * K > (int64_t(1) << 30) - 1 || N * K > (int64_t(1) << 30) - 1) {
-    return fail(MOE_ERR_CAPACITY, "%s: M=%lld N=%lld K=%lld exceed the 32-bit offsets (3M*N, 3M*K, N*K < 2^30)", fn,
+  if (M * N > (int64_t(1) << 30) - 1 || M * K > (int64_t(1) << 30) - 1 || N * K > (int64_t(1) << 30) - 1) {
+    return fail(MOE_ERR_CAPACITY, "%s: M=%lld N=%lld K=%lld exceed the 32-bit offsets (M*N, M*K, N*K < 2^30)", fn,
                 (long long)M, (long long)N, (long long)K);
   }
   if (N == 0 || K == 0) return MOE_OK;
@@ -1936,49 +2106,57 @@ int moe_router_wgrad_tf32(const float *grad_output, int64_t M, int64_t N, const 
   if (!is_aligned(grad_output, 16) || !is_aligned(inp, 16) || !is_aligned(grad_weight, 16)) {
     return fail(MOE_ERR_ALIGN, "%s: grad_output, inp and grad_weight must be 16-byte aligned", fn);
   }
-  const size_t need = moe_router_wgrad_tf32_workspace_size(M, N, K);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need || !is_aligned(workspace, kWsAlign))) {
-    return fail(MOE_ERR_WORKSPACE, "%s: a 256-byte aligned workspace of %zu bytes is needed (got %zu)", fn, need,
+  const WgradTf32Layout l = wgrad_tf32_layout(M, N, K);
+  if (workspace == nullptr || workspace_bytes < l.total || !is_aligned(workspace, kWsAlign)) {
+    return fail(MOE_ERR_WORKSPACE, "%s: a 256-byte aligned workspace of %zu bytes is needed (got %zu)", fn, l.total,
                 workspace == nullptr ? size_t(0) : workspace_bytes);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // One wgrad over 3M stacked rows: [A_hi; A_hi; A_lo]^T [B_hi; B_lo; B_hi] =
-  // A_hi^T B_hi + A_hi^T B_lo + A_lo^T B_hi.  A = grad_output [M, N], B = inp [M, K].
   char *w = static_cast<char *>(workspace);
-  const size_t sz_a = align_up(static_cast<size_t>(3 * M) * N * 2), sz_b = align_up(static_cast<size_t>(3 * M) * K * 2);
-  uint16_t *a3 = reinterpret_cast<uint16_t *>(w);
-  uint16_t *b3 = reinterpret_cast<uint16_t *>(w + sz_a);
-  float *planes = reinterpret_cast<float *>(w + sz_a + sz_b);
+  uint16_t *a16 = reinterpret_cast<uint16_t *>(w + l.a16);
+  uint16_t *b16 = reinterpret_cast<uint16_t *>(w + l.b16);
+  int32_t *row_exp = reinterpret_cast<int32_t *>(w + l.row_exp);
+  int32_t *col_exp = reinterpret_cast<int32_t *>(w + l.col_exp);
+  float *part_a = reinterpret_cast<float *>(w + l.part_a);
+  float *part_b = reinterpret_cast<float *>(w + l.part_b);
+  float *planes = reinterpret_cast<float *>(w + l.planes);
+  // Scale exponents of grad_output's columns (dw rows) and inp's columns (dw columns), then the fp16 copies.
+  colmax_partial_kernel<<<dim3(static_cast<uint32_t>(l.ca.xb), static_cast<uint32_t>(l.ca.S)), dim3(256), 0, s>>>(
+      grad_output, M, N, l.ca.rps, l.ca.cg, part_a);
+  colmax_partial_kernel<<<dim3(static_cast<uint32_t>(l.cb.xb), static_cast<uint32_t>(l.cb.S)), dim3(256), 0, s>>>(
+      inp, M, K, l.cb.rps, l.cb.cg, part_b);
+  colmax_final_kernel<<<dim3(static_cast<uint32_t>(ceil_div(N, 256))), dim3(256), 0, s>>>(part_a, static_cast<int>(l.ca.S), N,
+                                                                                          row_exp);
+  colmax_final_kernel<<<dim3(static_cast<uint32_t>(ceil_div(K, 256))), dim3(256), 0, s>>>(part_b, static_cast<int>(l.cb.S), K,
+                                                                                          col_exp);
   if (M > 0) {
-    SplitArgs sa{grad_output, M, N, a3, a3 + M * N, a3 + 2 * M * N, N, N, N};
-    SplitArgs sb{inp, M, K, b3, b3 + 2 * M * K, b3 + M * K, K, K, K};
-    launch_split(sa, s);
-    launch_split(sb, s);
-    if (int rc = check_launch(fn)) return rc;
+    const int64_t ga = std::max<int64_t>(1, std::min<int64_t>(ceil_div(M * N / 4, 256), 8192));
+    const int64_t gb = std::max<int64_t>(1, std::min<int64_t>(ceil_div(M * K / 4, 256), 8192));
+    tf32_to_f16_cols_kernel<<<dim3(static_cast<uint32_t>(ga)), dim3(256), 0, s>>>(grad_output, M, N, row_exp, a16);
+    tf32_to_f16_cols_kernel<<<dim3(static_cast<uint32_t>(gb)), dim3(256), 0, s>>>(inp, M, K, col_exp, b16);
   }
-  const WgradPlan pl = wgrad_plan(M, N, K);
-  const bool split = pl.s > 1;
+  if (int rc = check_launch(fn)) return rc;
+  // dw planes over the reduction chunks (fp16 MFMA, exact products, fp32 sums), then their sum scaled back.
   BwdArgs p;
-  p.a = a3;
-  p.b = b3;
+  p.a = a16;
+  p.b = b16;
   p.offsets = nullptr;
-  p.out = split ? static_cast<void *>(planes) : static_cast<void *>(grad_weight);
-  p.M = 3 * M;
+  p.out = planes;
+  p.M = M;
   p.N = N;
   p.K = K;
-  p.G = pl.s;
+  p.G = l.pl.s;
   p.ntiles = ceil_div(K, kBN);
-  p.chunk = pl.c;
+  p.chunk = l.pl.c;
   p.kchunk = 0;
   p.order = nullptr;
   p.order_rows = nullptr;
   p.tails = nullptr;
-  launch_pipe<true, 1>(p, ceil_div(N, 256) * p.ntiles * p.G, s);
-  if (split) {
-    const int64_t q = N * K / 4;
-    const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(ceil_div(q, 256), 4096));
-    sum_planes_kernel<<<dim3(grid), dim3(256), 0, s>>>(planes, static_cast<int>(pl.s), N * K, grad_weight);
-  }
+  launch_pipe<true, 1, false, false, true>(p, ceil_div(N, 256) * p.ntiles * p.G, s);
+  const int64_t q = N * K / 4;
+  const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(ceil_div(q, 256), 4096));
+  sum_planes_scaled_kernel<<<dim3(static_cast<uint32_t>(grid)), dim3(256), 0, s>>>(planes, static_cast<int>(l.pl.s), N, K,
+                                                                                   row_exp, col_exp, grad_weight);
   return check_launch(fn);
 }
 

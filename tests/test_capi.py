@@ -204,8 +204,14 @@ def test_workspace_sizes():
     assert lib.moe_grouped_gemm_workspace_size(1000, 1024, 1000, 1) == 16 * 5 * 65536 * 4  # 16 tiles, 5 ranges
     assert lib.moe_grouped_gemm_workspace_size(4096, 2560, 8192, 1) == 0   # case14: 512 tiles, two full rounds
     assert lib.moe_grouped_gemm_workspace_size(4096, 8192, 5120, 2) == (4 * (64 + 2) + 255) // 256 * 256
-    # router tf32 wgrad: [A_hi; A_hi; A_lo] and [B_hi; B_lo; B_hi] over 3M rows (+ fp32 planes when split)
-    assert lib.moe_router_wgrad_tf32_workspace_size(4096, 64, 1000) >= 3 * 4096 * (64 + 1000) * 2
+    # router tf32 wgrad: fp16 copies of both operands (M x (N + K)), the column exponents and column-max slabs
+    # (64 slabs of 64 rows for each operand here), and 8 fp32 planes of N x K (8 reduction chunks of 512 rows)
+    def up(b):
+        return (b + 255) // 256 * 256
+    want = (up(4096 * 64 * 2) + up(4096 * 1000 * 2) + up(64 * 4) + up(1000 * 4) + up(64 * 64 * 4) + up(64 * 1000 * 4)
+            + up(8 * 64 * 1000 * 4))
+    assert lib.moe_router_wgrad_tf32_workspace_size(4096, 64, 1000) == want
+    assert lib.moe_router_wgrad_tf32_workspace_size(0, 16, 24) > 0  # one plane: the output is written through it
 
 
 def test_status_strings():

@@ -1,10 +1,12 @@
 """GPU parity of the tf32 router backward GEMMs (case39 dgrad, case31 wgrad).
 
 The golden (reference_tf32, case39...:61-68 / case31...:61-68) multiplies tf32-rounded operands
-exactly and accumulates in fp32.  Here every tf32 product is three exact bf16 products (the
-dropped lo*lo term is below 2^-16 |a b|) accumulated in fp32 in another order, so the bound is
+exactly and accumulates in fp32.  Here (dgrad) every tf32 product is three exact bf16 products (the
+dropped lo*lo term is below 2^-16 |a b|), or (wgrad) one exact product of fp16 values scaled by a
+power of two per column, accumulated in fp32 in another order, so the bound is
 |ours - golden| <= 1e-4 * sum_k |a_k b_k| + 1e-5.  The cases' own checks against an explicit sum
-(case39: 1e-3, case31: 1e-2 absolute) are applied as written at full size.
+(case39: 1e-3, case31: 1e-2 absolute) are applied as written at full size; the full-size goldens
+are computed on the CPU.
 """
 from __future__ import annotations
 
@@ -50,10 +52,11 @@ def test_case39_full_size(pkg, dev):
     go, w = case.make_inputs(seed=0, device=dev)
     got = case.kernel_function(go, w)
     assert got.shape == (case.M, case.N) and got.dtype == torch.float32
-    a, b = ref_torch.round_tf32_rne(go), ref_torch.round_tf32_rne(w)
-    ref = a @ b
+    a, b = ref_torch.round_tf32_rne(go.cpu()), ref_torch.round_tf32_rne(w.cpu())
+    ref = ref_torch.router_dgrad_tf32(go.cpu(), w.cpu())
     bound = 1e-4 * (a.abs() @ b.abs()) + 1e-5
-    assert bool(((got - ref).abs() <= bound).all())
+    assert bool(((got.cpu() - ref).abs() <= bound).all())
+    a, b = a.to(dev), b.to(dev)
     rows = torch.tensor([0, case.M // 2, case.M - 1], device=dev)
     manual = (a[rows].double().unsqueeze(-1) * b.double().unsqueeze(0)).sum(dim=1)
     assert (got[rows].double() - manual).abs().max().item() <= 1e-3
@@ -64,10 +67,33 @@ def test_case31_full_size(pkg, dev):
     go, x = case.make_inputs(seed=0, device=dev)
     got = case.kernel_function(go, x)
     assert got.shape == (case.N, case.K) and got.dtype == torch.float32
-    a, b = ref_torch.round_tf32_rne(go), ref_torch.round_tf32_rne(x)
-    ref = a.t() @ b
+    a, b = ref_torch.round_tf32_rne(go.cpu()), ref_torch.round_tf32_rne(x.cpu())
+    ref = ref_torch.router_wgrad_tf32(go.cpu(), x.cpu())
     bound = 1e-4 * (a.abs().t() @ b.abs()) + 1e-5
-    assert bool(((got - ref).abs() <= bound).all())
+    assert bool(((got.cpu() - ref).abs() <= bound).all())
+    a, b = a.to(dev), b.to(dev)
     cols = torch.tensor([0, case.N // 2, case.N - 1], device=dev)
     manual = torch.stack([(a[:, c].double().unsqueeze(1) * b.double()).sum(dim=0) for c in cols.tolist()])
     assert (got[cols].double() - manual).abs().max().item() <= 1e-2
+
+
+def test_router_wgrad_tf32_columns_of_any_scale(pkg, dev):
+    # Each operand column is scaled by its own power of two into the fp16 range: columns of grad_output
+    # near 1e-30 and 1e18, and of inp near 1e-20 and 1e15, keep the relative accuracy of the others
+    # (the bound without its absolute term on the scaled rows and columns of dw).
+    M, N, K = 1000, 64, 520
+    g = torch.Generator().manual_seed(77)
+    go = torch.randn(M, N, generator=g)
+    x = torch.randn(M, K, generator=g)
+    go[:, 3] *= 1e-30
+    go[:, 5] *= 1e18
+    x[:, 7] *= 1e-20
+    x[:, 9] *= 1e15
+    got = pkg.ops.router_wgrad_tf32(go.to(dev), x.to(dev)).cpu().double()
+    ref = ref_torch.router_wgrad_tf32(go.double(), x.double())
+    absprod = ref_torch.round_tf32_rne(go).abs().t().double() @ ref_torch.round_tf32_rne(x).abs().double()
+    rel = (got - ref).abs() / absprod.clamp(min=1e-300)
+    assert bool(torch.isfinite(got).all())
+    for what, sel in (("row 3", rel[3]), ("row 5", rel[5]), ("column 7", rel[:, 7]), ("column 9", rel[:, 9]),
+                      ("all", rel)):
+        assert rel.numel() and bool((sel <= 1e-4).all()), f"{what}: worst relative error {sel.max().item():.3e}"
