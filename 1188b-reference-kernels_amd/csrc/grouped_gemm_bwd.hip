@@ -80,7 +80,27 @@ struct BwdArgs {
   const int16_t *order;     // wgrad (kOrder): the groups in the order the tiles take them
   const int32_t *order_rows;  // wgrad (kOrder): [2 G] the clamped row range (lo, hi) of order[i] at 2 i
   int *tails;               // dgrad ping-pong kernel: tail list (kTail* layout) or nullptr
+  int sweep_rows = 0;       // wgrad (kOrder): > 0 leaves the groups of at most this many rows to the sweep kernel
+  int sweep_len = 0;        // sweep kernel: tiles per unit (one fixed slab)
 };
+
+// Groups of the largest-first order with more than `limit` rows: the first
+// position whose clamped row count is at most `limit` (binary search over the
+// ordered row ranges; the counts do not increase along the order).
+__device__ __forceinline__ int long_group_count(const int32_t *order_rows, int G, int m32, int limit) {
+  int lo = 0, hi = G;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    const int r0 = min(max(ld_inv(order_rows, 2 * mid), 0), m32);
+    const int r1 = min(max(ld_inv(order_rows, 2 * mid + 1), r0), m32);
+    if (r1 - r0 <= limit) {
+      hi = mid;
+    } else {
+      lo = mid + 1;
+    }
+  }
+  return lo;
+}
 
 __device__ __forceinline__ int kc_swz(int row) { return (row >> 1) & 7; }
 // RM chunk swizzle of the 128-row kernel's 32 x 32 x 16 fragments (a half-wave
@@ -1131,6 +1151,11 @@ __device__ __forceinline__ void bwd_pp_body(const BwdArgs &p, char *smem, const 
       group_range(g, lo, hi);
     }
   };
+  // With a sweep limit the walker ends before the first group the sweep kernel takes.
+  int g_end = g_count;
+  if constexpr (kOrder) {
+    if (p.sweep_rows > 0) g_end = long_group_count(p.order_rows, g_count, m32, p.sweep_rows);
+  }
   int g_cur = 0, g_act = group_at(0), g_lo, g_hi;
   uint32_t tiles_before = 0;
   range_at(0, g_act, g_lo, g_hi);
@@ -1148,16 +1173,16 @@ __device__ __forceinline__ void bwd_pp_body(const BwdArgs &p, char *smem, const 
     // reverse, so a workgroup that took one of the larger tiles of a round
     // takes one of the smaller ones of the next (the patches stay whole).
     const uint32_t L = round * P32 + ((kOrder && (round & 1u)) ? P32 - 1u - L0 : L0);
-    while (g_cur < g_count && L >= tiles_before + mt_g * ntl) {
+    while (g_cur < g_end && L >= tiles_before + mt_g * ntl) {
       tiles_before += mt_g * ntl;
       ++g_cur;
-      if (g_cur < g_count) {
+      if (g_cur < g_end) {
         g_act = group_at(g_cur);
         range_at(g_cur, g_act, g_lo, g_hi);
         mt_g = row_tiles(g_lo, g_hi);
       }
     }
-    if (g_cur >= g_count) return false;
+    if (g_cur >= g_end) return false;
     const uint32_t q = L - tiles_before;
     const uint32_t per_grp = kGroupM * ntl;
     const uint32_t full = mt_g / kGroupM;
@@ -1450,6 +1475,244 @@ __global__ __launch_bounds__(512) void grouped_gemm_bwd_pp_kernel(BwdArgs p) {
       bwd_pp_body<kWgrad, kOrder, 128, kTails>(p, smem, &t);
     }
   }
+}
+
+// Weight gradient of the short groups (at most kSweepRows rows, e.g.
+// kernel_cases/case09_moe_grouped_gemm_fc1_wgrad.py:57-64: 40 groups of ~102
+// rows): dw[g] is large and its reduction short, so the work is the stream of
+// dw stores. The whole reduction (the group's rows, zeros from past the
+// operands' buffer resources up to 128) fits one LDS stage. A unit is (group,
+// range of swept tiles, fixed tile): the fixed operand's 256-column slab
+// (64 KiB) stays in LDS while the unit's tiles sweep the other operand's
+// 128-column slabs (32 KiB, three slots, DMA'd two tiles ahead). Units are
+// numbered with the fixed tile fastest and dealt round-robin so that the
+// workgroups of an XCD (consecutive numbers) take the same group and range
+// with neighbouring fixed tiles: they sweep the same slabs at about the same
+// time, and the slabs come from L2. A tile's stores are issued after the DMA
+// of the slab two tiles ahead, and the wait before the next tile (for the
+// next slab) leaves the stores of this tile and the one before in flight.
+// kFixD: dy's slab is fixed (tile 256 dw rows x 128 columns, sweeping x over
+// K); else x's (128 x 256, sweeping dy over N). The host picks the
+// orientation and the unit length (p.sweep_len) that spread the tiles most
+// evenly over the workgroups.
+constexpr int kSweepRows = 128;
+
+template <bool kFixD>
+__global__ __launch_bounds__(512) void grouped_gemm_wgrad_sweep_kernel(BwdArgs p) {
+  constexpr int kDN = kFixD ? 256 : 128;  // dw rows of a tile (dy columns)
+  constexpr int kXK = kFixD ? 128 : 256;  // dw columns of a tile (x columns)
+  constexpr int kDRow = kDN * 2, kXRow = kXK * 2;  // LDS row bytes of the dy and x slabs
+  constexpr int kFixRow = 512, kSwRow = 256;
+  constexpr int kFixBytes = kSweepRows * kFixRow, kSwBytes = kSweepRows * kSwRow;
+  constexpr int kWN = kDN / 64;                    // wavefronts along the dw rows (64 x 64 each)
+  constexpr int kFixDma = kFixBytes / 1024 / 8, kSwDma = kSwBytes / 1024 / 8;  // 1 KiB blocks per wavefront
+  constexpr int kStores = 8;                       // 16-byte stores per lane per tile
+  static_assert(kWN * (kXK / 64) == 8, "8 wavefronts");
+  static_assert(kFixBytes + 3 * kSwBytes <= 160 * 1024, "LDS");
+  static_assert(kStores + kSwDma + kStores <= 63 && kFixDma + 2 * kSwDma <= 63, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) char smem[kFixBytes + 3 * kSwBytes];
+  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_char *)smem));
+  const uint32_t fix_lds = lds_base, sw_lds = lds_base + kFixBytes;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int wn = wave % kWN, wk = wave / kWN;
+  const int m32 = static_cast<int>(p.M), g_count = static_cast<int>(p.G);
+  const int N = static_cast<int>(p.N), K = static_cast<int>(p.K);
+
+  const int first = long_group_count(p.order_rows, g_count, m32, kSweepRows);
+  const int n_fix = static_cast<int>(kFixD ? ceil_div(N, kDN) : ceil_div(K, kXK));
+  const int n_sw = static_cast<int>(kFixD ? ceil_div(K, kXK) : ceil_div(N, kDN));
+  const int len = max(1, min(p.sweep_len, n_sw));
+  const int n_rng = (n_sw + len - 1) / len;
+  const int64_t units = static_cast<int64_t>(g_count - first) * n_rng * n_fix;
+  const int64_t P = gridDim.x, b = blockIdx.x;
+  const int64_t r = (b % 8) * (P / 8) + b / 8;  // consecutive numbers on one XCD
+
+  int ln = lane;
+  asm volatile("" : "+v"(ln));
+  // ---- DMA: slab rows of kRow bytes; 1 KiB block B holds rows B * (1024 / kRow) ..; lane l writes row
+  // l / (kRow / 16) of the block, chunk position l % (kRow / 16), holding logical chunk position ^
+  // rm16_swz(row); wavefront w's blocks are w + 8 j (the swizzle of a lane's row does not depend on j).
+  auto lane_off = [&](int row_bytes, int gstride) -> int {
+    const int cpr = row_bytes / 16, rpb = 1024 / row_bytes;
+    const int row = wave * rpb + ln / cpr;
+    const int lchunk = (ln % cpr) ^ rm16_swz(row);
+    return row * gstride + lchunk * 16;
+  };
+  const int fix_stride = (kFixD ? N : K) * 2, sw_stride = (kFixD ? K : N) * 2;
+  const int fix_off = lane_off(kFixRow, fix_stride), sw_off = lane_off(kSwRow, sw_stride);
+  __amdgpu_buffer_rsrc_t rfix = make_rsrc(p.a, 0u), rsw = make_rsrc(p.b, 0u);
+  auto dma_fixed = [&](int fi) {
+    int o = fix_off;
+    asm volatile("" : "+v"(o));
+#pragma unroll
+    for (int j = 0; j < kFixDma; ++j)
+      dma16b(rfix, (lds_void *)(uintptr_t)(fix_lds + (wave + 8 * j) * 1024), o + j * 8 * (1024 / kFixRow) * fix_stride,
+             fi * (kFixD ? kDN : kXK) * 2);
+  };
+  auto dma_swept = [&](int wi, int slot) {
+    int o = sw_off;
+    asm volatile("" : "+v"(o));
+#pragma unroll
+    for (int j = 0; j < kSwDma; ++j)
+      dma16b(rsw, (lds_void *)(uintptr_t)(sw_lds + slot * kSwBytes + (wave + 8 * j) * 1024),
+             o + j * 8 * (1024 / kSwRow) * sw_stride, wi * (kFixD ? kXK : kDN) * 2);
+  };
+
+  // ---- fragments (16-lane group rg reads reduction rows 8 rg .. 8 rg + 7)
+  const int rg = lane >> 4, rj = (lane >> 2) & 3, rq = lane & 3;
+  const uint32_t rm_in = ((rq >> 1) << 4) + (rq & 1) * 8;
+  uint32_t rmx = static_cast<uint32_t>((rj << 1) | (rg & 1)) << 5;
+  asm volatile("" : "+v"(rmx));
+  const uint32_t fd0 = (8 * rg + rj) * kDRow + rm_in, fx0 = (8 * rg + rj) * kXRow + rm_in;
+  f32x4_t acc[4][4];
+  // acc[i][j] = dw rows wn * 64 + 16 i .., columns wk * 64 + 16 j .. of the tile, with the MFMA operands of
+  // the ping-pong kernel (x fragment first): every dw element is the same MFMA sequence.
+  auto compute = [&](int slot) {
+    const uint32_t d_lds = (kFixD ? fix_lds : sw_lds + slot * kSwBytes) + fd0;
+    const uint32_t x_lds = (kFixD ? sw_lds + slot * kSwBytes : fix_lds) + fx0;
+#pragma unroll
+    for (int ks = 0; ks < kSweepRows / 32; ++ks) {
+      bf16x8 fa[4], fb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        fa[i] = read_rm_frag_rows<kDRow>(d_lds + ks * 32 * kDRow + ((static_cast<uint32_t>(wn * 4 + i) * 32u) ^ rmx));
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        fb[j] = read_rm_frag_rows<kXRow>(x_lds + ks * 32 * kXRow + ((static_cast<uint32_t>(wk * 4 + j) * 32u) ^ rmx));
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = mma16<false>(fb[j], fa[i], ks == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : acc[i][j]);
+    }
+  };
+  // Epilogue: register r of lane l in block (i, j) holds dw row wn * 64 + i * 16 + l % 16 and column
+  // wk * 64 + j * 16 + 4 (l / 16) + r of the tile; bf16 RNE, v_permlane16_swap pairs blocks j, j + 1 so
+  // each lane stores 8 consecutive columns (16 bytes). Rows past N lie past the resource, columns past K
+  // get an offset past it.
+  const uint32_t ld = static_cast<uint32_t>(K) * 2u;
+  auto epilogue = [&](int g, int nt, int kt) {
+    const __amdgpu_buffer_rsrc_t ro =
+        make_rsrc(static_cast<const uint16_t *>(p.out) + static_cast<int64_t>(g) * N * K, static_cast<uint32_t>(N) * ld);
+    const int eq = ln >> 4;
+    const int col0 = kt * kXK + wk * 64 + (eq & 1) * 16 + (eq >> 1) * 8;
+    const uint32_t row0 = static_cast<uint32_t>(nt * kDN + wn * 64 + (ln & 15));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int jp = 0; jp < 4; jp += 2) {
+        uint32_t wd[2][2];
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+          const bf16x2 a0 = {(__bf16)acc[i][jp + d][0], (__bf16)acc[i][jp + d][1]};
+          const bf16x2 a1 = {(__bf16)acc[i][jp + d][2], (__bf16)acc[i][jp + d][3]};
+          wd[d][0] = __builtin_bit_cast(uint32_t, a0);
+          wd[d][1] = __builtin_bit_cast(uint32_t, a1);
+        }
+        u32x4 o;
+#if defined(__HIP_DEVICE_COMPILE__)
+        const auto s0 = __builtin_amdgcn_permlane16_swap(wd[0][0], wd[1][0], false, false);
+        const auto s1 = __builtin_amdgcn_permlane16_swap(wd[0][1], wd[1][1], false, false);
+        o = u32x4{s0[0], s1[0], s0[1], s1[1]};
+#else
+        o = u32x4{0u, 0u, 0u, 0u};
+#endif
+        const int gcol = col0 + jp * 16;
+        const uint32_t off = gcol < K ? (row0 + i * 16) * ld + static_cast<uint32_t>(gcol) * 2u : kNoAccess;
+#if defined(__HIP_DEVICE_COMPILE__)
+        __builtin_amdgcn_raw_buffer_store_b128(o, ro, static_cast<int>(off), 0, 0);
+#else
+        (void)off;
+        (void)ro;
+        (void)o;
+#endif
+      }
+    }
+  };
+
+  // ---- units r, r + P, ...: (group position, range, fixed tile), the fixed tile fastest
+  for (int64_t u = r; u < units; u += P) {
+    const int per_g = n_rng * n_fix;
+    const int gi = first + static_cast<int>(u / per_g);
+    const int rem = static_cast<int>(u - static_cast<int64_t>(gi - first) * per_g);
+    const int rng = rem / n_fix, fi = rem - rng * n_fix;
+    const int w0 = rng * len, n = min(len, n_sw - w0);
+    const int g = min(max(ld_inv(p.order, gi), 0), g_count - 1);
+    const int lo = min(max(ld_inv(p.order_rows, 2 * gi), 0), m32);
+    const int hi = min(max(ld_inv(p.order_rows, 2 * gi + 1), lo), m32);
+    // Rows past the group's end lie past the resources: zeros.
+    const uint32_t rows = static_cast<uint32_t>(hi - lo);
+    const __amdgpu_buffer_rsrc_t rd = make_rsrc(p.a + static_cast<int64_t>(lo) * N, rows * static_cast<uint32_t>(N) * 2u);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.b + static_cast<int64_t>(lo) * K, rows * static_cast<uint32_t>(K) * 2u);
+    rfix = kFixD ? rd : rx;
+    rsw = kFixD ? rx : rd;
+    // The previous unit is done (its stores included) and every wavefront has left its slabs.
+    wait_dma();
+    barrier();
+    dma_fixed(fi);
+    dma_swept(w0, 0);
+    if (n > 1) dma_swept(w0 + 1, 1);
+    wait_dma();
+    barrier();
+    int slot = 0;
+    for (int i = 0; i < n; ++i) {
+      const bool ahead = i + 2 < n;
+      const int slot2 = slot == 0 ? 2 : slot - 1;  // (i + 2) % 3: the slot tile i - 1 read (barrier since)
+      if (ahead) dma_swept(w0 + i + 2, slot2);
+      compute(slot);
+      const int wi = w0 + i;
+      epilogue(g, kFixD ? fi : wi, kFixD ? wi : fi);
+      if (i + 1 < n) {
+        // Tile i + 1's slab has landed (issued before the stores of tile i - 1); those stores, the slab of
+        // tile i + 2 and this tile's stores may be in flight.
+        if (ahead) {
+          wait_vm_n<kStores + kSwDma + kStores>();
+        } else {
+          wait_vm_n<kStores + kStores>();
+        }
+        barrier();
+      }
+      slot = slot == 2 ? 0 : slot + 1;
+    }
+  }
+}
+
+template <bool kFixD>
+void launch_sweep(const BwdArgs &p, hipStream_t s) {
+  const int64_t grid = std::max<int64_t>(8, num_cus() / 8 * 8);
+  grouped_gemm_wgrad_sweep_kernel<kFixD><<<dim3(static_cast<uint32_t>(grid)), dim3(512), 0, s>>>(p);
+}
+
+// Orientation and unit length of the sweep: the fewest tiles on the busiest workgroup (each unit also costs
+// about 1.5 tiles of slab loading), counting every group as short.
+struct SweepPlan {
+  bool fixd;
+  int len;
+};
+SweepPlan sweep_plan(int64_t N, int64_t K, int64_t G, int64_t cus) {
+  SweepPlan best{K >= N, 1};
+  double best_work = -1.0;
+  const int64_t P = std::max<int64_t>(8, cus / 8 * 8);
+  for (int f = 0; f < 2; ++f) {
+    const bool fixd = f == 0;
+    const int64_t n_fix = fixd ? ceil_div(N, 256) : ceil_div(K, 256);
+    const int64_t n_sw = fixd ? ceil_div(K, 128) : ceil_div(N, 128);
+    const int lens[] = {8, 10, 12, 16, 20, 24, 32, 40, 48, 64};
+    for (int li = -1; li < 10; ++li) {
+      const int64_t L = li < 0 ? n_sw : lens[li];
+      if (L > n_sw || L < 1) continue;
+      const int64_t units = G * ceil_div(n_sw, L) * n_fix;
+      const int64_t per = ceil_div(units, P);
+      const double work = static_cast<double>(per) * (static_cast<double>(L) + 1.5);
+      if (best_work < 0 || work < best_work) {
+        best_work = work;
+        best = {fixd, static_cast<int>(L)};
+      }
+    }
+  }
+  return best;
 }
 
 template <bool kWgrad, int kOut = 0, bool kSplit = false, bool kOrder = false, bool kF16 = false>
@@ -1947,6 +2210,18 @@ int moe_grouped_gemm_wgrad(const moe_bf16_t *dy, const moe_bf16_t *x, int64_t M_
                                                       order_rows);
     p.order = order;
     p.order_rows = order_rows;
+    // Groups averaging under 256 rows: the groups of at most 128 rows go to the sweep kernel (the dw store
+    // stream), the rest to the ping-pong kernel, whose walker ends where the sweep's groups begin.
+    if (MOE_GEMM_BWD_PINGPONG && M_total < 256 * G && N < (int64_t(1) << 22) && K < (int64_t(1) << 22)) {
+      const SweepPlan sp = sweep_plan(N, K, G, num_cus());
+      p.sweep_rows = kSweepRows;
+      p.sweep_len = sp.len;
+      if (sp.fixd) {
+        launch_sweep<true>(p, s);
+      } else {
+        launch_sweep<false>(p, s);
+      }
+    }
     if (MOE_GEMM_BWD_PINGPONG) {
       launch_pp<true, true>(p, tiles, s);
     } else {

@@ -345,7 +345,11 @@ int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, con
  *   int32 row range) and the GEMM's tiles take them in that order, dealt to
  *   the workgroups in reverse on every other round, which evens out the work
  *   per workgroup when the group sizes are skewed; each tile's result is the
- *   same bit for bit either way. The size is 0 (no order) for one group. */
+ *   same bit for bit either way. When the groups average under 256 rows, the
+ *   groups of at most 128 rows (the end of that order) are computed by a
+ *   kernel that keeps their whole reduction in LDS and sweeps the output
+ *   tiles (the dw store stream), again the same bits. The size is 0 (no
+ *   order) for one group. */
 size_t moe_grouped_gemm_wgrad_workspace_size(int64_t M_total, int64_t N, int64_t K, int64_t G);
 int moe_grouped_gemm_wgrad(const moe_bf16_t *dy, const moe_bf16_t *x, int64_t M_total, int64_t N,
                            int64_t K, int64_t G, const int32_t *group_offsets, moe_bf16_t *dw,

@@ -242,6 +242,45 @@ def test_wgrad_group_order_matches_stable_sort(pkg, dev, G):
     assert_bits_equal(dw, plain, "wgrad with the workspace order vs by index")
 
 
+@pytest.mark.parametrize("sizes,N,K", [
+    ([3, 0, 700, 41, 128, 129, 1, 64, 100, 5] * 2, 264, 520),   # long groups mixed in, N and K tails
+    ([3, 0, 700, 41, 128, 129, 1, 64, 100, 5] * 2, 520, 264),
+    ([102] * 8 + [103] * 4, 384, 1032),                          # the case05/09 group sizes, a K tail
+    ([102] * 8 + [103] * 4, 1032, 384),
+    ([7] * 300, 136, 200),                                       # many tiny groups: units over many groups
+    ([0, 0, 0], 136, 200),                                       # only empty groups: zeros
+])
+def test_wgrad_sweep_short_groups(pkg, dev, sizes, N, K):
+    # Groups averaging under 256 rows: with the workspace the groups of at most 128 rows run in the
+    # sweep kernel (the whole reduction in one LDS stage) and the longer ones in the ping-pong kernel.
+    # Each output element is the same sequence of MFMAs as without the workspace (ping-pong only), so
+    # dw is bit for bit the same; against the CPU oracle at the task tolerance; nothing past dw written.
+    lib, ptr = pkg._lib.lib(), pkg._lib.ptr
+    G, M = len(sizes), sum(sizes)
+    assert M < 256 * G
+    g = torch.Generator().manual_seed(M + 7 * N + K)
+    dy = torch.randn(max(M, 1), N, generator=g).to(torch.bfloat16).to(dev)[:M]
+    x = torch.randn(max(M, 1), K, generator=g).to(torch.bfloat16).to(dev)[:M]
+    offs = _offsets(sizes, dev)
+    buf = torch.full((G * N * K + 8192,), 3.0, dtype=torch.bfloat16, device=dev)
+    swept = buf[:G * N * K].view(G, N, K)
+    ws = torch.full((lib.moe_grouped_gemm_wgrad_workspace_size(M, N, K, G),), 0x55, dtype=torch.uint8, device=dev)
+    pkg.ops.grouped_gemm_wgrad(dy, x, offs, out=swept, workspace=ws)
+    again = pkg.ops.grouped_gemm_wgrad(dy, x, offs, workspace=ws)
+    plain = torch.empty_like(swept)
+    rc = lib.moe_grouped_gemm_wgrad(ptr(dy), ptr(x), M, N, K, G, ptr(offs), ptr(plain), None, 0,
+                                    pkg._lib.stream_handle())
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.all(buf[G * N * K:] == 3.0), "written past dw"
+    assert_bits_equal(swept, plain, "wgrad sweep + ping-pong vs ping-pong only")
+    assert_bits_equal(again, swept, "wgrad sweep, second call")
+    _check(swept, ref_torch.grouped_gemm_wgrad_fp32(dy.cpu(), x.cpu(), sizes), f"wgrad sweep sizes={sizes}")
+    for gi, m in enumerate(sizes):
+        if m == 0:
+            assert torch.count_nonzero(swept[gi]) == 0
+
+
 def test_wgrad_one_row_groups_exact(pkg, dev):
     # A group of one row is the outer product dy[r] x[r]^T: exact in fp32, one rounding.
     g = torch.Generator().manual_seed(91)
