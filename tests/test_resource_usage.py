@@ -38,5 +38,9 @@ def test_gemm_kernels_do_not_spill():
     # with and without them, wgrad, ordered wgrad
     assert len(pingpong) == 12, pingpong
     assert all(v.get("occ") == 2 and v.get("vgpr", 0) + v.get("agpr", 0) <= 256 for _, v in pingpong), pingpong
+    # the short-group wgrad sweep: two wavefronts per SIMD as well (both orientations)
+    sweep = [(name, v) for name, v in rows if "_sweep_kernel" in name]
+    assert len(sweep) == 2 and all(v.get("occ") == 2 and v.get("vgpr", 0) + v.get("agpr", 0) <= 256 for _, v in sweep), sweep
     assert all(v.get("agpr") in (128, 256) for name, v in rows if "gemm" in name and "kernel" in name and "sum_planes" not in name
-               and "split" not in name and "tails_init" not in name and "_pp_kernel" not in name)
+               and "split" not in name and "tails_init" not in name and "_pp_kernel" not in name
+               and "_sweep_kernel" not in name)
