@@ -78,9 +78,11 @@ constexpr uint32_t kNoAccess = 0x80000000u;
 
 // 16-byte buffer -> LDS copy: lane i writes bytes [16 i, 16 i + 16) of the 1 KiB
 // block at `lds` (wave-uniform); the global address is rsrc base + voff + soff.
+// kAux: cache policy bits (2: nt, a streaming load whose lines are not kept for reuse).
+template <int kAux = 0>
 __device__ __forceinline__ void dma16b(__amdgpu_buffer_rsrc_t rsrc, lds_void *lds, int voff, int soff) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds, 16, voff, soff, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds, 16, voff, soff, 0, kAux);
 #else
   (void)rsrc; (void)lds; (void)voff; (void)soff;
 #endif

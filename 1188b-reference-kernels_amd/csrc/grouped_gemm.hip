@@ -55,6 +55,7 @@
 // lane's DMA offset is that source row's, so the permuted A operand of fc1 is
 // read straight from the token rows and never materialised.
 #include <algorithm>
+#include <type_traits>
 
 #include "gemm_device.h"
 
@@ -68,6 +69,21 @@ constexpr int kBM = 256, kBN = 256;
 #define MOE_GEMM_GROUP_M 8
 #endif
 constexpr int kGroupM = MOE_GEMM_GROUP_M;         // row tiles per tile-order group
+#ifndef MOE_GEMM_FWD128
+#define MOE_GEMM_FWD128 1
+#endif
+#ifndef MOE_GEMM_FWD128_NB
+#define MOE_GEMM_FWD128_NB 0  // column tile width / 32 of the 128-row forward kernel (0: the host picks it)
+#endif
+#ifndef MOE_GEMM_FWD128_SA
+#define MOE_GEMM_FWD128_SA 0  // ring stages of the 128-row forward kernel: A (0: 5, 4 from 192 columns),
+#endif
+#ifndef MOE_GEMM_FWD128_SB
+#define MOE_GEMM_FWD128_SB 0  // B (0: 4, fewer where the LDS holds no more)
+#endif
+#ifndef MOE_GEMM_FWD128_NT
+#define MOE_GEMM_FWD128_NT 1  // the 128-row forward kernel loads the weights non-temporally (each is used by one tile)
+#endif
 #ifndef MOE_GEMM_PINGPONG
 #define MOE_GEMM_PINGPONG 1
 #endif
@@ -1456,6 +1472,247 @@ __global__ __launch_bounds__(256) void split_sum_kernel(GemmArgs p) {
   }
 }
 
+// Forward GEMM for short groups (plain epilogue, A rows in place; e.g.
+// kernel_cases/case03_moe_grouped_gemm_fc1_fwd.py: 40 groups of ~102 rows,
+// every weight element used by ~102 rows, so the stream of w is the work):
+// tiles of 128 rows x 32 kNB columns (a group's rows in ceil(m / 128) row
+// tiles, N in column tiles), numbered group by group and dealt round-robin to
+// persistent workgroups so an XCD takes neighbouring column tiles of a group
+// (its rows come from L2). 8 wavefronts, on each SIMD one computing (64 rows x
+// 16 kNB columns as 4 x kNB blocks of v_mfma_f32_16x16x32_bf16, the weight
+// fragment first and K ascending: the MFMA sequence of the ping-pong kernel,
+// so the output is bit-identical) and one loading: two DMA the tile's rows
+// into a ring of kSA stages, two the weight rows into a ring of kSB stages
+// (a wavefront's loads complete in issue order, so each operand keeps its own
+// lookahead; the weights load non-temporally, each is used by one tile when
+// the groups have at most 128 rows). One barrier per step; the stages of a
+// workgroup's tiles form one stream, so the next tile's first stages load
+// while the last tile's results are stored. The host picks kNB (the column
+// tile width) that spreads the tiles most evenly over the workgroups. Output:
+// 4 consecutive bf16 columns per lane and block, one 8-byte store; rows past
+// the group's end lie past the store resource, columns past N get an offset
+// past it.
+template <int kNB, bool kNtW = MOE_GEMM_FWD128_NT>
+__global__ __launch_bounds__(512) void grouped_gemm_fwd128_kernel(GemmArgs p) {
+  constexpr int kTM = 128;
+  constexpr int kTN = 32 * kNB;
+  constexpr int kABytes = kTM * kRowBytes;       // 16 KiB
+  constexpr int kBBytes = kTN * kRowBytes;
+  constexpr int kSA = MOE_GEMM_FWD128_SA ? MOE_GEMM_FWD128_SA : (kNB <= 5 ? 5 : 4);
+  constexpr int kSBFit = (160 * 1024 - kSA * kABytes) / kBBytes;
+  constexpr int kSBCap = MOE_GEMM_FWD128_SB ? MOE_GEMM_FWD128_SB : 4;
+  constexpr int kSB = kSBFit > kSBCap ? kSBCap : kSBFit;
+  constexpr int kDmaA = kABytes / 1024 / 2, kDmaB = kBBytes / 1024 / 2;  // per loading wavefront
+  static_assert(kSA >= 3 && kSB >= 3 && kSA * kABytes + kSB * kBBytes <= 160 * 1024, "LDS budget");
+  static_assert((kSA - 1) * kDmaA <= 63 && (kSB - 1) * kDmaB <= 63, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) char smem[kSA * kABytes + kSB * kBBytes];
+  lds_char *const sbase = (lds_char *)smem;
+  const uint32_t a_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sbase));
+  const uint32_t b_lds = a_lds + kSA * kABytes;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  // ---- roles: the first wavefront of each SIMD computes (index = its SIMD), the second loads (SIMD 0 and
+  // 1: the tile's rows, 2 and 3: weight rows), read from HW_ID and exchanged through LDS.
+  int role_simd, loader;
+  {
+    const int simd = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_s_getreg((1 << 11) | (4 << 6) | 4)) & 3;
+    volatile int *sid = reinterpret_cast<volatile int *>(smem);
+    if (lane == 0) sid[wave] = simd;
+    __syncthreads();
+    int before = 0, per_simd[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      const int sv = sid[w] & 3;
+      per_simd[sv] += 1;
+      before += (sv == simd) && (w < wave);
+    }
+    __syncthreads();
+    const bool ok = per_simd[0] == 2 && per_simd[1] == 2 && per_simd[2] == 2 && per_simd[3] == 2;
+    role_simd = __builtin_amdgcn_readfirstlane(ok ? simd : (wave & 3));
+    loader = __builtin_amdgcn_readfirstlane(ok ? before : (wave >> 2));
+  }
+  const int64_t K = p.K, N = p.N;
+  const int ktiles = static_cast<int>(K / kBK);
+  const uint32_t row_bytes = static_cast<uint32_t>(K) * 2u;
+  const int m32 = static_cast<int>(p.M), g_count = static_cast<int>(p.G);
+  const int ntl = static_cast<int>((N + kTN - 1) / kTN);
+
+  // ---- tile walker (every wavefront walks the same tiles): group by group, row tile-major
+  struct Tile {
+    int g, i0, rows, nt;
+  };
+  int g_cur = 0, g_lo = 0, g_hi = 0, mt_g = 0;
+  int64_t tiles_before = 0;
+  auto range = [&](int g) {
+    g_lo = min(max(ld_inv(p.offsets, g), 0), m32);
+    g_hi = min(max(ld_inv(p.offsets, g + 1), g_lo), m32);
+    mt_g = (g_hi - g_lo + kTM - 1) / kTM;
+  };
+  range(0);
+  const int64_t P = gridDim.x, b = blockIdx.x;
+  const int64_t r0 = (b % 8) * (P / 8) + b / 8;
+  auto find = [&](int64_t round, Tile &t) -> bool {
+    const int64_t L = round * P + r0;
+    while (g_cur < g_count && L >= tiles_before + static_cast<int64_t>(mt_g) * ntl) {
+      tiles_before += static_cast<int64_t>(mt_g) * ntl;
+      if (++g_cur < g_count) range(g_cur);
+    }
+    if (g_cur >= g_count) return false;
+    const int q = static_cast<int>(L - tiles_before);
+    const int mt = q / ntl;
+    t.g = g_cur;
+    t.i0 = g_lo + mt * kTM;
+    t.rows = min(kTM, g_hi - t.i0);
+    t.nt = q - mt * ntl;
+    return true;
+  };
+
+  Tile t;
+  if (!find(0, t)) return;  // no tiles: every wavefront leaves before the first barrier
+
+  if (loader) {
+    const bool is_a = role_simd < 2;
+    const int li = role_simd & 1;
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    auto tile_rsrc = [&](const Tile &u, bool a) {
+      // Rows past the tile's rows / past N lie past the resource: zeros.
+      return a ? make_rsrc(p.a + static_cast<int64_t>(u.i0) * K, static_cast<uint32_t>(u.rows) * row_bytes)
+               : make_rsrc(p.w + static_cast<int64_t>(u.g) * N * K + static_cast<int64_t>(u.nt) * kTN * K,
+                           static_cast<uint32_t>(min<int64_t>(kTN, N - static_cast<int64_t>(u.nt) * kTN)) * row_bytes);
+    };
+    // The stages of this workgroup's tiles form one stream (tile by tile, K ascending), so the rings run on
+    // from one tile into the next: the next tile's first stages load while the last one's results are stored.
+    auto run = [&](auto is_a_c) {
+      constexpr bool kA = decltype(is_a_c)::value;
+      constexpr int kS = kA ? kSA : kSB;
+      constexpr int kN = kA ? kDmaA : kDmaB;
+      constexpr int kSlot = kA ? kABytes : kBBytes;
+      const uint32_t ring = (kA ? a_lds : b_lds) + li * kN * 1024;
+      const int r_0 = li * kN * 8 + (ln >> 3);  // row of this wavefront's 1 KiB block j (8 rows): r_0 + 8 j
+      int off[kN];
+#pragma unroll
+      for (int j = 0; j < kN; ++j) {
+        const int r = r_0 + j * 8;
+        off[j] = static_cast<int>(static_cast<uint32_t>(r) * row_bytes + static_cast<uint32_t>(((ln & 7) ^ swz(r)) << 4));
+      }
+      __amdgpu_buffer_rsrc_t rs = tile_rsrc(t, kA);
+      int64_t round = 0;
+      int kt = 0;
+      bool more = true;
+      int64_t issued = 0, end = INT64_MAX;  // stages issued; stages of all tiles (known once the last is issued)
+      // The next stage of the stream (its resource and K step); past the last one, the last stage again (the
+      // same number of loads in flight in every step; they land in slots nothing reads any more).
+      struct Src {
+        __amdgpu_buffer_rsrc_t rs;
+        int k;
+      };
+      auto advance = [&]() -> Src {
+        const Src v{rs, more ? kt : ktiles - 1};
+        ++issued;
+        if (more && ++kt == ktiles) {
+          kt = 0;
+          more = find(++round, t);
+          if (more) rs = tile_rsrc(t, kA);
+          else end = issued;
+        }
+        return v;
+      };
+      constexpr int kAux = (!kA && kNtW) ? 2 : 0;
+      auto one = [&](int slot) {
+        const Src v = advance();
+        const uint32_t dst = ring + slot * kSlot;
+#pragma unroll
+        for (int j = 0; j < kN; ++j) dma16b<kAux>(v.rs, (lds_void *)(uintptr_t)(dst + j * 1024), off[j], v.k * kBK * 2);
+      };
+      for (int st = 0; st < kS - 1; ++st) one(st);
+      wait_vm_n<(kS - 2) * kN>();  // stage 0 has landed
+      barrier();
+      int slot = kS - 1;
+      // Step s: the computing wavefronts read stage s; its barrier is passed once stage s + 1 has landed.
+      // `end` is known here: `issued` runs kS - 1 stages ahead of s.
+      for (int64_t s = 0; s < end; ++s) {
+        one(slot);  // into the slot of stage s - 1, read before the last barrier
+        slot = slot + 1 == kS ? 0 : slot + 1;
+        wait_vm_n<(kS - 2) * kN>();
+        barrier();
+      }
+      wait_dma();
+    };
+    if (is_a) run(std::true_type{});
+    else run(std::false_type{});
+    return;
+  }
+
+  const int wr = role_simd >> 1, wc = role_simd & 1;
+  const int frow = lane & 15, fq = lane >> 4;
+  auto frag_addr = [&](uint32_t slot_base, int r, int ks) {
+    return slot_base + r * kRowBytes + ((((ks << 2) | fq) ^ swz(r)) << 4);
+  };
+  bf16x8 fa[2][4], fb[2][kNB];
+  int sa = 0, sb = 0;  // ring slots of the stage being read
+  auto read_half = [&](int ks, int buf) {
+    const uint32_t ab = a_lds + sa * kABytes, bb = b_lds + sb * kBBytes;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      fa[buf][i] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)frag_addr(ab, wr * 64 + i * 16 + frow, ks));
+#pragma unroll
+    for (int j = 0; j < kNB; ++j)
+      fb[buf][j] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)frag_addr(bb, wc * 16 * kNB + j * 16 + frow, ks));
+  };
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  f32x4 acc[4][kNB];
+  auto mfma_half = [&](int buf, bool zero) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < kNB; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[buf][j], fa[buf][i], zero ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j],
+                                                           0, 0, 0);
+  };
+  const uint32_t ld = static_cast<uint32_t>(p.ncols) * 2u;
+  barrier();  // stage 0 has landed
+  for (int64_t round = 0;;) {
+    read_half(0, 0);
+    for (int kt = 0; kt < ktiles; ++kt) {
+      read_half(1, 1);
+      mfma_half(0, kt == 0);
+      __builtin_amdgcn_sched_barrier(0);
+      wait_lds();  // this wavefront's reads of stage kt are done before its slot can be refilled
+      barrier();   // the next stage has landed
+      sa = sa + 1 == kSA ? 0 : sa + 1;
+      sb = sb + 1 == kSB ? 0 : sb + 1;
+      if (kt + 1 < ktiles) read_half(0, 0);
+      mfma_half(1, false);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // acc[i][j] register r of lane l: row wr 64 + i 16 + l % 16, column wc 16 kNB + j 16 + 4 (l / 16) + r.
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(p.out + static_cast<int64_t>(t.i0) * p.ncols, static_cast<uint32_t>(t.rows) * ld);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t orow = static_cast<uint32_t>(wr * 64 + i * 16 + frow);
+#pragma unroll
+      for (int j = 0; j < kNB; ++j) {
+        const int64_t col = static_cast<int64_t>(t.nt) * kTN + wc * 16 * kNB + j * 16 + fq * 4;
+        const bf16x2 lo = {(__bf16)acc[i][j][0], (__bf16)acc[i][j][1]};
+        const bf16x2 hi = {(__bf16)acc[i][j][2], (__bf16)acc[i][j][3]};
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 v = {__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+        const uint32_t off = col < N ? orow * ld + static_cast<uint32_t>(col) * 2u : kNoAccess;
+#if defined(__HIP_DEVICE_COMPILE__)
+        __builtin_amdgcn_raw_buffer_store_b64(v, ro, static_cast<int>(off), 0, 0);
+#else
+        (void)off;
+        (void)v;
+        (void)ro;
+#endif
+      }
+    }
+    if (!find(++round, t)) break;
+  }
+}
+
 }  // namespace
 }  // namespace moe
 
@@ -1494,6 +1751,20 @@ SplitPlan split_plan(int64_t M_total, int64_t K, int64_t N, int64_t G, int64_t c
   sp.steps = static_cast<int>(S / ways);
   sp.bytes = static_cast<size_t>(L * ways) * 65536 * sizeof(float);
   return sp;
+}
+
+// Column tile width (32 kNB) of the 128-row forward kernel: tiles of groups of the mean row count, the
+// rounds over P workgroups priced at their width plus a fixed 32 columns (the tile's A rows and stores).
+int fwd128_nb(int64_t M_total, int64_t N, int64_t G, int64_t P) {
+  const int64_t mt = moe::ceil_div(moe::ceil_div(M_total, G), 128);
+  int best = 4;
+  int64_t best_cost = INT64_MAX;
+  for (int nb : {4, 5, 6}) {
+    const int64_t tn = 32 * nb;
+    const int64_t cost = moe::ceil_div(G * mt * moe::ceil_div(N, tn), P) * (tn + 32);
+    if (cost < best_cost) best_cost = cost, best = nb;
+  }
+  return best;
 }
 
 int launch_grouped_gemm(const char *fn, const moe_bf16_t *a, int64_t a_src_rows, const int32_t *a_rows,
@@ -1551,6 +1822,17 @@ int launch_grouped_gemm(const char *fn, const moe_bf16_t *a, int64_t a_src_rows,
   const bool pipe = K > 2 * kBK && p.vec_out && ncols < (int64_t(1) << 22) && (!gather || M_total < (int64_t(1) << 29));
   // The ping-pong kernel: the same conditions, whole K steps and row numbers in 31 bits.
   const bool pingpong = MOE_GEMM_PINGPONG && pipe && K % kBK == 0 && M_total < (int64_t(1) << 31);
+  // Groups of at most 128 rows on average, plain epilogue, A rows in place: 128-row tiles with their own
+  // loading wavefronts (no workspace).
+  if (MOE_GEMM_FWD128 && pingpong && !swiglu && !gather && M_total <= 128 * G) {
+    const int64_t P = std::max<int64_t>(8, num_cus() / 8 * 8);
+    switch (MOE_GEMM_FWD128_NB ? MOE_GEMM_FWD128_NB : fwd128_nb(M_total, N, G, P)) {
+      case 4: grouped_gemm_fwd128_kernel<4><<<dim3(P), dim3(512), 0, s>>>(p); break;
+      case 5: grouped_gemm_fwd128_kernel<5><<<dim3(P), dim3(512), 0, s>>>(p); break;
+      default: grouped_gemm_fwd128_kernel<6><<<dim3(P), dim3(512), 0, s>>>(p); break;
+    }
+    return check_launch(fn);
+  }
   // With a workspace and a long reduction, group tails of at most 128 rows
   // are listed first and computed as 128-row tiles after the 256-row ones
   // (with short reductions the 128-row tiles' start and drain measured slower

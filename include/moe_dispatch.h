@@ -279,7 +279,12 @@ int moe_index_select(const moe_bf16_t *src, int64_t src_rows, int64_t row_elems,
  *   rows of a multiple of 16 bytes on a 16-byte aligned out, fewer than 2^22
  *   output columns, M_total < 2^31, and M_total < 2^29 for the gather form);
  *   a workspace is ignored elsewhere, and NULL, 0 or a smaller size runs every
- *   tile whole with 256 rows. Calls that share a workspace must not overlap. */
+ *   tile whole with 256 rows. Calls that share a workspace must not overlap.
+ *   moe_grouped_gemm (A rows in place) with MOE_EPILOGUE_NONE and groups of
+ *   at most 128 rows on average (M_total <= 128 G, e.g. case03/04) under the
+ *   same conditions runs 128-row tiles of 128-192 columns with no workspace
+ *   (a given one is not used), with the same summation order: the same
+ *   result bit for bit. */
 size_t moe_grouped_gemm_workspace_size(int64_t M_total, int64_t K, int64_t N, int64_t G);
 int moe_grouped_gemm(const moe_bf16_t *a, int64_t M_total, int64_t K, const moe_bf16_t *w,
                      int64_t G, int64_t N, const int32_t *group_offsets, int epilogue,

@@ -258,3 +258,35 @@ def test_tail_tiles_match_full_tiles(pkg, dev, sizes, K, N, swiglu, gather):
     assert torch.equal(tails.view(torch.int16), full.view(torch.int16)), f"sizes={sizes[:6]} K={K} N={N}"
     a = x[rows.long()] if gather else x
     _sampled_check(a, w, offs.cpu(), tails, swiglu, rows_per_group=8)
+
+
+@pytest.mark.parametrize("sizes,K,N", [
+    ([102] * 39 + [118], 8192, 5120),                             # case03 shape (160-column tiles)
+    ([102] * 39 + [118], 2560, 8192),                             # case04 shape
+    ([3, 0, 700, 41, 128, 129, 1, 64, 100, 5] * 4, 448, 520),     # ragged: groups of 6 row tiles, empty groups
+    ([1] * 300, 192, 200),                                        # 3 K steps: the rings run across tiles
+    ([0, 0, 5], 192, 136),                                        # a single tile
+    ([128] * 8, 1024, 8),                                         # one partial column tile per group
+])
+def test_short_group_kernel_bit_identical(pkg, dev, sizes, K, N):
+    """Groups of at most 128 rows on average (plain epilogue, rows in place) run 128-row tiles with
+    loading wavefronts; the gathered form with identity rows runs the ping-pong kernel. Both take the
+    same v_mfma_f32_16x16x32_bf16 sequence per output element: equal bit for bit, nothing written past
+    the output, and both against the CPU oracle."""
+    g = torch.Generator().manual_seed(sum(sizes) + 3 * K + N)
+    M, G = sum(sizes), len(sizes)
+    assert M <= 128 * G
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(G, N, K, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    offs = pkg.ops.group_offsets_from_splits(sizes, dev)
+    buf = torch.full((M * N + 256,), float("nan"), dtype=torch.bfloat16, device=dev)
+    out = buf[:M * N].view(M, N)
+    pkg.ops.grouped_gemm(x, w, offs, out=out)
+    rows = torch.arange(M, dtype=torch.int32, device=dev)
+    pp = pkg.ops.grouped_gemm_gather(x, rows, w, offs)
+    again = pkg.ops.grouped_gemm(x, w, offs)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), pp.view(torch.int16)), f"sizes={sizes[:6]} K={K} N={N}"
+    assert torch.equal(again.view(torch.int16), pp.view(torch.int16))
+    assert torch.isnan(buf[M * N:].float()).all()
+    _sampled_check(x, w, offs.cpu(), out, False, rows_per_group=8)
