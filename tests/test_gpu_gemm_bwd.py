@@ -248,6 +248,9 @@ def test_wgrad_group_order_matches_stable_sort(pkg, dev, G):
     ([102] * 8 + [103] * 4, 384, 1032),                          # the case05/09 group sizes, a K tail
     ([102] * 8 + [103] * 4, 1032, 384),
     ([7] * 300, 136, 200),                                       # many tiny groups: units over many groups
+    ([7] * 300, 136, 1800),                                      # units of 8 and 7 swept tiles
+    ([102] * 8 + [103] * 4, 128, 1032),                          # one fixed tile per group
+    ([50] * 6 + [200], 96, 120),                                 # N, K <= 128: one tile per group
     ([0, 0, 0], 136, 200),                                       # only empty groups: zeros
 ])
 def test_wgrad_sweep_short_groups(pkg, dev, sizes, N, K):
