@@ -155,8 +155,9 @@ __device__ __forceinline__ f32x4_t mma16(bf16x8 a, bf16x8 b, f32x4_t c) {
 // not whole steps): 1 x 4 waves of 128 x 64, a three-stage ring (the stream of
 // w is HBM-bound here and needs two stages in flight), v_mfma_f32_32x32x16_bf16.
 // kOut: 0 = bf16 output, 1 = fp32 output (the next tile's stages are then
-// issued after the stores).
-template <int kOut>
+// issued after the stores). kNtB: w is streamed once (the groups average at
+// most 160 rows, one or two row tiles each): non-temporal loads for it.
+template <int kOut, bool kNtB = false>
 __global__ __launch_bounds__(256) void grouped_gemm_dgrad128_kernel(BwdArgs p) {
   constexpr int kBM = 128, kWavesM = 1, kStages = 3;
   constexpr int kWaves = 4;
@@ -283,7 +284,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_dgrad128_kernel(BwdArgs p) {
     const uint32_t st = lds_base + (slot % kStages) * kStageBytes + kABytes;
 #pragma unroll
     for (int j = 0; j < kDmaB; ++j)
-      dma16b(rb, (lds_void *)(uintptr_t)(st + (j * kWaves + wave) * 1024), b_off[j], kt * b_step);
+      dma16b<kNtB ? 2 : 0>(rb, (lds_void *)(uintptr_t)(st + (j * kWaves + wave) * 1024), b_off[j], kt * b_step);
   };
   // dgrad: zero dy's chunks past column N in the A tile of stage kt.
   auto zero_ktail_a = [&](int kt) {
@@ -1780,11 +1781,11 @@ __global__ __launch_bounds__(1024) void group_order_kernel(const int32_t *offset
   }
 }
 
-template <int kOut = 0>
+template <int kOut = 0, bool kNtB = false>
 void launch_dgrad128(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
   int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
   grid = std::max<int64_t>(8, (grid + 7) / 8 * 8);
-  grouped_gemm_dgrad128_kernel<kOut><<<dim3(grid), dim3(256), 0, s>>>(p);
+  grouped_gemm_dgrad128_kernel<kOut, kNtB><<<dim3(grid), dim3(256), 0, s>>>(p);
 }
 
 // ---- tf32 GEMMs of the router backward on the bf16 matrix cores ---------
@@ -2132,7 +2133,10 @@ int moe_grouped_gemm_dgrad(const moe_bf16_t *dy, int64_t M_total, int64_t N, con
   // 128-row tiles when the groups average at most 160 rows (less padding in
   // every group's last row tile) and for reductions that are not whole steps
   // of at least three (N % 64 != 0 or N < 192); the pipelined 256-row kernel otherwise.
-  if (M_total <= 160 * G || N % kBK != 0 || N < 3 * kBK) {
+  // With short groups w is streamed once: non-temporal loads (case08 0.387 -> 0.365 ms, case07 unchanged).
+  if (M_total <= 160 * G) {
+    launch_dgrad128<0, true>(p, (ceil_div(M_total, 128) + G) * p.ntiles, s);
+  } else if (N % kBK != 0 || N < 3 * kBK) {
     launch_dgrad128(p, (ceil_div(M_total, 128) + G) * p.ntiles, s);
   } else if (MOE_GEMM_BWD_PINGPONG) {
     // With a workspace and a long reduction, group tails of at most 128 rows
