@@ -8,9 +8,10 @@
 // the case's bit formula, written for finite inputs, would wrap a NaN's bits).
 // The timed op is inp.to(torch.bfloat16) (case25...py:107).
 //
-// HBM-bound streaming: each thread converts 8 elements per iteration (32-byte
-// fp32 and 16-byte bf16 vectors; non-temporal loads), grid-stride over the array;
-// a scalar tail covers the last n % 8 elements and unaligned pointers.
+// HBM-bound streaming, grid-stride over the array: fp32 -> bf16 converts 8
+// elements per thread and iteration (32-byte fp32 in, non-temporal loads;
+// 16-byte bf16 out), bf16 -> fp32 4 (8-byte bf16 in, plain loads; 16-byte fp32
+// out); a scalar tail covers the last elements and unaligned pointers.
 #include <algorithm>
 
 #include "moe_common.h"
@@ -34,14 +35,15 @@ __global__ __launch_bounds__(kThreads) void f32_to_bf16_vec(const float *src, in
   }
 }
 
+// 4 elements per thread: an 8-byte load (plain: the output is twice the input, and non-temporal loads
+// measured 11% slower here) and one 16-byte store, both contiguous across the wavefront.
 __global__ __launch_bounds__(kThreads) void bf16_to_f32_vec(const uint16_t *src, int64_t nvec, float *dst) {
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < nvec; i += stride) {
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src) + i);
+    const u32x2 v = *(reinterpret_cast<const u32x2 *>(src) + i);
     const u32x4 a = {v.x << 16, v.x & 0xffff0000u, v.y << 16, v.y & 0xffff0000u};
-    const u32x4 b = {v.z << 16, v.z & 0xffff0000u, v.w << 16, v.w & 0xffff0000u};
-    *(reinterpret_cast<u32x4 *>(dst) + 2 * i) = a;
-    *(reinterpret_cast<u32x4 *>(dst) + 2 * i + 1) = b;
+    *(reinterpret_cast<u32x4 *>(dst) + i) = a;
   }
 }
 
@@ -90,14 +92,14 @@ int moe_cast_bf16_to_f32(const moe_bf16_t *src, int64_t n, float *dst, void *str
   if (n == 0) return MOE_OK;
   if (src == nullptr || dst == nullptr) return fail(MOE_ERR_INVALID_ARG, "moe_cast_bf16_to_f32: null src or dst");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool vec = is_aligned(src, 16) && is_aligned(dst, 32);
-  const int64_t nvec = vec ? n / 8 : 0;
+  const bool vec = is_aligned(src, 8) && is_aligned(dst, 16);
+  const int64_t nvec = vec ? n / 4 : 0;
   if (nvec > 0) bf16_to_f32_vec<<<dim3(vec_grid(nvec)), dim3(kThreads), 0, s>>>(src, nvec, dst);
-  const int64_t rest = n - nvec * 8;
+  const int64_t rest = n - nvec * 4;
   if (rest > 0) {
     const int64_t g = ceil_div(rest, kThreads);
     if (g > 0x7fffffff) return fail(MOE_ERR_CAPACITY, "moe_cast_bf16_to_f32: n=%lld too large for the scalar path", (long long)n);
-    bf16_to_f32_scalar<<<dim3(g), dim3(kThreads), 0, s>>>(src, nvec * 8, n, dst);
+    bf16_to_f32_scalar<<<dim3(g), dim3(kThreads), 0, s>>>(src, nvec * 4, n, dst);
   }
   return check_launch("moe_cast_bf16_to_f32");
 }

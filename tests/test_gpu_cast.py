@@ -37,7 +37,8 @@ def test_f32_to_bf16_bits(pkg, dev, n, offset):
     assert bool(torch.isnan(got.cpu()[~fin].float()).all())
 
 
-@pytest.mark.parametrize("n,offset", [(0, 0), (3, 0), (8, 0), (1001, 0), (4099, 1), (65536 + 5, 7)])
+@pytest.mark.parametrize("n,offset", [(0, 0), (3, 0), (8, 0), (1001, 0), (4099, 1), (65536 + 5, 7),
+                                      (1003, 4)])  # 8-byte but not 16-byte aligned source: the vector path
 def test_bf16_to_f32_exact(pkg, dev, n, offset):
     g = torch.Generator().manual_seed(7 * n + offset)
     x = torch.randn(n + offset, generator=g).to(torch.bfloat16)
