@@ -9,7 +9,7 @@
 // token, each owning every 4th / 2nd 1 KiB slice of the row (PermShape).  A
 // wave reads the token's
 // map entries 64 experts at a time, turns "entry >= 0" into a 64-bit ballot,
-// loads the x row once into VGPRs as 16-byte vectors (non-temporal), then
+// loads the x row once into VGPRs as 16-byte vectors (plain loads), then
 // walks the ballot's set bits in ascending expert order and stores the row to
 // each destination (plain stores: measured 4-5% faster than non-temporal ones
 // at c5 with a 1 GiB flush between calls).  The row is read from HBM once and written k times, which
@@ -129,7 +129,9 @@ __global__ __launch_bounds__(PermShape<kExpertMajor>::kThreads) void permute_ker
 #pragma unroll
         for (int j = 0; j < kMaxVecPerLane; ++j) {
           const int64_t v = seg + (j * kSplit + part) * kWave + lane;
-          if (v < nvec) buf[j] = __builtin_nontemporal_load(src + v);
+          // plain loads: the row is written k times, and with the writes dominating the non-temporal
+          // loads measured slower (c5 0.396 against 0.408 ms, back to back)
+          if (v < nvec) buf[j] = src[v];
         }
         for (int c = 0; c < nchunks; ++c) {
           int64_t dst = -1;
@@ -183,7 +185,7 @@ __global__ __launch_bounds__(PermShape<kExpertMajor>::kThreads) void permute_ker
 // entries outside [0, num_out)); the padded LDS row (E rounded up to 64, + 1)
 // keeps the transposing writes off a single bank. Then one wavefront per token
 // builds the 64-bit ballots of its routed experts, writes the permuted probs,
-// loads the token's row into VGPRs (non-temporal, 16 vectors per lane per pass)
+// loads the token's row into VGPRs (16 vectors per lane per pass)
 // and stores it to each destination in ascending expert order.
 // 8 tokens, one wavefront each (case21 map, 1 GiB flush: 0.476-0.478 ms; 4 tokens 0.501, 16 tokens 0.486
 // (two per wavefront), 32 tokens 0.492; the per-token staged kernel below 0.500).
@@ -243,7 +245,7 @@ __global__ __launch_bounds__(kTileThreads) void permute_tile_kernel(PermuteArgs 
 #pragma unroll
       for (int j = 0; j < kVecPerLane; ++j) {
         const int64_t v = seg + (j * kSplit + part) * kWave + lane;
-        if (v < nvec) buf[j] = __builtin_nontemporal_load(src + v);
+        if (v < nvec) buf[j] = src[v];
       }
       for (int c = 0; c < nch; ++c) {
         uint64_t mask = uniform_u64(s_valid[tk * nch + c]);
