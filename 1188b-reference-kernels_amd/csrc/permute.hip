@@ -9,7 +9,8 @@
 // token, each owning every 4th / 2nd 1 KiB slice of the row (PermShape).  A
 // wave reads the token's
 // map entries 64 experts at a time, turns "entry >= 0" into a 64-bit ballot,
-// loads the x row once into VGPRs as 16-byte vectors (plain loads), then
+// loads the x row once into VGPRs as 16-byte vectors (non-temporal loads, plain
+// ones when the permuted output is 1 GiB or more), then
 // walks the ballot's set bits in ascending expert order and stores the row to
 // each destination (plain stores: measured 4-5% faster than non-temporal ones
 // at c5 with a 1 GiB flush between calls).  The row is read from HBM once and written k times, which
@@ -63,7 +64,8 @@ __device__ __forceinline__ int64_t map_at(const PermuteArgs &a, int64_t t, int64
 constexpr int kMaxStagedE = 1024;
 __host__ __device__ inline int stage_bytes_per_token(int nchunks) { return nchunks * (kWave * 8 + 8); }
 
-template <bool kI64, bool kExpertMajor, bool kProbs, bool kVec, bool kStaged>
+// kNtRow: non-temporal loads of the x row (16-byte rows only), else plain loads.
+template <bool kI64, bool kExpertMajor, bool kProbs, bool kVec, bool kStaged, bool kNtRow>
 __global__ __launch_bounds__(PermShape<kExpertMajor>::kThreads) void permute_kernel(PermuteArgs a) {
   constexpr int kThreads = PermShape<kExpertMajor>::kThreads;
   constexpr int kSplit = PermShape<kExpertMajor>::kSplit;
@@ -129,9 +131,11 @@ __global__ __launch_bounds__(PermShape<kExpertMajor>::kThreads) void permute_ker
 #pragma unroll
         for (int j = 0; j < kMaxVecPerLane; ++j) {
           const int64_t v = seg + (j * kSplit + part) * kWave + lane;
-          // plain loads: the row is written k times, and with the writes dominating the non-temporal
-          // loads measured slower (c5 0.396 against 0.408 ms, back to back)
-          if (v < nvec) buf[j] = src[v];
+          if constexpr (kNtRow) {
+            if (v < nvec) buf[j] = __builtin_nontemporal_load(src + v);
+          } else {
+            if (v < nvec) buf[j] = src[v];
+          }
         }
         for (int c = 0; c < nchunks; ++c) {
           int64_t dst = -1;
@@ -245,7 +249,7 @@ __global__ __launch_bounds__(kTileThreads) void permute_tile_kernel(PermuteArgs 
 #pragma unroll
       for (int j = 0; j < kVecPerLane; ++j) {
         const int64_t v = seg + (j * kSplit + part) * kWave + lane;
-        if (v < nvec) buf[j] = src[v];
+        if (v < nvec) buf[j] = __builtin_nontemporal_load(src + v);
       }
       for (int c = 0; c < nch; ++c) {
         uint64_t mask = uniform_u64(s_valid[tk * nch + c]);
@@ -313,6 +317,11 @@ __global__ __launch_bounds__(kTailThreads) void permute_zero_tail_kernel(const i
 
 template <bool kI64, bool kExpertMajor, bool kProbs>
 void launch_permute_3(const PermuteArgs &a, bool vec, int64_t grid, hipStream_t s) {
+  // Row loads: plain when the permuted output is 1 GiB or more, non-temporal below (1 GiB flush between
+  // calls; H = 7168 and 8 destinations per token: non-temporal 1.2-2% faster up to 8192 tokens, 0.94 GB
+  // written, plain 0.7-2% faster from 12288 tokens, 1.41 GB, to 32768; with 2 or 4 destinations per
+  // token, 0.05-0.54 GB written, non-temporal 6-18% faster).
+  const bool nt = static_cast<double>(a.num_out) * static_cast<double>(a.H) * 2.0 < 1073741824.0;
   constexpr int kThreads = PermShape<kExpertMajor>::kThreads;
   // Staged for expert-major maps only: 1.5-3% faster there (case21/22/30), 2% slower with a token-major map
   // (case17), whose row of entries is one contiguous read.
@@ -320,14 +329,18 @@ void launch_permute_3(const PermuteArgs &a, bool vec, int64_t grid, hipStream_t 
   const size_t lds = staged ? static_cast<size_t>(PermShape<kExpertMajor>::kTokensPerBlock) *
                                   stage_bytes_per_token(static_cast<int>(ceil_div(a.E, kWave)))
                             : 0;
-  if (vec && staged) {
-    permute_kernel<kI64, kExpertMajor, kProbs, true, true><<<dim3(grid), dim3(kThreads), lds, s>>>(a);
+  if (vec && staged && nt) {
+    permute_kernel<kI64, kExpertMajor, kProbs, true, true, true><<<dim3(grid), dim3(kThreads), lds, s>>>(a);
+  } else if (vec && staged) {
+    permute_kernel<kI64, kExpertMajor, kProbs, true, true, false><<<dim3(grid), dim3(kThreads), lds, s>>>(a);
+  } else if (vec && nt) {
+    permute_kernel<kI64, kExpertMajor, kProbs, true, false, true><<<dim3(grid), dim3(kThreads), 0, s>>>(a);
   } else if (vec) {
-    permute_kernel<kI64, kExpertMajor, kProbs, true, false><<<dim3(grid), dim3(kThreads), 0, s>>>(a);
+    permute_kernel<kI64, kExpertMajor, kProbs, true, false, false><<<dim3(grid), dim3(kThreads), 0, s>>>(a);
   } else if (staged) {
-    permute_kernel<kI64, kExpertMajor, kProbs, false, true><<<dim3(grid), dim3(kThreads), lds, s>>>(a);
+    permute_kernel<kI64, kExpertMajor, kProbs, false, true, false><<<dim3(grid), dim3(kThreads), lds, s>>>(a);
   } else {
-    permute_kernel<kI64, kExpertMajor, kProbs, false, false><<<dim3(grid), dim3(kThreads), 0, s>>>(a);
+    permute_kernel<kI64, kExpertMajor, kProbs, false, false, false><<<dim3(grid), dim3(kThreads), 0, s>>>(a);
   }
 }
 

@@ -94,6 +94,26 @@ def test_permute_matches_oracle(pkg, dev, layout, idx, T, E, k, H):
         assert_bits_equal(pp, ref_pp, f"permuted probs num_out={num_out}")
 
 
+# The per-token kernel loads the x row with non-temporal loads below 1 GiB of permuted output and with plain
+# loads from 1 GiB on: 9300 tokens write 1.067e9 bytes, 9400 tokens 1.078e9 (H = 7168, 8 rows per token).
+@pytest.mark.parametrize("T", [9300, 9400], ids=["nt_row_loads", "plain_row_loads"])
+def test_permute_row_load_policies_large(pkg, dev, T):
+    E, k, H = 64, 8, 7168
+    assert (T * k * H * 2 >= 1 << 30) == (T == 9400)
+    rm = _mask(T, E, k, seed=T)
+    _, tm = ref_torch.row_id_map(rm)
+    x = pkg.inputs.randn_bf16((T, H), seed=T, device=dev)
+    probs = torch.rand(T, E, generator=torch.Generator().manual_seed(T)) * rm
+    out, pp = pkg.ops.permute(x, tm.to(dev), probs.to(dev), num_out=T * k, layout="token_major",
+                              zero_tail=False)
+    t, e = rm.nonzero(as_tuple=True)
+    rows = tm[t, e]
+    assert torch.equal(torch.sort(rows).values, torch.arange(T * k, dtype=rows.dtype)), "every row is named once"
+    rows_d, t_d = rows.to(dev), t.to(dev)
+    assert torch.equal(out[rows_d].view(torch.int16), x[t_d].view(torch.int16))
+    assert torch.equal(pp.cpu()[rows], probs[t, e])
+
+
 @pytest.mark.parametrize("layout", ["token_major", "expert_major"])
 @pytest.mark.parametrize("E", [96, 320])
 def test_permute_stores_stay_inside_out(pkg, dev, layout, E):
