@@ -376,7 +376,8 @@ __global__ __launch_bounds__(256) void permute_index_kernel(const void *map, int
 // more than the pass); map_extent_final_kernel adds the partials up in block
 // order and counts the set bytes of [0, max]: the map names every row of
 // [0, max] exactly once iff count == max + 1 == that byte count.
-constexpr int kExtentMaxBlocks = 1024;
+constexpr int kExtentMaxBlocks = 2048;
+constexpr int kExtentUnroll = 4;  // 16-byte vectors each thread loads before using them
 template <bool kI64, bool kVec>
 __global__ __launch_bounds__(256) void map_extent_partial_kernel(const void *map, int64_t n, int64_t *partials,
                                                                  uint8_t *seen) {
@@ -390,16 +391,26 @@ __global__ __launch_bounds__(256) void map_extent_partial_kernel(const void *map
   const int64_t gstride = static_cast<int64_t>(gridDim.x) * 256;
   constexpr int kPer = kI64 ? 2 : 4;  // entries per 16-byte vector
   const int64_t nvec = kVec ? n / kPer : 0;
-  for (int64_t i = gtid; i < nvec; i += gstride) {
-    const u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(map) + i);
-    if constexpr (kI64) {
-      take(static_cast<int64_t>(static_cast<uint64_t>(q.x) | (static_cast<uint64_t>(q.y) << 32)));
-      take(static_cast<int64_t>(static_cast<uint64_t>(q.z) | (static_cast<uint64_t>(q.w) << 32)));
-    } else {
-      take(static_cast<int32_t>(q.x));
-      take(static_cast<int32_t>(q.y));
-      take(static_cast<int32_t>(q.z));
-      take(static_cast<int32_t>(q.w));
+  // kExtentUnroll vectors per thread in flight before any is used
+  for (int64_t i0 = gtid; i0 < nvec; i0 += gstride * kExtentUnroll) {
+    u32x4 q[kExtentUnroll];
+#pragma unroll
+    for (int u = 0; u < kExtentUnroll; ++u) {
+      const int64_t i = i0 + u * gstride;
+      if (i < nvec) q[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(map) + i);
+    }
+#pragma unroll
+    for (int u = 0; u < kExtentUnroll; ++u) {
+      if (i0 + u * gstride >= nvec) break;
+      if constexpr (kI64) {
+        take(static_cast<int64_t>(static_cast<uint64_t>(q[u].x) | (static_cast<uint64_t>(q[u].y) << 32)));
+        take(static_cast<int64_t>(static_cast<uint64_t>(q[u].z) | (static_cast<uint64_t>(q[u].w) << 32)));
+      } else {
+        take(static_cast<int32_t>(q[u].x));
+        take(static_cast<int32_t>(q[u].y));
+        take(static_cast<int32_t>(q[u].z));
+        take(static_cast<int32_t>(q[u].w));
+      }
     }
   }
   for (int64_t i = nvec * kPer + gtid; i < n; i += gstride) take(load_idx<kI64>(map, i));
@@ -431,11 +442,19 @@ __global__ __launch_bounds__(kExtentFinal) void map_extent_final_kernel(const in
                                                                const uint8_t *seen, int64_t *out) {
   __shared__ int64_t s_a[kExtentFinal / kWave], s_b[kExtentFinal / kWave];
   const int wave = threadIdx.x / kWave;
-  int64_t mx = -1, cnt = 0;
-  for (int b = threadIdx.x; b < nblocks; b += kExtentFinal) {
-    mx = partials[2 * b] > mx ? partials[2 * b] : mx;
-    cnt += partials[2 * b + 1];
+  // at most two (max, count) pairs per thread, both loaded before either is used
+  static_assert(kExtentMaxBlocks <= 2 * kExtentFinal, "two partials per thread");
+  int64_t m0 = -1, c0 = 0, m1 = -1, c1 = 0;
+  const int b0 = threadIdx.x, b1 = threadIdx.x + kExtentFinal;
+  if (b0 < nblocks) {
+    m0 = partials[2 * b0];
+    c0 = partials[2 * b0 + 1];
   }
+  if (b1 < nblocks) {
+    m1 = partials[2 * b1];
+    c1 = partials[2 * b1 + 1];
+  }
+  int64_t mx = m1 > m0 ? m1 : m0, cnt = c0 + c1;
 #pragma unroll
   for (int off = kWave / 2; off > 0; off >>= 1) {
     const int64_t omx = __shfl_xor(mx, off);
@@ -459,9 +478,19 @@ __global__ __launch_bounds__(kExtentFinal) void map_extent_final_kernel(const in
   int64_t pop = 0;
   if (cnt == mx + 1 && mx >= 0) {
     const int64_t rows = mx + 1, nvec = rows / 16;
-    for (int64_t i = threadIdx.x; i < nvec; i += kExtentFinal) {
-      const u32x4 q = reinterpret_cast<const u32x4 *>(seen)[i];
-      pop += __builtin_popcount(q.x) + __builtin_popcount(q.y) + __builtin_popcount(q.z) + __builtin_popcount(q.w);
+    constexpr int kU = 8;  // 16-byte vectors per thread in flight before any is counted
+    for (int64_t i0 = threadIdx.x; i0 < nvec; i0 += static_cast<int64_t>(kExtentFinal) * kU) {
+      u32x4 q[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int64_t i = i0 + static_cast<int64_t>(u) * kExtentFinal;
+        q[u] = i < nvec ? reinterpret_cast<const u32x4 *>(seen)[i] : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        pop += __builtin_popcount(q[u].x) + __builtin_popcount(q[u].y) + __builtin_popcount(q[u].z) +
+               __builtin_popcount(q[u].w);
+      }
     }
     for (int64_t i = nvec * 16 + threadIdx.x; i < rows; i += kExtentFinal) pop += seen[i];
   }
