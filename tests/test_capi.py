@@ -163,7 +163,9 @@ def test_workspace_sizes():
     assert lib.moe_permute_workspace_size(16384) >= 4096 * 4
     # map extent: one (max, count) int64 pair per partial block, at most 1024 blocks
     assert lib.moe_map_extent_workspace_size(0) == 256  # partials (256-byte aligned), then n bytes of row marks
-    assert lib.moe_map_extent_workspace_size(320 * 16384) == 1024 * 16 + 320 * 16384
+    # one (max, count) pair per block, a block per 4096 entries up to 2048 blocks: 1280 at case21
+    assert lib.moe_map_extent_workspace_size(320 * 16384) == 1280 * 16 + 320 * 16384
+    assert lib.moe_map_extent_workspace_size(1 << 24) == 2048 * 16 + (1 << 24)
     assert lib.moe_map_extent_workspace_size(33) == 256 + 48
     assert lib.moe_map_extent_workspace_size(-1) == 0
     assert lib.moe_row_id_map_workspace_size(-1, 4) == 0
