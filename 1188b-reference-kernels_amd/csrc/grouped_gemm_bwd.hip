@@ -82,6 +82,11 @@ struct BwdArgs {
   int *tails;               // dgrad ping-pong kernel: tail list (kTail* layout) or nullptr
   int sweep_rows = 0;       // wgrad (kOrder): > 0 leaves the groups of at most this many rows to the sweep kernel
   int sweep_len = 0;        // sweep kernel: tiles per unit (one fixed slab)
+  // fp16 dgrad (the tf32 router dgrad, 128-row kernel): the power-of-two scale exponents of dy's rows (int8,
+  // permuted within each 128-row block: row 128 b + 32 i + l at byte 128 b + 4 l + i) and of dx's columns
+  // (int8 [K]).
+  const int8_t *row_exp8 = nullptr;
+  const int8_t *col_exp8 = nullptr;
 };
 
 // Groups of the largest-first order with more than `limit` rows: the first
@@ -133,7 +138,7 @@ __device__ __forceinline__ bf16x8 read_rm_frag(uint32_t addr) {
 #endif
 }
 
-// One 16 x 16 x 32 MFMA on 16-bit operands: bf16, or fp16 (kF16: the tf32 router wgrad's scaled operands,
+// One 16 x 16 x 32 MFMA on 16-bit operands: bf16, or fp16 (kF16: the tf32 router GEMMs' scaled operands,
 // the same bit layout in LDS and registers).
 template <bool kF16>
 __device__ __forceinline__ f32x4_t mma16(bf16x8 a, bf16x8 b, f32x4_t c) {
@@ -157,8 +162,12 @@ __device__ __forceinline__ f32x4_t mma16(bf16x8 a, bf16x8 b, f32x4_t c) {
 // kOut: 0 = bf16 output, 1 = fp32 output (the next tile's stages are then
 // issued after the stores). kNtB: w is streamed once (the groups average at
 // most 160 rows, one or two row tiles each): non-temporal loads for it.
-template <int kOut, bool kNtB = false>
+// kF16 (the tf32 router dgrad, fp32 output, rows [0, M) as one group): fp16
+// operands scaled by powers of two per dy row and per dx column
+// (p.row_exp8, p.col_exp8), undone in the epilogue.
+template <int kOut, bool kNtB = false, bool kF16 = false>
 __global__ __launch_bounds__(256) void grouped_gemm_dgrad128_kernel(BwdArgs p) {
+  static_assert(!kF16 || kOut == 1, "fp16 operands: the tf32 router dgrad (fp32 output)");
   constexpr int kBM = 128, kWavesM = 1, kStages = 3;
   constexpr int kWaves = 4;
   constexpr int kWavesN = kWaves / kWavesM;
@@ -169,8 +178,10 @@ __global__ __launch_bounds__(256) void grouped_gemm_dgrad128_kernel(BwdArgs p) {
   constexpr int kBBytes = kBN * kBK * 2;
   constexpr int kStageBytes = kABytes + kBBytes;
   constexpr int kDmaA = kABytes / 1024 / kWaves, kDmaB = kBBytes / 1024 / kWaves;
-  constexpr bool kLate = kOut != 0;             // next tile's stages issued after the stores
-  constexpr int kStores = kLate ? 0 : kMI * kNI * 2;  // stores younger than the next stages
+  // Next tile's stages issued after the stores (fp32 output; the fp16 form issues them before, as the bf16
+  // output does: its tiles have few reduction steps, so the next stages' latency would not be hidden).
+  constexpr bool kLate = kOut != 0 && !kF16;
+  constexpr int kStores = kLate ? 0 : kMI * kNI * (kOut != 0 ? 4 : 2);  // stores younger than the next stages
   constexpr int kReads = kMI + 2 * kNI;          // LDS reads per sub-step
   constexpr int kMfma = kMI * kNI;              // MFMAs per sub-step
   static_assert(kStages * kStageBytes <= 160 * 1024, "LDS budget");
@@ -333,11 +344,48 @@ __global__ __launch_bounds__(256) void grouped_gemm_dgrad128_kernel(BwdArgs p) {
     for (int i = 0; i < kMI; ++i)
 #pragma unroll
       for (int j = 0; j < kNI; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks][j], fa[ks][i], acc[i][j], 0, 0, 0);
+        if constexpr (kF16) {
+          typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, fb[ks][j]),
+                                                            __builtin_bit_cast(f16x8, fa[ks][i]), acc[i][j], 0, 0, 0);
+        } else {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks][j], fa[ks][i], acc[i][j], 0, 0, 0);
+        }
+  };
+  // kF16: the tile's scale exponents, int8 (rows 32 i + l % 32: byte i of ex_row; columns
+  // 32 j + 8 g + 4 (l / 32) + r: byte r of ex_col[4 j + g]): the first tile's before its stage DMAs, the
+  // next tile's after this tile's stores; the full wait that ends each tile's reduction covers them.
+  uint32_t ex_row = 0u, ex_col[kNI * 4] = {};
+  auto load_exps = [&](const Tile &t) {
+    if constexpr (kF16) {
+      const int64_t wrow0 = t.i0 + wm * kWaveRows;
+      const bool rows_in = t.hi > wrow0;
+      const __amdgpu_buffer_rsrc_t rr = make_rsrc(p.row_exp8 + (rows_in ? wrow0 : 0), rows_in ? 128u : 0u);
+      const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.col_exp8, static_cast<uint32_t>(K));
+      const int64_t tcol0 = static_cast<int64_t>(t.nt) * kBN + wn * kWaveCols + (lane >> 5) * 4;
+#if defined(__HIP_DEVICE_COMPILE__)
+      ex_row = __builtin_amdgcn_raw_buffer_load_b32(rr, (lane & 31) * 4, 0, 0);
+#pragma unroll
+      for (int j = 0; j < kNI; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int64_t gcol = tcol0 + j * 32 + g * 8;
+          ex_col[4 * j + g] =
+              __builtin_amdgcn_raw_buffer_load_b32(rc, gcol < K ? static_cast<int>(gcol) : static_cast<int>(kNoAccess), 0, 0);
+        }
+#else
+      (void)rr;
+      (void)rc;
+      (void)tcol0;
+#endif
+    } else {
+      (void)t;
+    }
   };
 
   Tile cur;
   if (!find_tile(0, cur)) return;
+  load_exps(cur);
   setup_dma(cur);
   // Every stage slot is filled (stages past the last re-read the last one), so
   // the count of outstanding loads is the same for every tile.
@@ -457,8 +505,15 @@ __global__ __launch_bounds__(256) void grouped_gemm_dgrad128_kernel(BwdArgs p) {
           for (int g = 0; g < 4; ++g) {
             const int64_t gcol = tcol0 + j * 32 + g * 8 + half * 4;
             const uint32_t off = gcol < K ? static_cast<uint32_t>(orow) * ld + static_cast<uint32_t>(gcol) * 4u : kNoAccess;
-            const u32x4 v = {__float_as_uint(acc[i][j][4 * g]), __float_as_uint(acc[i][j][4 * g + 1]),
-                             __float_as_uint(acc[i][j][4 * g + 2]), __float_as_uint(acc[i][j][4 * g + 3])};
+            float x[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+            if constexpr (kF16) {
+              // the scales undone: x 2^-(e_row + e_col), exact unless the result is subnormal
+              const int er = static_cast<int8_t>(ex_row >> (8 * i));
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                x[r] = __builtin_ldexpf(x[r], -(er + static_cast<int8_t>(ex_col[4 * j + g] >> (8 * r))));
+            }
+            const u32x4 v = {__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3])};
 #if defined(__HIP_DEVICE_COMPILE__)
             __builtin_amdgcn_raw_buffer_store_b128(v, ro, static_cast<int>(off), 0, 0);
 #else
@@ -514,6 +569,9 @@ __global__ __launch_bounds__(256) void grouped_gemm_dgrad128_kernel(BwdArgs p) {
           }
         }
       }
+    }
+    if constexpr (kF16) {
+      if (more) load_exps(nxt);
     }
     if (!more) break;
     if constexpr (kLate) {
@@ -1726,6 +1784,10 @@ void launch_pipe(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
 #ifndef MOE_GEMM_BWD_PINGPONG
 #define MOE_GEMM_BWD_PINGPONG 1
 #endif
+// The tf32 router dgrad on the fp16 matrix cores (1) or on the bf16 hi/lo split (0).
+#ifndef MOE_ROUTER_DGRAD_F16
+#define MOE_ROUTER_DGRAD_F16 1
+#endif
 template <bool kWgrad, bool kOrder = false, bool kTails = false>
 void launch_pp(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
   int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
@@ -1781,11 +1843,11 @@ __global__ __launch_bounds__(1024) void group_order_kernel(const int32_t *offset
   }
 }
 
-template <int kOut = 0, bool kNtB = false>
+template <int kOut = 0, bool kNtB = false, bool kF16 = false>
 void launch_dgrad128(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
   int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
   grid = std::max<int64_t>(8, (grid + 7) / 8 * 8);
-  grouped_gemm_dgrad128_kernel<kOut, kNtB><<<dim3(grid), dim3(256), 0, s>>>(p);
+  grouped_gemm_dgrad128_kernel<kOut, kNtB, kF16><<<dim3(grid), dim3(256), 0, s>>>(p);
 }
 
 // ---- tf32 GEMMs of the router backward on the bf16 matrix cores ---------
@@ -1906,8 +1968,11 @@ __global__ __launch_bounds__(256) void colmax_partial_kernel(const float *src, i
   }
 }
 
-// exp[c] = scale_exp(largest of part[0..S)[c]) (S <= 64: eight independent loads per round).
-__global__ __launch_bounds__(256) void colmax_final_kernel(const float *part, int S, int64_t C, int32_t *exp) {
+// exp[c] = scale_exp(largest of part[0..S)[c]) (S <= 64: eight independent loads per round); kI8: clamped to
+// at most 127 (columns whose largest magnitude lies below 2^-112) and also written as int8 to exp8.
+template <bool kI8 = false>
+__global__ __launch_bounds__(256) void colmax_final_kernel(const float *part, int S, int64_t C, int32_t *exp,
+                                                           int8_t *exp8) {
   const int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (c >= C) return;
   float m = 0.f;
@@ -1918,7 +1983,55 @@ __global__ __launch_bounds__(256) void colmax_final_kernel(const float *part, in
 #pragma unroll
     for (int u = 0; u < 8; ++u) m = fmaxf(m, v[u]);
   }
-  exp[c] = scale_exp(m);
+  if constexpr (kI8) {
+    const int e = min(scale_exp(m), 127);
+    exp[c] = e;
+    exp8[c] = static_cast<int8_t>(e);
+  } else {
+    (void)exp8;
+    exp[c] = scale_exp(m);
+  }
+}
+
+// Row-scaled fp16 copy for the tf32 router dgrad: one wavefront per row r of src [R, C] (C % 4 == 0):
+// e = scale_exp(largest magnitude of the row), at most 127; dst[r][c] = fp16(tf32(src[r][c]) 2^e) (RNE) and
+// exp8 at the row's permuted position (128 b + 4 (r % 32) + (r % 128) / 32 for r = 128 b + (r % 128)).
+// Rows R .. R8 - 1 (R8 = R rounded up to 128) only get exponent 0.
+__global__ __launch_bounds__(256) void tf32_to_f16_rows_kernel(const float *src, int64_t R, int64_t R8, int64_t C,
+                                                               uint16_t *dst, int8_t *exp8) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  if (r >= R8) return;
+  const int64_t q = C / 4;
+  const u32x4 *row = reinterpret_cast<const u32x4 *>(src + r * C);
+  float m = 0.f;
+  if (r < R) {
+    for (int64_t i = lane; i < q; i += kWave) {
+      const u32x4 v = row[i];
+      m = fmaxf(m, fmaxf(fmaxf(fabsf(__uint_as_float(v.x)), fabsf(__uint_as_float(v.y))),
+                         fmaxf(fabsf(__uint_as_float(v.z)), fabsf(__uint_as_float(v.w)))));
+    }
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  const int e = r < R ? min(scale_exp(m), 127) : 0;
+  if (lane == 0) {
+    const int64_t w = r % 128;
+    exp8[r - w + (w % 32) * 4 + w / 32] = static_cast<int8_t>(e);
+  }
+  if (r >= R) return;
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  for (int64_t i = lane; i < q; i += kWave) {
+    const u32x4 v = __builtin_nontemporal_load(row + i);
+    const uint32_t in[4] = {v.x, v.y, v.z, v.w};
+    uint32_t h[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float t = __builtin_ldexpf(__uint_as_float(tf32_rne_bits(in[k])), e);
+      h[k] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(t));
+    }
+    *reinterpret_cast<u32x2 *>(dst + r * C + i * 4) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+  }
 }
 
 // dst[r][c] = fp16(tf32(src[r][c]) 2^exp[c]) (RNE; C % 4 == 0).
@@ -2067,6 +2180,45 @@ bool dgrad_pp_tails(int64_t M, int64_t N, int64_t G) {
   using namespace moe;
   return MOE_GEMM_BWD_PINGPONG && G >= 1 && G <= 4096 && M > 160 * G && M < (int64_t(1) << 31) && N % kBK == 0 &&
          N >= std::max<int64_t>(3 * kBK, gemm::kTailsMinK);
+}
+
+// tf32 router dgrad, grad_input [M, N] = grad_output [M, K] weight [K, N]. With more than 160 rows and a
+// reduction of whole steps (K % 64 == 0, K >= 192) it runs on the fp16 matrix cores: grad_output's rows and
+// weight's columns are scaled by powers of two into the fp16 range (one exact fp16 product per tf32
+// product) and the GEMM's epilogue undoes both scales; otherwise it runs on the bf16 hi/lo split (three
+// products, a 3K reduction). Workspace (byte offsets, each 256-byte aligned): fp16 path: the fp16 copies
+// a16 [M, K] and b16 [K, N], the int8 row exponents (M rounded up to 128), the column exponents (int32 and
+// int8) and the column-max slabs; split path: the stacked bf16 operands [M, 3K] and [3K, N].
+struct DgradTf32Layout {
+  bool f16;
+  moe::ColmaxPlan cb;
+  int64_t m8;  // M rounded up to 128
+  size_t a16, b16, row_e8, col_e32, col_e8, part_b, total;
+};
+DgradTf32Layout dgrad_tf32_layout(int64_t M, int64_t K, int64_t N) {
+  using moe::align_up;
+  DgradTf32Layout l{};
+  l.f16 = MOE_ROUTER_DGRAD_F16 != 0;
+  if (!l.f16) {
+    l.total = align_up(static_cast<size_t>(M) * 3 * K * 2) + align_up(static_cast<size_t>(3 * K) * N * 2);
+    return l;
+  }
+  l.cb = moe::colmax_plan(K, N);
+  l.m8 = moe::ceil_div(M, 128) * 128;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += align_up(bytes);
+    return at;
+  };
+  l.a16 = take(static_cast<size_t>(M) * K * 2);
+  l.b16 = take(static_cast<size_t>(K) * N * 2);
+  l.row_e8 = take(static_cast<size_t>(l.m8));
+  l.col_e32 = take(static_cast<size_t>(N) * 4);
+  l.col_e8 = take(static_cast<size_t>(N));
+  l.part_b = take(static_cast<size_t>(l.cb.S) * N * 4);
+  l.total = off;
+  return l;
 }
 
 }  // namespace
@@ -2241,7 +2393,7 @@ int moe_grouped_gemm_wgrad(const moe_bf16_t *dy, const moe_bf16_t *x, int64_t M_
 
 size_t moe_router_dgrad_tf32_workspace_size(int64_t M, int64_t K, int64_t N) {
   if (M < 0 || K < 0 || N < 0) return 0;
-  return moe::align_up(static_cast<size_t>(M) * 3 * K * 2) + moe::align_up(static_cast<size_t>(3 * K) * N * 2);
+  return dgrad_tf32_layout(M, K, N).total;
 }
 
 int moe_router_dgrad_tf32(const float *grad_output, int64_t M, int64_t K, const float *weight, int64_t N,
@@ -2263,12 +2415,51 @@ int moe_router_dgrad_tf32(const float *grad_output, int64_t M, int64_t K, const 
   if (!is_aligned(grad_output, 16) || !is_aligned(weight, 16) || !is_aligned(grad_input, 16)) {
     return fail(MOE_ERR_ALIGN, "%s: grad_output, weight and grad_input must be 16-byte aligned", fn);
   }
-  const size_t need = moe_router_dgrad_tf32_workspace_size(M, K, N);
+  const DgradTf32Layout l = dgrad_tf32_layout(M, K, N);
+  const size_t need = l.total;
   if (workspace == nullptr || workspace_bytes < need || !is_aligned(workspace, kWsAlign)) {
     return fail(MOE_ERR_WORKSPACE, "%s: a 256-byte aligned workspace of %zu bytes is needed (got %zu)", fn, need,
                 workspace == nullptr ? size_t(0) : workspace_bytes);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (l.f16) {
+    char *w = static_cast<char *>(workspace);
+    uint16_t *a16 = reinterpret_cast<uint16_t *>(w + l.a16);
+    uint16_t *b16 = reinterpret_cast<uint16_t *>(w + l.b16);
+    int8_t *row_e8 = reinterpret_cast<int8_t *>(w + l.row_e8);
+    int32_t *col_e32 = reinterpret_cast<int32_t *>(w + l.col_e32);
+    int8_t *col_e8 = reinterpret_cast<int8_t *>(w + l.col_e8);
+    float *part_b = reinterpret_cast<float *>(w + l.part_b);
+    // Scale exponents of weight's columns and its fp16 copy, then grad_output's rows with their fp16 copy.
+    colmax_partial_kernel<<<dim3(static_cast<uint32_t>(l.cb.xb), static_cast<uint32_t>(l.cb.S)), dim3(256), 0, s>>>(
+        weight, K, N, l.cb.rps, l.cb.cg, part_b);
+    colmax_final_kernel<true><<<dim3(static_cast<uint32_t>(ceil_div(N, 256))), dim3(256), 0, s>>>(
+        part_b, static_cast<int>(l.cb.S), N, col_e32, col_e8);
+    const int64_t gb = std::max<int64_t>(1, std::min<int64_t>(ceil_div(K * N / 4, 256), 8192));
+    tf32_to_f16_cols_kernel<<<dim3(static_cast<uint32_t>(gb)), dim3(256), 0, s>>>(weight, K, N, col_e32, b16);
+    tf32_to_f16_rows_kernel<<<dim3(static_cast<uint32_t>(ceil_div(l.m8, 4))), dim3(256), 0, s>>>(grad_output, M, l.m8,
+                                                                                                 K, a16, row_e8);
+    if (int rc = check_launch(fn)) return rc;
+    BwdArgs p;
+    p.a = a16;
+    p.b = b16;
+    p.offsets = nullptr;
+    p.out = grad_input;
+    p.M = M;
+    p.N = K;
+    p.K = N;
+    p.G = 1;
+    p.ntiles = ceil_div(N, kBN);
+    p.chunk = M;
+    p.kchunk = 0;
+    p.order = nullptr;
+    p.order_rows = nullptr;
+    p.tails = nullptr;
+    p.row_exp8 = row_e8;
+    p.col_exp8 = col_e8;
+    launch_dgrad128<1, false, true>(p, (ceil_div(M, 128) + 1) * p.ntiles, s);
+    return check_launch(fn);
+  }
   // A' = [A_hi | A_hi | A_lo] [M, 3K] and B' = [B_hi; B_lo; B_hi] [3K, N]:
   // A' B' = A_hi B_hi + A_hi B_lo + A_lo B_hi, one GEMM with a 3K reduction.
   uint16_t *a3 = static_cast<uint16_t *>(workspace);
@@ -2405,9 +2596,9 @@ int moe_router_wgrad_tf32(const float *grad_output, int64_t M, int64_t N, const 
   colmax_partial_kernel<<<dim3(static_cast<uint32_t>(l.cb.xb), static_cast<uint32_t>(l.cb.S)), dim3(256), 0, s>>>(
       inp, M, K, l.cb.rps, l.cb.cg, part_b);
   colmax_final_kernel<<<dim3(static_cast<uint32_t>(ceil_div(N, 256))), dim3(256), 0, s>>>(part_a, static_cast<int>(l.ca.S), N,
-                                                                                          row_exp);
+                                                                                          row_exp, nullptr);
   colmax_final_kernel<<<dim3(static_cast<uint32_t>(ceil_div(K, 256))), dim3(256), 0, s>>>(part_b, static_cast<int>(l.cb.S), K,
-                                                                                          col_exp);
+                                                                                          col_exp, nullptr);
   if (M > 0) {
     const int64_t ga = std::max<int64_t>(1, std::min<int64_t>(ceil_div(M * N / 4, 256), 8192));
     const int64_t gb = std::max<int64_t>(1, std::min<int64_t>(ceil_div(M * K / 4, 256), 8192));

@@ -403,25 +403,26 @@ int moe_cast_f32_to_bf16(const float *src, int64_t n, moe_bf16_t *dst, void *str
  *  kernel_cases/case31_ref_musa_asm_tf32_ssgemm_tn_128x256.py:61-68): both fp32
  * operands rounded to tf32 (round_tf32_rne, :51-58), products accumulated in
  * fp32, fp32 out.
- *   dgrad: grad_input [M, N] = tf32(grad_output [M, K]) @ tf32(weight [K, N]),
- *     on the bf16 matrix cores: each tf32 value t is split into bf16
- *     hi = RNE(t) and lo = t - hi (exact) and a b is taken as
- *     hi_a hi_b + hi_a lo_b + lo_a hi_b (the dropped lo_a lo_b is below
- *     2^-16 |a b|); every partial product is exact in the fp32 accumulator.
- *   wgrad: grad_weight [N, K] = tf32(grad_output [M, N])^T @ tf32(inp [M, K]),
- *     on the fp16 matrix cores: a tf32 value has fp16's 11 significant bits;
- *     each operand column is scaled by the power of two that brings its
- *     largest magnitude into [2^14, 2^15), so its values are fp16 values
- *     (exactly, unless 2^29 or more below that largest one: then within
- *     2^-38 of it), the products are exact in fp32, and the sums are scaled
- *     back exactly (a column whose largest magnitude is 0, Inf or NaN keeps
- *     scale 1).
+ *   Both run on the fp16 matrix cores: a tf32 value has fp16's 11 significant
+ *     bits; each operand row or column along which the sum runs is scaled by
+ *     the power of two that brings its largest magnitude into [2^14, 2^15),
+ *     so its values are fp16 values (exactly, unless 2^29 or more below that
+ *     largest one: then within 2^-38 of it), the products are exact in fp32,
+ *     and the sums are scaled back exactly (unless the result is an fp32
+ *     subnormal); a row or column whose largest magnitude is 0, Inf or NaN
+ *     keeps scale 1, one below 2^-112 takes 2^127.
+ *   dgrad: grad_input [M, N] = tf32(grad_output [M, K]) @ tf32(weight [K, N]):
+ *     grad_output scaled per row, weight per column, the scales undone in the
+ *     GEMM's epilogue.
+ *   wgrad: grad_weight [N, K] = tf32(grad_output [M, N])^T @ tf32(inp [M, K]):
+ *     both scaled per column, undone where the reduction planes are added.
  * Limits: the column counts (K and N) % 8 == 0; dgrad 3K, N < 2^22 and
  *   3K*N < 2^30; wgrad M*N, M*K, N*K < 2^30; 16-byte aligned tensors.
- * Workspace: the *_workspace_size bytes, 256-byte aligned (dgrad: the bf16
- *   hi/lo planes, 3 M K + 3 K N bf16 values; wgrad: the fp16 copies,
- *   M N + M K values, the column exponents, column-max slabs and the fp32
- *   planes of the reduction chunks, at least one). */
+ * Workspace: the *_workspace_size bytes, 256-byte aligned (dgrad: the fp16
+ *   copies, M K + K N values, the row and column exponents and the
+ *   column-max slabs; wgrad: the fp16 copies, M N + M K values, the column
+ *   exponents, column-max slabs and the fp32 planes of the reduction chunks,
+ *   at least one). */
 size_t moe_router_dgrad_tf32_workspace_size(int64_t M, int64_t K, int64_t N);
 int moe_router_dgrad_tf32(const float *grad_output, int64_t M, int64_t K, const float *weight, int64_t N,
                           float *grad_input, void *workspace, size_t workspace_bytes, void *stream);

@@ -1,9 +1,9 @@
 """GPU parity of the tf32 router backward GEMMs (case39 dgrad, case31 wgrad).
 
 The golden (reference_tf32, case39...:61-68 / case31...:61-68) multiplies tf32-rounded operands
-exactly and accumulates in fp32.  Here (dgrad) every tf32 product is three exact bf16 products (the
-dropped lo*lo term is below 2^-16 |a b|), or (wgrad) one exact product of fp16 values scaled by a
-power of two per column, accumulated in fp32 in another order, so the bound is
+exactly and accumulates in fp32.  Here every tf32 product is one exact product of fp16 values scaled
+by powers of two (dgrad: per grad_output row and per weight column; wgrad: per operand column),
+accumulated in fp32 in another order, so the bound is
 |ours - golden| <= 1e-4 * sum_k |a_k b_k| + 1e-5.  The cases' own checks against an explicit sum
 (case39: 1e-3, case31: 1e-2 absolute) are applied as written at full size; the full-size goldens
 are computed on the CPU.
@@ -24,7 +24,10 @@ def _bound_check(got, ref, absprod, what):
     assert bool((err <= bound).all()), f"{what}: worst err/bound {(err / bound).max().item():.3f}"
 
 
-@pytest.mark.parametrize("M,K,N", [(64, 64, 256), (5, 8, 8), (300, 320, 520), (1000, 64, 8192), (130, 1000, 264)])
+# Reductions of whole and partial 64-wide steps (K = 40, 1000), output columns past a 256-column tile, row
+# tiles with 1-127 valid rows.
+@pytest.mark.parametrize("M,K,N", [(64, 64, 256), (5, 8, 8), (300, 320, 520), (1000, 64, 8192), (130, 1000, 264),
+                                   (700, 192, 1000), (129, 40, 72)])
 def test_router_dgrad_tf32_shapes(pkg, dev, M, K, N):
     g = torch.Generator().manual_seed(M + K + N)
     go = torch.randn(M, K, generator=g)
@@ -97,3 +100,27 @@ def test_router_wgrad_tf32_columns_of_any_scale(pkg, dev):
     for what, sel in (("row 3", rel[3]), ("row 5", rel[5]), ("column 7", rel[:, 7]), ("column 9", rel[:, 9]),
                       ("all", rel)):
         assert rel.numel() and bool((sel <= 1e-4).all()), f"{what}: worst relative error {sel.max().item():.3e}"
+
+
+def test_router_dgrad_tf32_rows_and_columns_of_any_scale(pkg, dev):
+    # grad_output's rows and weight's columns are each scaled by their own power of two into the fp16 range:
+    # rows near 1e-30, 1e-25 and 1e18, columns near 1e-20 and 1e15 keep the relative accuracy of the others.
+    # Reference: the float64 sum of the tf32-rounded operands' products; outputs in fp32's subnormal range
+    # (row 600 x column 7, ~1e-44) are held to an absolute 2^-126, fp32's smallest normal.
+    M, K, N = 700, 320, 520
+    g = torch.Generator().manual_seed(78)
+    go = torch.randn(M, K, generator=g)
+    w = torch.randn(K, N, generator=g)
+    go[3] *= 1e-30
+    go[5] *= 1e18
+    go[600] *= 1e-25
+    w[:, 7] *= 1e-20
+    w[:, 9] *= 1e15
+    got = pkg.ops.router_dgrad_tf32(go.to(dev), w.to(dev)).cpu().double()
+    a, b = ref_torch.round_tf32_rne(go).double(), ref_torch.round_tf32_rne(w).double()
+    ref = a @ b
+    excess = (got - ref).abs() - (1e-4 * (a.abs() @ b.abs()) + 2.0 ** -126)
+    assert bool(torch.isfinite(got).all())
+    for what, sel in (("row 3", excess[3]), ("row 5", excess[5]), ("row 600", excess[600]),
+                      ("column 7", excess[:, 7]), ("column 9", excess[:, 9]), ("all", excess)):
+        assert bool((sel <= 0).all()), f"{what}: error above the bound by {sel.max().item():.3e}"
