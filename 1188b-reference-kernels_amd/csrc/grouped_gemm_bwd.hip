@@ -1915,8 +1915,14 @@ void launch_split(const SplitArgs &a, hipStream_t s) {
 // subnormal: an error below 2^-38 of the column's largest magnitude). The
 // product of two fp16 values is exact in fp32, so one fp16 MFMA replaces the
 // three bf16 products of the hi/lo split, and the fp32 sums are scaled back by
-// 2^-(e_row + e_col) (exact) when the reduction planes are added. A column
-// whose largest magnitude is 0, Inf or NaN keeps scale 1.
+// 2^-(e_row + e_col) (exact) when the reduction planes are added. The scale
+// comes from the largest finite magnitude (Inf and NaN entries stay Inf and
+// NaN when scaled, so every finite value still converts exactly); a column
+// with no finite nonzero value keeps scale 1.
+__device__ __forceinline__ float finite_abs(float x) {
+  const float a = fabsf(x);
+  return a < __builtin_huge_valf() ? a : 0.f;  // Inf and NaN -> 0
+}
 __device__ __forceinline__ int scale_exp(float mx) {
   if (!(mx > 0.f) || !(mx < __builtin_huge_valf())) return 0;
   int e = 0;
@@ -1924,7 +1930,7 @@ __device__ __forceinline__ int scale_exp(float mx) {
   return 15 - e;                   // mx 2^(15 - e) in [2^14, 2^15)
 }
 
-// Largest magnitude per column over a slab of rows: block (x, y) covers cg
+// Largest finite magnitude per column over a slab of rows: block (x, y) covers cg
 // groups of 4 columns from x 4 cg and rows y rps .. + rps - 1, its threads
 // split over the groups (t % cg) and 256 / cg interleaved row phases (t / cg,
 // combined in LDS), 8 independent rows per round; part[y][c].
@@ -1946,10 +1952,10 @@ __global__ __launch_bounds__(256) void colmax_partial_kernel(const float *src, i
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        m0 = fmaxf(m0, fabsf(__uint_as_float(v[u].x)));
-        m1 = fmaxf(m1, fabsf(__uint_as_float(v[u].y)));
-        m2 = fmaxf(m2, fabsf(__uint_as_float(v[u].z)));
-        m3 = fmaxf(m3, fabsf(__uint_as_float(v[u].w)));
+        m0 = fmaxf(m0, finite_abs(__uint_as_float(v[u].x)));
+        m1 = fmaxf(m1, finite_abs(__uint_as_float(v[u].y)));
+        m2 = fmaxf(m2, finite_abs(__uint_as_float(v[u].z)));
+        m3 = fmaxf(m3, finite_abs(__uint_as_float(v[u].w)));
       }
     }
   }
@@ -1994,7 +2000,7 @@ __global__ __launch_bounds__(256) void colmax_final_kernel(const float *part, in
 }
 
 // Row-scaled fp16 copy for the tf32 router dgrad: one wavefront per row r of src [R, C] (C % 4 == 0):
-// e = scale_exp(largest magnitude of the row), at most 127; dst[r][c] = fp16(tf32(src[r][c]) 2^e) (RNE) and
+// e = scale_exp(largest finite magnitude of the row), at most 127; dst[r][c] = fp16(tf32(src[r][c]) 2^e) (RNE) and
 // exp8 at the row's permuted position (128 b + 4 (r % 32) + (r % 128) / 32 for r = 128 b + (r % 128)).
 // Rows R .. R8 - 1 (R8 = R rounded up to 128) only get exponent 0.
 __global__ __launch_bounds__(256) void tf32_to_f16_rows_kernel(const float *src, int64_t R, int64_t R8, int64_t C,
@@ -2008,8 +2014,8 @@ __global__ __launch_bounds__(256) void tf32_to_f16_rows_kernel(const float *src,
   if (r < R) {
     for (int64_t i = lane; i < q; i += kWave) {
       const u32x4 v = row[i];
-      m = fmaxf(m, fmaxf(fmaxf(fabsf(__uint_as_float(v.x)), fabsf(__uint_as_float(v.y))),
-                         fmaxf(fabsf(__uint_as_float(v.z)), fabsf(__uint_as_float(v.w)))));
+      m = fmaxf(m, fmaxf(fmaxf(finite_abs(__uint_as_float(v.x)), finite_abs(__uint_as_float(v.y))),
+                         fmaxf(finite_abs(__uint_as_float(v.z)), finite_abs(__uint_as_float(v.w)))));
     }
   }
 #pragma unroll

@@ -409,8 +409,9 @@ int moe_cast_f32_to_bf16(const float *src, int64_t n, moe_bf16_t *dst, void *str
  *     so its values are fp16 values (exactly, unless 2^29 or more below that
  *     largest one: then within 2^-38 of it), the products are exact in fp32,
  *     and the sums are scaled back exactly (unless the result is an fp32
- *     subnormal); a row or column whose largest magnitude is 0, Inf or NaN
- *     keeps scale 1, one below 2^-112 takes 2^127.
+ *     subnormal); the scale comes from the largest finite magnitude (Inf and
+ *     NaN entries stay Inf and NaN), a row or column with no finite nonzero
+ *     value keeps scale 1, one whose largest is below 2^-112 takes 2^127.
  *   dgrad: grad_input [M, N] = tf32(grad_output [M, K]) @ tf32(weight [K, N]):
  *     grad_output scaled per row, weight per column, the scales undone in the
  *     GEMM's epilogue.

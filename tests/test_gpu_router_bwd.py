@@ -124,3 +124,40 @@ def test_router_dgrad_tf32_rows_and_columns_of_any_scale(pkg, dev):
     for what, sel in (("row 3", excess[3]), ("row 5", excess[5]), ("row 600", excess[600]),
                       ("column 7", excess[:, 7]), ("column 9", excess[:, 9]), ("all", excess)):
         assert bool((sel <= 0).all()), f"{what}: error above the bound by {sel.max().item():.3e}"
+
+
+@pytest.mark.parametrize("which", ["dgrad", "wgrad"])
+def test_router_tf32_inf_and_nan_entries(pkg, dev, which):
+    # A row / column holding Inf (or NaN) and finite values above fp16's range: the scale comes from the largest
+    # finite magnitude, so the finite values convert exactly and the Inf / NaN entries stay Inf / NaN; the
+    # outputs match torch's fp32 product of the tf32-rounded operands in their Inf (with sign) and NaN
+    # positions, and the finite ones within the bound.
+    g = torch.Generator().manual_seed(91)
+    if which == "dgrad":
+        M, K, N = 300, 320, 264
+        a = torch.randn(M, K, generator=g)
+        b = torch.randn(K, N, generator=g)
+        a[10, 0], a[10, 1], a[10, 2] = float("inf"), 1e6, -3e5  # one grad_output row: Inf and large finite values
+        a[11, 5] = float("nan")
+        b[3, 20], b[4, 20] = float("-inf"), 2e5                 # one weight column
+        got = pkg.ops.router_dgrad_tf32(a.to(dev), b.to(dev)).cpu()
+        ra, rb = ref_torch.round_tf32_rne(a), ref_torch.round_tf32_rne(b)
+        ref = ref_torch.router_dgrad_tf32(a, b)
+        absprod = ra.abs() @ rb.abs()
+    else:
+        M, N, K = 1000, 64, 520
+        a = torch.randn(M, N, generator=g)
+        b = torch.randn(M, K, generator=g)
+        a[0, 6], a[1, 6], a[2, 6] = float("inf"), 1e6, -3e5     # one grad_output column
+        a[7, 8] = float("nan")
+        b[3, 30], b[4, 30] = float("-inf"), 2e5                 # one inp column
+        got = pkg.ops.router_wgrad_tf32(a.to(dev), b.to(dev)).cpu()
+        ra, rb = ref_torch.round_tf32_rne(a), ref_torch.round_tf32_rne(b)
+        ref = ref_torch.router_wgrad_tf32(a, b)
+        absprod = ra.abs().t() @ rb.abs()
+    assert torch.equal(torch.isnan(got), torch.isnan(ref))
+    assert torch.equal(torch.isposinf(got), torch.isposinf(ref)) and torch.equal(torch.isneginf(got), torch.isneginf(ref))
+    fin = torch.isfinite(ref)
+    assert int((~fin).sum()) > 0 and int(fin.sum()) > 0
+    err = (got[fin].double() - ref[fin].double()).abs()
+    assert bool((err <= 1e-4 * absprod[fin].double() + 1e-5).all())
