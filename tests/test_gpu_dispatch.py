@@ -215,6 +215,15 @@ def test_map_extent_matches_torch(pkg, dev, dtype):
     em = pkg.cases.case21_permute_with_mask_map_trans.make_row_id_map(device=dev).to(dtype)
     assert pkg.ops.map_extent(em) == _extent_ref(em)
     assert pkg.ops.map_extent(em)[2], "a row-id map names every row once"
+    # Large maps: several rounds of the partial pass's four loads per thread over 2048 blocks (a partial last
+    # round and a scalar tail), and a permutation whose 2^23 + 5 row marks the final pass counts in many rounds.
+    big = torch.randint(-1, 1 << 20, (2 ** 24 + 3,), generator=g).to(dtype).to(dev)
+    assert pkg.ops.map_extent(big) == _extent_ref(big)
+    perm = torch.randperm(2 ** 23 + 5, generator=g).to(dtype).to(dev)
+    assert pkg.ops.map_extent(perm) == (2 ** 23 + 4, 2 ** 23 + 5, True)
+    perm[77] = perm[78]  # one row named twice, one never
+    got = pkg.ops.map_extent(perm)
+    assert got == _extent_ref(perm) and not got[2]
 
 
 def _extent_ref(m: torch.Tensor) -> tuple[int, int, bool]:
