@@ -125,18 +125,21 @@ __device__ __forceinline__ v4bf16 read_tr(lds_v4bf16 *__restrict__ p) {
 #endif
 }
 
-// Fragment of an RM operand: 8 consecutive reduction values of one column per
-// lane, from two transposing LDS reads 4 rows apart.
-__device__ __forceinline__ bf16x8 read_rm_frag(uint32_t addr) {
+// Fragment of an RM operand whose LDS rows are kRow bytes apart: 8 consecutive
+// reduction values of one column per lane, from two transposing reads 4 rows apart.
+template <int kRow>
+__device__ __forceinline__ bf16x8 read_rm_frag_rows(uint32_t addr) {
 #if defined(__HIP_DEVICE_COMPILE__)
   const v4bf16 lo = read_tr((lds_v4bf16 *)(uintptr_t)addr);
-  const v4bf16 hi = read_tr((lds_v4bf16 *)(uintptr_t)(addr + 4 * kRMRow));
+  const v4bf16 hi = read_tr((lds_v4bf16 *)(uintptr_t)(addr + 4 * kRow));
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 #else
   (void)addr;
   return bf16x8{};
 #endif
 }
+// The same with 256-column tiles (kRMRow-byte rows).
+__device__ __forceinline__ bf16x8 read_rm_frag(uint32_t addr) { return read_rm_frag_rows<kRMRow>(addr); }
 
 // One 16 x 16 x 32 MFMA on 16-bit operands: bf16, or fp16 (kF16: the tf32 router GEMMs' scaled operands,
 // the same bit layout in LDS and registers).
@@ -165,17 +168,24 @@ __device__ __forceinline__ f32x4_t mma16(bf16x8 a, bf16x8 b, f32x4_t c) {
 // kF16 (the tf32 router dgrad, fp32 output, rows [0, M) as one group): fp16
 // operands scaled by powers of two per dy row and per dx column
 // (p.row_exp8, p.col_exp8), undone in the epilogue.
-template <int kOut, bool kNtB = false, bool kF16 = false>
-__global__ __launch_bounds__(256) void grouped_gemm_dgrad128_kernel(BwdArgs p) {
+// kTN, kStagesT: columns per tile (256, or 128: 256-byte RM rows) and ring
+// stages; with 128 columns and 2 stages (64 KiB of LDS, 64 accumulators per
+// lane) two workgroups share a CU, so one's stores drain under the other's
+// MFMAs.
+template <int kOut, bool kNtB = false, bool kF16 = false, int kTN = 256, int kStagesT = 3>
+__global__ __launch_bounds__(256, kTN == 128 ? 2 : 1) void grouped_gemm_dgrad128_kernel(BwdArgs p) {
   static_assert(!kF16 || kOut == 1, "fp16 operands: the tf32 router dgrad (fp32 output)");
-  constexpr int kBM = 128, kWavesM = 1, kStages = 3;
+  static_assert(kTN == 256 || kTN == 128, "256 or 128 columns per tile");
+  constexpr int kBM = 128, kWavesM = 1, kStages = kStagesT;
   constexpr int kWaves = 4;
   constexpr int kWavesN = kWaves / kWavesM;
   constexpr int kWaveRows = kBM / kWavesM;
-  constexpr int kWaveCols = kBN / kWavesN;
+  constexpr int kWaveCols = kTN / kWavesN;
   constexpr int kMI = kWaveRows / 32, kNI = kWaveCols / 32;
   constexpr int kABytes = kBM * kBK * 2;
-  constexpr int kBBytes = kBN * kBK * 2;
+  constexpr int kBBytes = kTN * kBK * 2;
+  constexpr int kRow = kTN * 2;                  // bytes per RM row of the B tile
+  constexpr int kRowsPerBlk = 1024 / kRow;       // RM rows per 1 KiB DMA block
   constexpr int kStageBytes = kABytes + kBBytes;
   constexpr int kDmaA = kABytes / 1024 / kWaves, kDmaB = kBBytes / 1024 / kWaves;
   // Next tile's stages issued after the stores (fp32 output; the fp16 form issues them before, as the bf16
@@ -259,7 +269,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_dgrad128_kernel(BwdArgs p) {
   int a_step = 0, b_step = 0;  // bytes per reduction step
   auto setup_dma = [&](const Tile &t) {
     // RM operand lane map: DMA block blk holds reduction rows 2 blk, 2 blk + 1.
-    const int rm_krow = lane >> 5, rm_pchunk = lane & 31;
+    const int rm_krow = lane / (64 / kRowsPerBlk), rm_pchunk = lane & (kRow / 16 - 1);
     {
       const int rows_valid = static_cast<int>(min(t.hi - t.i0, int64_t(kBM)));
       ra = make_rsrc(p.a + t.i0 * N, static_cast<uint32_t>(rows_valid) * static_cast<uint32_t>(N) * 2u);
@@ -277,10 +287,10 @@ __global__ __launch_bounds__(256) void grouped_gemm_dgrad128_kernel(BwdArgs p) {
       }
     }
     b_step = kBK * static_cast<int>(K) * 2;
-    const uint32_t col0 = t.nt * static_cast<uint32_t>(kBN);
+    const uint32_t col0 = t.nt * static_cast<uint32_t>(kTN);
 #pragma unroll
     for (int j = 0; j < kDmaB; ++j) {
-      const int krow = (j * kWaves + wave) * 2 + rm_krow;
+      const int krow = (j * kWaves + wave) * kRowsPerBlk + rm_krow;
       const int lchunk = rm_pchunk ^ rm_swz(krow);
       b_off[j] = static_cast<int>(static_cast<uint32_t>(krow) * static_cast<uint32_t>(K) * 2u + col0 * 2u + lchunk * 16);
     }
@@ -311,7 +321,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_dgrad128_kernel(BwdArgs p) {
   // RM: lane 16 G + 4 j + q reads row (G / 2) * 8 + j (+ 4 for the second
   // read), bytes ((G & 1) * 16 + 4 q) * 2 of the 32-column block, swizzled.
   const int rm_g = lane >> 4, rm_j = (lane >> 2) & 3, rm_q = lane & 3;
-  const int rm_lane = ((rm_g >> 1) * 8 + rm_j) * kRMRow + (((rm_g & 1) * 2 + (rm_q >> 1)) << 4) + (rm_q & 1) * 8;
+  const int rm_lane = ((rm_g >> 1) * 8 + rm_j) * kRow + (((rm_g & 1) * 2 + (rm_q >> 1)) << 4) + (rm_q & 1) * 8;
   auto rm_base = [&](int c0) { return rm_lane + ((c0 * 2) ^ (rm_j << 6)); };
   const int khalf = lane >> 5;
   int fa_base[kMI], fb_base[kNI];
@@ -337,7 +347,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_dgrad128_kernel(BwdArgs p) {
 #pragma unroll
     for (int i = 0; i < kMI; ++i) fa[ks][i] = *reinterpret_cast<const lds_bf16x8 *>((uintptr_t)(rd_a[i] ^ (ks << 5)));
 #pragma unroll
-    for (int j = 0; j < kNI; ++j) fb[ks][j] = read_rm_frag(rd_b[j] + ks * 16 * kRMRow);
+    for (int j = 0; j < kNI; ++j) fb[ks][j] = read_rm_frag_rows<kRow>(rd_b[j] + ks * 16 * kRow);
   };
   auto mfma_ks = [&](int ks) {
 #pragma unroll
@@ -362,7 +372,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_dgrad128_kernel(BwdArgs p) {
       const bool rows_in = t.hi > wrow0;
       const __amdgpu_buffer_rsrc_t rr = make_rsrc(p.row_exp8 + (rows_in ? wrow0 : 0), rows_in ? 128u : 0u);
       const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.col_exp8, static_cast<uint32_t>(K));
-      const int64_t tcol0 = static_cast<int64_t>(t.nt) * kBN + wn * kWaveCols + (lane >> 5) * 4;
+      const int64_t tcol0 = static_cast<int64_t>(t.nt) * kTN + wn * kWaveCols + (lane >> 5) * 4;
 #if defined(__HIP_DEVICE_COMPILE__)
       ex_row = __builtin_amdgcn_raw_buffer_load_b32(rr, (lane & 31) * 4, 0, 0);
 #pragma unroll
@@ -494,7 +504,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_dgrad128_kernel(BwdArgs p) {
       const uint32_t ld = static_cast<uint32_t>(K) * 4u;
       const __amdgpu_buffer_rsrc_t ro =
           make_rsrc(obase + (rows_out > 0 ? wrow0 * K : 0), static_cast<uint32_t>(rows_out) * ld);
-      const int64_t tcol0 = static_cast<int64_t>(cur.nt) * kBN + wn * kWaveCols;
+      const int64_t tcol0 = static_cast<int64_t>(cur.nt) * kTN + wn * kWaveCols;
       const int half = lane >> 5;
 #pragma unroll
       for (int i = 0; i < kMI; ++i) {
@@ -531,7 +541,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_dgrad128_kernel(BwdArgs p) {
       const uint32_t ld = static_cast<uint32_t>(K) * 2u;
       const __amdgpu_buffer_rsrc_t ro =
           make_rsrc(obase + (rows_out > 0 ? wrow0 * K : 0), static_cast<uint32_t>(rows_out) * ld);
-      const int64_t tcol0 = static_cast<int64_t>(cur.nt) * kBN + wn * kWaveCols;
+      const int64_t tcol0 = static_cast<int64_t>(cur.nt) * kTN + wn * kWaveCols;
       const int half = lane >> 5;
 #pragma unroll
       for (int i = 0; i < kMI; ++i) {
@@ -1066,20 +1076,6 @@ __global__ __launch_bounds__(256) void grouped_gemm_bwd_pipe_kernel(BwdArgs p) {
     more = find_tile(round + 2, nxt);
   }
   wait_dma();  // no LDS DMA outlives the workgroup
-}
-
-// Fragment of an RM operand whose LDS rows are kRow bytes apart: 8 consecutive
-// reduction values of one column per lane, from two transposing reads 4 rows apart.
-template <int kRow>
-__device__ __forceinline__ bf16x8 read_rm_frag_rows(uint32_t addr) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  const v4bf16 lo = read_tr((lds_v4bf16 *)(uintptr_t)addr);
-  const v4bf16 hi = read_tr((lds_v4bf16 *)(uintptr_t)(addr + 4 * kRow));
-  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-#else
-  (void)addr;
-  return bf16x8{};
-#endif
 }
 
 // Ping-pong backward kernel (bf16 output; dgrad with N % 64 == 0 and N >= 192,
@@ -1788,6 +1784,10 @@ void launch_pipe(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
 #ifndef MOE_ROUTER_DGRAD_F16
 #define MOE_ROUTER_DGRAD_F16 1
 #endif
+// Its GEMM's column tiles: 128 (two workgroups per CU) or 256.
+#ifndef MOE_ROUTER_DGRAD_TN
+#define MOE_ROUTER_DGRAD_TN 128
+#endif
 template <bool kWgrad, bool kOrder = false, bool kTails = false>
 void launch_pp(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
   int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
@@ -1843,11 +1843,12 @@ __global__ __launch_bounds__(1024) void group_order_kernel(const int32_t *offset
   }
 }
 
-template <int kOut = 0, bool kNtB = false, bool kF16 = false>
+template <int kOut = 0, bool kNtB = false, bool kF16 = false, int kTN = 256, int kStagesT = 3>
 void launch_dgrad128(const BwdArgs &p, int64_t max_tiles, hipStream_t s) {
-  int64_t grid = std::min<int64_t>(num_cus(), max_tiles);
+  // one workgroup per CU, two with 128-column tiles
+  int64_t grid = std::min<int64_t>((kTN == 128 ? 2 : 1) * num_cus(), max_tiles);
   grid = std::max<int64_t>(8, (grid + 7) / 8 * 8);
-  grouped_gemm_dgrad128_kernel<kOut, kNtB, kF16><<<dim3(grid), dim3(256), 0, s>>>(p);
+  grouped_gemm_dgrad128_kernel<kOut, kNtB, kF16, kTN, kStagesT><<<dim3(grid), dim3(256), 0, s>>>(p);
 }
 
 // ---- tf32 GEMMs of the router backward on the bf16 matrix cores ---------
@@ -2455,7 +2456,8 @@ int moe_router_dgrad_tf32(const float *grad_output, int64_t M, int64_t K, const 
     p.N = K;
     p.K = N;
     p.G = 1;
-    p.ntiles = ceil_div(N, kBN);
+    constexpr int kTN = MOE_ROUTER_DGRAD_TN;
+    p.ntiles = ceil_div(N, kTN);
     p.chunk = M;
     p.kchunk = 0;
     p.order = nullptr;
@@ -2463,7 +2465,7 @@ int moe_router_dgrad_tf32(const float *grad_output, int64_t M, int64_t K, const 
     p.tails = nullptr;
     p.row_exp8 = row_e8;
     p.col_exp8 = col_e8;
-    launch_dgrad128<1, false, true>(p, (ceil_div(M, 128) + 1) * p.ntiles, s);
+    launch_dgrad128<1, false, true, kTN, kTN == 128 ? 2 : 3>(p, (ceil_div(M, 128) + 1) * p.ntiles, s);
     return check_launch(fn);
   }
   // A' = [A_hi | A_hi | A_lo] [M, 3K] and B' = [B_hi; B_lo; B_hi] [3K, N]:
