@@ -4,7 +4,7 @@ The one-wavefront-per-SIMD GEMM kernels hold 128 or 256 fp32 accumulators in AGP
 step of operand fragments in VGPRs; the ping-pong kernels (forward and backward, two
 wavefronts per SIMD) hold their 128 accumulators and fragments in the 256 registers a
 wavefront gets at that occupancy, and so do the short-group kernels (wgrad sweep, 128-row
-forward tiles) with their smaller tiles. A spill puts scratch loads (which wait on the vector-memory counter, and so on
+forward tiles) and the tf32 router dgrad's 128 x 128 tiles with their smaller tiles. A spill puts scratch loads (which wait on the vector-memory counter, and so on
 the LDS DMA in flight) inside the MFMA stream. The compiler's kernel-resource-usage remarks
 for the device code must report 0 scratch bytes per lane for every instantiation.
 """
@@ -45,6 +45,9 @@ def test_gemm_kernels_do_not_spill():
     # the short-group forward kernel (128-row tiles of 128, 160 and 192 columns, loading wavefronts): the same
     fwd128 = [(name, v) for name, v in rows if "_fwd128_kernel" in name]
     assert len(fwd128) == 3 and all(v.get("occ") == 2 and v.get("vgpr", 0) + v.get("agpr", 0) <= 256 for _, v in fwd128), fwd128
+    # the tf32 router dgrad's 128 x 128 tiles: two workgroups per CU, its 64 accumulators in VGPRs
+    dg128 = [(name, v) for name, v in rows if "dgrad128_kernel" in name and "ELi128ELi2E" in name]
+    assert len(dg128) == 1 and all(v.get("occ") == 2 and v.get("vgpr", 0) + v.get("agpr", 0) <= 256 for _, v in dg128), dg128
     assert all(v.get("agpr") in (128, 256) for name, v in rows if "gemm" in name and "kernel" in name and "sum_planes" not in name
                and "split" not in name and "tails_init" not in name and "_pp_kernel" not in name
-               and "_sweep_kernel" not in name and "_fwd128_kernel" not in name)
+               and "_sweep_kernel" not in name and "_fwd128_kernel" not in name and (name, v) not in dg128)
