@@ -2000,24 +2000,34 @@ __global__ __launch_bounds__(256) void colmax_final_kernel(const float *part, in
   }
 }
 
-// Row-scaled fp16 copy for the tf32 router dgrad: one wavefront per row r of src [R, C] (C % 4 == 0):
+// Row-scaled fp16 copy for the tf32 router dgrad: one wavefront per row r of src [R, C] (C % 4 == 0), the row's
+// first 1024 values read once and kept in registers for the conversion:
 // e = scale_exp(largest finite magnitude of the row), at most 127; dst[r][c] = fp16(tf32(src[r][c]) 2^e) (RNE) and
 // exp8 at the row's permuted position (128 b + 4 (r % 32) + (r % 128) / 32 for r = 128 b + (r % 128)).
 // Rows R .. R8 - 1 (R8 = R rounded up to 128) only get exponent 0.
 __global__ __launch_bounds__(256) void tf32_to_f16_rows_kernel(const float *src, int64_t R, int64_t R8, int64_t C,
                                                                uint16_t *dst, int8_t *exp8) {
+  constexpr int kKeep = 4;  // 16-byte vectors per lane kept in registers between the two passes (rows of <= 1024)
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
   const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   if (r >= R8) return;
   const int64_t q = C / 4;
   const u32x4 *row = reinterpret_cast<const u32x4 *>(src + r * C);
+  auto vmax = [](float m, const u32x4 &v) {
+    return fmaxf(m, fmaxf(fmaxf(finite_abs(__uint_as_float(v.x)), finite_abs(__uint_as_float(v.y))),
+                          fmaxf(finite_abs(__uint_as_float(v.z)), finite_abs(__uint_as_float(v.w)))));
+  };
   float m = 0.f;
+  u32x4 keep[kKeep];
+#pragma unroll
+  for (int u = 0; u < kKeep; ++u) {
+    const int64_t i = lane + u * kWave;
+    keep[u] = (r < R && i < q) ? __builtin_nontemporal_load(row + i) : u32x4{0u, 0u, 0u, 0u};
+    m = vmax(m, keep[u]);
+  }
   if (r < R) {
-    for (int64_t i = lane; i < q; i += kWave) {
-      const u32x4 v = row[i];
-      m = fmaxf(m, fmaxf(fmaxf(finite_abs(__uint_as_float(v.x)), finite_abs(__uint_as_float(v.y))),
-                         fmaxf(finite_abs(__uint_as_float(v.z)), finite_abs(__uint_as_float(v.w)))));
-    }
+    for (int64_t i = lane + kKeep * kWave; i < q; i += kWave) m = vmax(m, row[i]);
   }
 #pragma unroll
   for (int off = kWave / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
@@ -2027,9 +2037,7 @@ __global__ __launch_bounds__(256) void tf32_to_f16_rows_kernel(const float *src,
     exp8[r - w + (w % 32) * 4 + w / 32] = static_cast<int8_t>(e);
   }
   if (r >= R) return;
-  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-  for (int64_t i = lane; i < q; i += kWave) {
-    const u32x4 v = __builtin_nontemporal_load(row + i);
+  auto convert = [&](int64_t i, const u32x4 &v) {
     const uint32_t in[4] = {v.x, v.y, v.z, v.w};
     uint32_t h[4];
 #pragma unroll
@@ -2038,7 +2046,13 @@ __global__ __launch_bounds__(256) void tf32_to_f16_rows_kernel(const float *src,
       h[k] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(t));
     }
     *reinterpret_cast<u32x2 *>(dst + r * C + i * 4) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+  };
+#pragma unroll
+  for (int u = 0; u < kKeep; ++u) {
+    const int64_t i = lane + u * kWave;
+    if (i < q) convert(i, keep[u]);
   }
+  for (int64_t i = lane + kKeep * kWave; i < q; i += kWave) convert(i, row[i]);
 }
 
 // dst[r][c] = fp16(tf32(src[r][c]) 2^exp[c]) (RNE; C % 4 == 0).

@@ -24,10 +24,10 @@ def _bound_check(got, ref, absprod, what):
     assert bool((err <= bound).all()), f"{what}: worst err/bound {(err / bound).max().item():.3f}"
 
 
-# Reductions of whole and partial 64-wide steps (K = 40, 1000), output columns past a 256-column tile, row
-# tiles with 1-127 valid rows.
+# Reductions of whole and partial 64-wide steps (K = 40, 1000, 1200), output columns past a column tile, row
+# tiles with 1-127 valid rows, grad_output rows longer than the 1024 values the row conversion keeps in registers.
 @pytest.mark.parametrize("M,K,N", [(64, 64, 256), (5, 8, 8), (300, 320, 520), (1000, 64, 8192), (130, 1000, 264),
-                                   (700, 192, 1000), (129, 40, 72)])
+                                   (700, 192, 1000), (129, 40, 72), (300, 1200, 136)])
 def test_router_dgrad_tf32_shapes(pkg, dev, M, K, N):
     g = torch.Generator().manual_seed(M + K + N)
     go = torch.randn(M, K, generator=g)
