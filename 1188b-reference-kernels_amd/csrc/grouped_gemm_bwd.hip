@@ -2115,8 +2115,12 @@ struct ColmaxPlan {
 ColmaxPlan colmax_plan(int64_t R, int64_t C) {
   const int64_t S = std::max<int64_t>(1, std::min<int64_t>(64, ceil_div(R, 64)));
   const int64_t rps = std::max<int64_t>(1, ceil_div(R, S));
-  const int cg = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(256, ceil_div(C, 4))));
-  return {ceil_div(std::max<int64_t>(R, 1), rps), rps, cg, std::max<int64_t>(1, ceil_div(ceil_div(C, 4), cg))};
+  int cg = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(256, ceil_div(C, 4))));
+  const int64_t slabs = ceil_div(std::max<int64_t>(R, 1), rps);
+  // At least 512 workgroups where the shape allows: fewer column groups per block, more row phases
+  // (case39's weight, 320 rows: 40 -> 640 workgroups).
+  while (cg > 1 && ceil_div(ceil_div(C, 4), cg) * slabs < 512) cg >>= 1;
+  return {slabs, rps, cg, std::max<int64_t>(1, ceil_div(ceil_div(C, 4), cg))};
 }
 
 
