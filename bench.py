@@ -345,7 +345,8 @@ def backward_gemms(pkg, x, row_map, offs, h, w1, w2, dev, library=False):
 def router_section(pkg, x, dev):
     """The router front end and its backward (not part of the timed step): the c5 router GEMM on this
     batch's x with a random [E, H] gate, alone and with the top-k, and the reference router cases at
-    their own shapes (case38 logits, case39/case31 tf32 dgrad/wgrad, case11/case25 casts)."""
+    their own shapes (case38 logits, case39/case31 tf32 dgrad/wgrad, case11/case25 casts; 5 warm-up + 20 timed
+    calls each, as these take well under a millisecond)."""
     ops, inp = pkg.ops, pkg.inputs
     T, H = x.shape
     E, k = CFG["experts"], CFG["topk"]
@@ -359,27 +360,27 @@ def router_section(pkg, x, dev):
     cases = {}
     c = pkg.cases.case38_ref_musa_asm_bf16_ssgemm_nt_320x256
     a, b = c.make_inputs(seed=0, device=dev)
-    ms = _time_ms(lambda: c.kernel_function(a, b))
+    ms = _time_ms(lambda: c.kernel_function(a, b), reps=20, warm=5)
     cases["case38"] = {"ms": round(ms, 4), "TFLOP/s": round(2 * c.M * c.K * c.N / (ms * 1e-3) / 1e12, 2)}
     del a, b
     c = pkg.cases.case39_ref_musa_asm_tf32_ssgemm_nn_384x256
     a, b = c.make_inputs(seed=0, device=dev)
-    ms = _time_ms(lambda: c.kernel_function(a, b))
+    ms = _time_ms(lambda: c.kernel_function(a, b), reps=20, warm=5)
     cases["case39"] = {"ms": round(ms, 4), "tf32 TFLOP/s": round(2 * c.M * c.K * c.N / (ms * 1e-3) / 1e12, 2)}
     del a, b
     c = pkg.cases.case31_ref_musa_asm_tf32_ssgemm_tn_128x256
     a, b = c.make_inputs(seed=0, device=dev)
-    ms = _time_ms(lambda: c.kernel_function(a, b))
+    ms = _time_ms(lambda: c.kernel_function(a, b), reps=20, warm=5)
     cases["case31"] = {"ms": round(ms, 4), "tf32 TFLOP/s": round(2 * c.M * c.K * c.N / (ms * 1e-3) / 1e12, 2)}
     del a, b
     c = pkg.cases.case11_router_bwd_cast_bf16_to_fp32
     (a,) = c.get_inputs(dev)
-    ms = _time_ms(lambda: c.kernel_function(a))
+    ms = _time_ms(lambda: c.kernel_function(a), reps=20, warm=5)
     cases["case11"] = {"ms": round(ms, 4), "GB/s": round(a.numel() * 6 / (ms * 1e-3) / 1e9, 2)}
     del a
     c = pkg.cases.case25_ref_unary_cast_fp32_to_bf16
     a = c.make_inputs(seed=0, device=dev)
-    ms = _time_ms(lambda: c.kernel_function(a))
+    ms = _time_ms(lambda: c.kernel_function(a), reps=20, warm=5)
     cases["case25"] = {"ms": round(ms, 4), "GB/s": round(a.numel() * 6 / (ms * 1e-3) / 1e9, 2)}
     del a
     out["reference_cases"] = cases
